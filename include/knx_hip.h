@@ -1,0 +1,153 @@
+/* knx_hip.h — thin C ABI between the KERNIX host runtime (C) and the hand-written gfx950 kernels (HIP).
+ *
+ * Every function takes plain device pointers, sizes and a stream (a hipStream_t passed as void*, NULL = the null
+ * stream), enqueues its work and returns without synchronizing.  Return value: KNX_OK (0) or a negative KNX_E*
+ * code; the message of the last failure is available from knx_hip_last_error().  Arguments are checked on the host
+ * before any launch, so a bad shape is an error, never an out-of-bounds kernel.
+ *
+ * Fault injection for tests: if the environment variable KNX_HIP_FAIL names an entry point (e.g.
+ * "knx_hip_sgemm_ep") or is "all", that entry point returns KNX_EINJECT without touching the device.
+ *
+ * Reference interfaces replaced (reference paths, file:line):
+ *   knx_hip_quantize_rows   per-row int8 input quantization of kernix_qmatmul   include/kernix_model.h:112-142
+ *   knx_hip_i8gemm          int32 sdot accumulation + dequant/bias epilogue     include/kernix_model.h:143-178
+ *                           with the activation pass fused                      include/kernix_model.h:1854-1856
+ *   knx_hip_dequant         kernix_qweight_unpack into the fp32 copy            include/kernix_model.h:91-95, :1616-1622
+ *   knx_hip_sgemm_ep        kernix_matmul_ep_into (MPS+AMX row split)          src/kernix_metal.m:161-265,
+ *                           + kernix_bias_act epilogue                          include/kernix.h:951-977,
+ *                                                                               include/kernix_model.h:528-550
+ *   knx_hip_conv            kernix_conv_run (im2col → sgemm → bias_act)         include/kernix_model.h:711-771
+ *   knx_hip_layernorm       kernix_layer_norm_rows_into                         include/kernix.h:667-677
+ *   knx_hip_softmax         floats_softmax_into                                 include/kernix.h:652-657
+ *   knx_hip_bias_act        kernix_bias_act / ACT step                          include/kernix_model.h:528-541, :1866-1869
+ *   knx_hip_binary          kernix_binary_run                                   include/kernix_model.h:877-906
+ *   knx_hip_global_pool     kernix_global_pool_run                              include/kernix_model.h:810-830
+ *   knx_hip_attention_core  per-(b,h) QKᵀ·scale, mask, softmax, ·V             include/kernix_model.h:1021-1046
+ *   knx_hip_affine          AFFINE step                                         include/kernix_model.h:1882-1891
+ *   knx_hip_add_const       ADD_CONST step                                      include/kernix_model.h:1892-1896
+ *   knx_hip_pool            kernix_pooling_run                                  include/kernix_model.h:773-807
+ *   knx_hip_permute         kernix_permute_run                                  include/kernix_model.h:833-862
+ *   knx_hip_copy_cols       CONCAT (last axis) / SELECT (last axis)             include/kernix_model.h:908-949
+ *   knx_hip_pad             kernix_pad_run                                      include/kernix_model.h:951-968
+ *   knx_hip_upsample        kernix_upsample_run                                 include/kernix_model.h:970-984
+ *   knx_hip_embedding       kernix_embedding_run                                include/kernix_model.h:987-1000
+ *   knx_hip_rnn_gates       per-timestep gate update of kernix_rnn_dir          include/kernix_model.h:580-631
+ */
+#ifndef KNX_HIP_H
+#define KNX_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KNX_API __attribute__((visibility("default")))
+
+enum {
+    KNX_OK = 0,
+    KNX_EINVAL = -1,   /* bad argument (shape, pointer, enum) */
+    KNX_EHIP = -2,     /* HIP runtime error (allocation, launch, copy) */
+    KNX_ENODEV = -3,   /* no usable gfx950 device */
+    KNX_EINJECT = -4   /* failure injected through KNX_HIP_FAIL */
+};
+
+/* ---- runtime ---- */
+KNX_API int knx_hip_init(void);              /* selects device 0 once; KNX_ENODEV without a GPU */
+KNX_API const char* knx_hip_last_error(void);
+KNX_API int knx_hip_malloc(void** p, size_t bytes);
+KNX_API int knx_hip_free(void* p);
+KNX_API int knx_hip_host_malloc(void** p, size_t bytes); /* pinned host memory */
+KNX_API int knx_hip_host_free(void* p);
+KNX_API int knx_hip_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream);
+KNX_API int knx_hip_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream);
+KNX_API int knx_hip_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream);
+KNX_API int knx_hip_stream_create(void** stream);
+KNX_API int knx_hip_stream_destroy(void* stream);
+KNX_API int knx_hip_stream_sync(void* stream);
+
+/* ---- int8 path ---- */
+/* Per row r < rows of x (row stride ldx floats, k values): m = max|x|; a NaN or ±inf makes sx[r] = NaN (the whole
+ * output row becomes NaN); else sx = m > 0 ? m/127 : 1, inv = 1/sx, xq = clamp(rint(x·inv), −127, 127).
+ * xq rows have stride ldq bytes; columns [k, kp) are written as 0 (kp ≤ ldq, kp multiple of 64). */
+KNX_API int knx_hip_quantize_rows(const float* x, int ldx, int rows, int k, int kp, int8_t* xq, int ldq,
+                                  float* sx, void* stream);
+
+/* Y[m][n] = act( ((float)acc[m][n] · sa[m]) · sw[n] + bias[n] (+ Y[m][n] if accumulate) ), acc = Σ_k A[m][k]·W[n][k]
+ * in int32 (exact for K ≤ KERNIX_INT8_MAX_K).  A is M×K (stride lda bytes), W is N×K (stride ldw bytes), both int8 with
+ * K contiguous; K must be a multiple of 64 and lda/ldw multiples of 16 (pad with zeros).  bias may be NULL, act is a
+ * KERNIX_ACT_* id (−1 none).  Y (stride ldy floats) may be NULL; acc_out (stride ldacc int32) receives the raw int32
+ * accumulators when not NULL.  No FMA contraction: the products and the sum are rounded separately. */
+KNX_API int knx_hip_i8gemm(int M, int N, int K, const int8_t* A, int lda, const float* sa, const int8_t* W, int ldw,
+                           const float* sw, const float* bias, int act, float alpha, int accumulate, float* Y, int ldy,
+                           int32_t* acc_out, int ldacc, void* stream);
+
+/* dst (K×N row-major fp32) = (float)q[n][k] · scale[n]; q is N×K int8 with row stride ldq bytes. */
+KNX_API int knx_hip_dequant(const int8_t* q, int ldq, const float* scale, int K, int N, float* dst, void* stream);
+
+/* ---- fp32 GEMM ---- */
+/* C = act(A·W + bias): A M×K (stride lda), W K×N row-major (stride ldw), C M×N (stride ldc), all fp32.
+ * K may be 0 (then C = act(bias)). */
+KNX_API int knx_hip_sgemm_ep(int M, int N, int K, const float* A, int lda, const float* W, int ldw,
+                             const float* bias, int act, float alpha, float* C, int ldc, void* stream);
+
+/* ---- convolution (NHWC, groups, dilation, zero padding) ---- */
+typedef struct {
+    int B, H, W, C;        /* input: B×H×W×C */
+    int Ho, Wo, Co;        /* output: B×Ho×Wo×Co */
+    int kh, kw, sh, sw, dh, dw, pt, pl;
+    int groups;
+} knx_conv_geom;
+/* y = act(conv(x, w) + bias); w is (kh·kw·C/groups) × Co with rows ordered (ky, kx, ci). */
+KNX_API int knx_hip_conv(const knx_conv_geom* g, const float* x, const float* w, const float* bias, int act,
+                         float alpha, float* y, void* stream);
+
+/* ---- row and elementwise ops (y may equal x unless noted) ---- */
+KNX_API int knx_hip_layernorm(const float* x, float* y, int rows, int cols, const float* gamma, const float* beta,
+                              float eps, void* stream);
+KNX_API int knx_hip_softmax(const float* x, float* y, int rows, int cols, void* stream);
+KNX_API int knx_hip_bias_act(const float* x, float* y, int rows, int cols, const float* bias, int act, float alpha,
+                             void* stream);
+/* Per sample b < B and row i < R, column j < C: y = a ⊙ b with size-1 rows (ra/rb == 1) or channels (ca/cb == 1)
+ * broadcast within the sample. */
+KNX_API int knx_hip_binary(int op, const float* a, int ra, int ca, const float* b, int rb, int cb, float* y, int B,
+                           int R, int C, void* stream);
+/* Per sample, mean (type avg) or max over R rows of C channels → B×C. y must not alias x. */
+KNX_API int knx_hip_global_pool(int type, const float* x, int B, int R, int C, float* y, void* stream);
+/* y[r][c] = x[r][c]·scale[c] + shift[c] */
+KNX_API int knx_hip_affine(const float* x, float* y, int rows, int cols, const float* scale, const float* shift,
+                           void* stream);
+/* y[b][i] = x[b][i] + cst[i], i < per */
+KNX_API int knx_hip_add_const(const float* x, float* y, int B, int per, const float* cst, void* stream);
+
+/* Attention core, per (b, h): S = scale·Q_h·K_hᵀ (+ causal −inf above the diagonal), P = softmax(S), ctx_h = P·V_h.
+ * Q: (B·Rq) × (H·dk), K: (B·S) × (H·dk), V: (B·S) × (H·dv), ctx: (B·Rq) × (H·dv), all row-major fp32.
+ * scores: scratch of B·H·Rq·S floats used when the fused kernel does not apply (may be NULL otherwise). */
+KNX_API int knx_hip_attention_core(const float* Q, const float* K, const float* V, float* ctx, float* scores, int B,
+                                   int H, int Rq, int S, int dk, int dv, float scale, int causal, void* stream);
+
+/* ---- shape/copy ops for the remaining graph kinds ---- */
+/* Windowed pooling over NHWC (type max/avg, count_pad as PyTorch count_include_pad). */
+KNX_API int knx_hip_pool(int type, const knx_conv_geom* g, int count_pad, const float* x, float* y, void* stream);
+/* Per sample of n floats with shape d[0..nd) (row-major), out axis k = in axis perm[k]. */
+KNX_API int knx_hip_permute(const float* x, float* y, int B, int nd, const int* d, const int* perm, void* stream);
+/* y[r][y_off + j] = x[r][x_off + j], j < n, r < rows; row strides ldx, ldy. */
+KNX_API int knx_hip_copy_cols(const float* x, int ldx, int x_off, float* y, int ldy, int y_off, int rows, int n,
+                              void* stream);
+/* Zero padding of B×H×W×C into B×Ho×Wo×C at offset (pt, pl). */
+KNX_API int knx_hip_pad(const float* x, float* y, int B, int H, int W, int C, int Ho, int Wo, int pt, int pl,
+                        void* stream);
+/* Nearest upsampling by (sh, sw). */
+KNX_API int knx_hip_upsample(const float* x, float* y, int B, int H, int W, int C, int sh, int sw, void* stream);
+/* y[i] = table[id] for integral id in [0, V), else a NaN row; n ids, D floats per row. */
+KNX_API int knx_hip_embedding(const float* ids, int n, const float* table, int V, int D, float* y, void* stream);
+/* RNN gate update for one timestep (see the definition for the exact per-kind formulas). */
+KNX_API int knx_hip_rnn_gates(int kind, int act, float alpha, int B, int u, int first_step, float* z, const float* zh,
+                              float* c, float* h, float* dst, int dst_stride, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,83 @@
+// knx_common.hpp — shared device helpers and host-side error plumbing for the gfx950 kernels.
+// All HIP sources are compiled with -ffp-contract=off: a·b + c is two rounded operations everywhere, which is what
+// the reference's vector paths (vDSP / NEON, no FMA) compute and what makes the int8 epilogue bit-exact.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "knx_hip.h"
+
+namespace knx {
+
+// Records a formatted error message (thread-local) and returns code.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+// KNX_HIP_FAIL fault injection: true if the entry point `name` must fail.
+bool injected(const char* name);
+// Checks the last launch; returns KNX_OK or KNX_EHIP with the kernel name recorded.
+int check_launch(const char* what);
+// Number of compute units of the current device (cached).
+int num_cus();
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+}  // namespace knx
+
+#define KNX_ENTRY(name)                                                           \
+    do {                                                                          \
+        if (knx::injected(name)) return knx::fail(KNX_EINJECT, "%s: injected failure", name); \
+    } while (0)
+
+#define KNX_REQUIRE(cond, name)                                                   \
+    do {                                                                          \
+        if (!(cond)) return knx::fail(KNX_EINVAL, "%s: %s", name, #cond);         \
+    } while (0)
+
+// ---- activations (ids as the .knx file format); formulas of the reference's kernix_act_chunk
+//      (reference include/kernix_model.h:463-517) ----
+__device__ __forceinline__ float knx_relu6(float v) { return v < 0.0f ? 0.0f : v > 6.0f ? 6.0f : v; }
+__device__ __forceinline__ float knx_softplus(float v) { return v > 20.0f ? v : log1pf(expf(v)); }
+
+__device__ __forceinline__ float knx_act(float x, int act, float alpha)
+{
+    switch (act) {
+    case 0: return x >= 0.0f ? x : 0.0f;  // threshold at 0 (NaN → 0, as vDSP_vthr and Metal max)
+    case 1: {                              // GELU with Abramowitz–Stegun 7.1.26 erf
+        const float zz = x * 0.70710678f, t = expf(-zz * zz);
+        const float z = fabsf(x) * 0.70710678f;
+        const float k = 1.0f / (1.0f + 0.3275911f * z);
+        const float p = k * (0.254829592f + k * (-0.284496736f + k * (1.421413741f + k * (-1.453152027f + k * 1.061405429f))));
+        const float e = 1.0f - p * t;
+        return 0.5f * x * (1.0f + (x < 0.0f ? -e : e));
+    }
+    case 2: { const float s = 1.0f / (1.0f + expf(-x)); return x * s; }
+    case 3: return 1.0f / (1.0f + expf(-x));
+    case 4: return tanhf(x);
+    case 5: return x < 0.0f ? alpha * x : x;
+    case 6: return x < 0.0f ? alpha * expm1f(x) : x;
+    case 7: return 1.0507009873554805f * (x < 0.0f ? 1.6732632423543772f * expm1f(x) : x);
+    case 8: return knx_softplus(x);
+    case 9: return knx_relu6(x);
+    case 10: return knx_relu6(x + 3.0f) / 6.0f;
+    case 11: return x * knx_relu6(x + 3.0f) / 6.0f;
+    case 12: return 0.5f * x * (1.0f + tanhf(0.7978845608028654f * (x + 0.044715f * x * x * x)));
+    case 13: return expf(x);
+    case 14: return x * tanhf(knx_softplus(x));
+    case 15: return x / (1.0f + fabsf(x));
+    default: return x;
+    }
+}
+
+// Wave-wide (64 lanes) reductions through DPP/permute; every lane gets the result.
+__device__ __forceinline__ float knx_wave_sum(float v)
+{
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ float knx_wave_max(float v)
+{
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) { const float w = __shfl_xor(v, o, 64); v = w > v ? w : v; }
+    return v;
+}

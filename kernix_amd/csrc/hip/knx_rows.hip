@@ -1,0 +1,436 @@
+// knx_rows.hip — bandwidth-bound row and elementwise kernels of the KERNIX forward (gfx950).
+//
+// Row ops (layer_norm, softmax) run one 64-lane wavefront per row with DPP/permute reductions; elementwise ops are
+// grid-stride loops with one element per lane per iteration (consecutive lanes → consecutive addresses, so each
+// wave moves 256 contiguous bytes per access).  Formulas follow the reference CPU path line for line (file:line at
+// each kernel); summation order inside a row is the wave's tree order, which is why fp32 parity is by tolerance.
+#include "knx_common.hpp"
+
+namespace {
+
+inline unsigned grid_for(size_t n, unsigned block = 256)
+{
+    size_t g = (n + block - 1) / block;
+    const size_t cap = (size_t)knx::num_cus() * 16;
+    return (unsigned)(g < 1 ? 1 : g > cap ? cap : g);
+}
+
+// ---- layer_norm: reference include/kernix.h:667-677 (biased variance, rstd = 1/sqrtf(ss/cols + eps)) ----
+__global__ void __launch_bounds__(256) layernorm_kernel(const float* __restrict__ x, float* y, int rows, int cols,
+                                                         const float* __restrict__ gamma, const float* __restrict__ beta,
+                                                         float eps)
+{
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const float* xr = x + (size_t)row * cols;
+    float* yr = y + (size_t)row * cols;
+    float s = 0.0f;
+    for (int j = lane; j < cols; j += 64) s += xr[j];
+    const float mean = knx_wave_sum(s) / (float)cols;
+    float ss = 0.0f;
+    for (int j = lane; j < cols; j += 64) { const float d = xr[j] - mean; ss += d * d; }
+    const float rstd = 1.0f / sqrtf(knx_wave_sum(ss) / (float)cols + eps);
+    for (int j = lane; j < cols; j += 64) {
+        float v = (xr[j] - mean) * rstd;
+        if (gamma && beta) v = v * gamma[j] + beta[j];
+        else if (gamma) v = v * gamma[j];
+        else if (beta) v = v + beta[j];
+        yr[j] = v;
+    }
+}
+
+// ---- softmax: reference include/kernix.h:652-657 (exp(x − max) · (1/Σ)) ----
+__global__ void __launch_bounds__(256) softmax_kernel(const float* __restrict__ x, float* y, int rows, int cols)
+{
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const float* xr = x + (size_t)row * cols;
+    float* yr = y + (size_t)row * cols;
+    float m = -INFINITY;
+    for (int j = lane; j < cols; j += 64) m = xr[j] > m ? xr[j] : m;
+    m = knx_wave_max(m);
+    float s = 0.0f;
+    for (int j = lane; j < cols; j += 64) s += expf(xr[j] - m);
+    const float inv = 1.0f / knx_wave_sum(s);
+    for (int j = lane; j < cols; j += 64) yr[j] = expf(xr[j] - m) * inv;
+}
+
+// ---- bias + activation: reference include/kernix_model.h:528-541 ----
+__global__ void __launch_bounds__(256) bias_act_kernel(const float* x, float* y, size_t n, int cols,
+                                                        const float* __restrict__ bias, int act, float alpha)
+{
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        float v = x[i];
+        if (bias) v = v + bias[i % cols];
+        y[i] = knx_act(v, act, alpha);
+    }
+}
+
+// ---- broadcast binary: reference include/kernix_model.h:864-906 ----
+__device__ __forceinline__ float bin1(int op, float a, float b)
+{
+    switch (op) {
+    case 0: return a + b;
+    case 1: return a - b;
+    case 2: return a * b;
+    case 3: return a / b;
+    case 4: return a > b ? a : b;
+    default: return a < b ? a : b;
+    }
+}
+
+__global__ void __launch_bounds__(256) binary_kernel(int op, const float* a, int ra, int ca, const float* b, int rb, int cb,
+                                                      float* y, size_t n, int R, int C)
+{
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        const size_t row = i / C, j = i % C, bi = row / R, ri = row % R;
+        const float av = a[(bi * ra + (ra == 1 ? 0 : ri)) * ca + (ca == 1 ? 0 : j)];
+        const float bv = b[(bi * rb + (rb == 1 ? 0 : ri)) * cb + (cb == 1 ? 0 : j)];
+        y[i] = bin1(op, av, bv);
+    }
+}
+
+// ---- global pool: reference include/kernix_model.h:810-830 (sequential over rows, avg = Σ·(1/R)) ----
+__global__ void __launch_bounds__(256) global_pool_kernel(int type, const float* __restrict__ x, int B, int R, int C,
+                                                           float* __restrict__ y)
+{
+    const size_t n = (size_t)B * C;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        const size_t b = i / C, c = i % C;
+        const float* xp = x + b * (size_t)R * C + c;
+        float o = xp[0];
+        for (int r = 1; r < R; ++r) {
+            const float v = xp[(size_t)r * C];
+            o = type == 0 ? (o > v ? o : v) : o + v;
+        }
+        if (type == 1) o = o * (1.0f / (float)R);
+        y[i] = o;
+    }
+}
+
+// ---- affine / add_const: reference include/kernix_model.h:1882-1896 ----
+__global__ void __launch_bounds__(256) affine_kernel(const float* x, float* y, size_t n, int cols,
+                                                      const float* __restrict__ scale, const float* __restrict__ shift)
+{
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        const int c = (int)(i % cols);
+        y[i] = x[i] * scale[c] + shift[c];
+    }
+}
+
+__global__ void __launch_bounds__(256) add_const_kernel(const float* x, float* y, size_t n, int per,
+                                                         const float* __restrict__ cst)
+{
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        y[i] = x[i] + cst[i % per];
+}
+
+// ---- windowed pooling: reference include/kernix_model.h:773-807 ----
+__global__ void __launch_bounds__(256) pool_kernel(int type, knx_conv_geom g, int count_pad, const float* __restrict__ x,
+                                                    float* __restrict__ y)
+{
+    const size_t n = (size_t)g.B * g.Ho * g.Wo * g.C;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        const size_t c = i % g.C, r = i / g.C;
+        const size_t b = r / ((size_t)g.Ho * g.Wo), oy = (r / g.Wo) % g.Ho, ox = r % g.Wo;
+        float o = type == 0 ? -INFINITY : 0.0f;
+        int cnt = 0;
+        for (int ky = 0; ky < g.kh; ++ky) {
+            const long iy = (long)oy * g.sh - g.pt + ky;
+            if (iy < 0 || iy >= g.H) continue;
+            for (int kx = 0; kx < g.kw; ++kx) {
+                const long ix = (long)ox * g.sw - g.pl + kx;
+                if (ix < 0 || ix >= g.W) continue;
+                const float v = x[(((size_t)b * g.H + iy) * g.W + ix) * g.C + c];
+                o = type == 0 ? (o > v ? o : v) : o + v;
+                cnt++;
+            }
+        }
+        if (type == 1) o = o * (1.0f / (float)(count_pad ? g.kh * g.kw : (cnt ? cnt : 1)));
+        y[i] = o;
+    }
+}
+
+// ---- permute: reference include/kernix_model.h:833-862 ----
+struct PermArgs { int nd; int od[4]; int ist[4]; };
+
+__global__ void __launch_bounds__(256) permute_kernel(const float* __restrict__ x, float* __restrict__ y, size_t total,
+                                                       size_t per, PermArgs a)
+{
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+        const size_t b = i / per;
+        size_t rem = i % per, src = 0;
+        for (int k = a.nd - 1; k >= 0; --k) {
+            src += (rem % (size_t)a.od[k]) * (size_t)a.ist[k];
+            rem /= (size_t)a.od[k];
+        }
+        y[i] = x[b * per + src];
+    }
+}
+
+// ---- column block copy (CONCAT / SELECT): reference include/kernix_model.h:908-949 ----
+__global__ void __launch_bounds__(256) copy_cols_kernel(const float* __restrict__ x, int ldx, int x_off, float* __restrict__ y,
+                                                         int ldy, int y_off, int rows, int n)
+{
+    const size_t total = (size_t)rows * n;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+        const size_t r = i / n, j = i % n;
+        y[r * ldy + y_off + j] = x[r * ldx + x_off + j];
+    }
+}
+
+// ---- zero padding / nearest upsampling: reference include/kernix_model.h:951-984 ----
+__global__ void __launch_bounds__(256) pad_kernel(const float* __restrict__ x, float* __restrict__ y, int B, int H, int W,
+                                                   int C, int Ho, int Wo, int pt, int pl)
+{
+    const size_t n = (size_t)B * Ho * Wo * C;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        const size_t c = i % C, r = i / C;
+        const size_t b = r / ((size_t)Ho * Wo);
+        const long iy = (long)((r / Wo) % Ho) - pt, ix = (long)(r % Wo) - pl;
+        y[i] = (iy >= 0 && iy < H && ix >= 0 && ix < W) ? x[(((size_t)b * H + iy) * W + ix) * C + c] : 0.0f;
+    }
+}
+
+__global__ void __launch_bounds__(256) upsample_kernel(const float* __restrict__ x, float* __restrict__ y, int B, int H,
+                                                        int W, int C, int sh, int sw)
+{
+    const int Ho = H * sh, Wo = W * sw;
+    const size_t n = (size_t)B * Ho * Wo * C;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        const size_t c = i % C, r = i / C;
+        const size_t b = r / ((size_t)Ho * Wo), oy = (r / Wo) % Ho, ox = r % Wo;
+        y[i] = x[(((size_t)b * H + oy / sh) * W + ox / sw) * C + c];
+    }
+}
+
+// ---- embedding: reference include/kernix_model.h:987-1000 ----
+__global__ void __launch_bounds__(256) embedding_kernel(const float* __restrict__ ids, int n, const float* __restrict__ table,
+                                                         int V, int D, float* __restrict__ y)
+{
+    const size_t total = (size_t)n * D;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+        const size_t r = i / D, j = i % D;
+        const float id = ids[r];
+        y[i] = (id >= 0.0f && id < (float)V && id == floorf(id)) ? table[(size_t)id * D + j] : __int_as_float(0x7fc00000);
+    }
+}
+
+// ---- RNN gates for one timestep: reference include/kernix_model.h:594-627 ----
+// kind 4 LSTM (i f g o), 5 GRU (z r h, reset_after), 6 SimpleRNN.  z: B×gu input projection of this step (+ h·U for
+// LSTM/RNN when hu == NULL it is already included); hu: B×gu recurrent term to add (LSTM/RNN) or the GRU recurrent
+// term zh = brec + h·U (GRU).  c, h: B×u state.  dst: h written at dst + b·dst_stride when dst != NULL.
+__device__ __forceinline__ float sigm(float v) { return knx_act(v, 3, 0.0f); }
+
+__global__ void __launch_bounds__(256) rnn_gates_kernel(int kind, int act, float alpha, int B, int u, int step0, float* z,
+                                                         const float* hu, float* c, float* h, float* dst, int dst_stride)
+{
+    const int n = B * u;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+        const int b = i / u, j = i % u;
+        if (kind == 4) {
+            float* zb = z + (size_t)b * 4 * u;
+            float zi = zb[j], zf = zb[u + j], zg = zb[2 * u + j], zo = zb[3 * u + j];
+            if (hu) {
+                const float* hb = hu + (size_t)b * 4 * u;
+                zi = zi + hb[j]; zf = zf + hb[u + j]; zg = zg + hb[2 * u + j]; zo = zo + hb[3 * u + j];
+            }
+            const float ig = sigm(zi), fg = sigm(zf), gg = knx_act(zg, act, alpha), og = sigm(zo);
+            float cv = step0 ? ig * gg : fg * c[i];
+            if (!step0) cv = ig * gg + cv;
+            c[i] = cv;
+            const float hv = knx_act(cv, act, alpha) * og;
+            h[i] = hv;
+            if (dst) dst[(size_t)b * dst_stride + j] = hv;
+        } else if (kind == 5) {
+            float* zb = z + (size_t)b * 3 * u;
+            const float* hz = hu + (size_t)b * 3 * u;
+            const float zg = sigm(zb[j] + hz[j]);
+            const float rg = sigm(zb[u + j] + hz[u + j]);
+            const float hh = knx_act(rg * hz[2 * u + j] + zb[2 * u + j], act, alpha);
+            const float prev = step0 ? 0.0f : h[i];
+            const float hv = step0 ? (-hh) * zg + hh : (prev - hh) * zg + hh;
+            h[i] = hv;
+            if (dst) dst[(size_t)b * dst_stride + j] = hv;
+        } else {
+            float v = z[(size_t)b * u + j];
+            if (hu) v = v + hu[(size_t)b * u + j];
+            const float hv = knx_act(v, act, alpha);
+            h[i] = hv;
+            if (dst) dst[(size_t)b * dst_stride + j] = hv;
+        }
+    }
+}
+
+}  // namespace
+
+#define KNX_LAUNCH(name, kernel, grid, ...)                                                   \
+    do {                                                                                      \
+        hipLaunchKernelGGL(kernel, dim3(grid), dim3(256), 0, knx::as_stream(stream), __VA_ARGS__); \
+        return knx::check_launch(name);                                                       \
+    } while (0)
+
+extern "C" int knx_hip_layernorm(const float* x, float* y, int rows, int cols, const float* gamma, const float* beta,
+                                 float eps, void* stream)
+{
+    const char* name = "knx_hip_layernorm";
+    KNX_ENTRY(name);
+    KNX_REQUIRE(rows >= 0 && cols >= 1, name);
+    if (rows == 0) return KNX_OK;
+    KNX_REQUIRE(x && y, name);
+    KNX_LAUNCH(name, layernorm_kernel, (rows + 3) / 4, x, y, rows, cols, gamma, beta, eps);
+}
+
+extern "C" int knx_hip_softmax(const float* x, float* y, int rows, int cols, void* stream)
+{
+    const char* name = "knx_hip_softmax";
+    KNX_ENTRY(name);
+    KNX_REQUIRE(rows >= 0 && cols >= 1, name);
+    if (rows == 0) return KNX_OK;
+    KNX_REQUIRE(x && y, name);
+    KNX_LAUNCH(name, softmax_kernel, (rows + 3) / 4, x, y, rows, cols);
+}
+
+extern "C" int knx_hip_bias_act(const float* x, float* y, int rows, int cols, const float* bias, int act, float alpha,
+                                void* stream)
+{
+    const char* name = "knx_hip_bias_act";
+    KNX_ENTRY(name);
+    KNX_REQUIRE(rows >= 0 && cols >= 1 && act >= -1 && act <= 15, name);
+    const size_t n = (size_t)rows * cols;
+    if (n == 0) return KNX_OK;
+    KNX_REQUIRE(x && y, name);
+    KNX_LAUNCH(name, bias_act_kernel, grid_for(n), x, y, n, cols, bias, act, alpha);
+}
+
+extern "C" int knx_hip_binary(int op, const float* a, int ra, int ca, const float* b, int rb, int cb, float* y, int B,
+                              int R, int C, void* stream)
+{
+    const char* name = "knx_hip_binary";
+    KNX_ENTRY(name);
+    KNX_REQUIRE(op >= 0 && op <= 5 && B >= 0 && R >= 1 && C >= 1, name);
+    KNX_REQUIRE((ra == R || ra == 1) && (rb == R || rb == 1) && (ca == C || ca == 1) && (cb == C || cb == 1), name);
+    const size_t n = (size_t)B * R * C;
+    if (n == 0) return KNX_OK;
+    KNX_REQUIRE(a && b && y, name);
+    KNX_LAUNCH(name, binary_kernel, grid_for(n), op, a, ra, ca, b, rb, cb, y, n, R, C);
+}
+
+extern "C" int knx_hip_global_pool(int type, const float* x, int B, int R, int C, float* y, void* stream)
+{
+    const char* name = "knx_hip_global_pool";
+    KNX_ENTRY(name);
+    KNX_REQUIRE((type == 0 || type == 1) && B >= 0 && R >= 1 && C >= 1 && x != y, name);
+    if (B == 0) return KNX_OK;
+    KNX_REQUIRE(x && y, name);
+    KNX_LAUNCH(name, global_pool_kernel, grid_for((size_t)B * C), type, x, B, R, C, y);
+}
+
+extern "C" int knx_hip_affine(const float* x, float* y, int rows, int cols, const float* scale, const float* shift,
+                              void* stream)
+{
+    const char* name = "knx_hip_affine";
+    KNX_ENTRY(name);
+    KNX_REQUIRE(rows >= 0 && cols >= 1, name);
+    const size_t n = (size_t)rows * cols;
+    if (n == 0) return KNX_OK;
+    KNX_REQUIRE(x && y && scale && shift, name);
+    KNX_LAUNCH(name, affine_kernel, grid_for(n), x, y, n, cols, scale, shift);
+}
+
+extern "C" int knx_hip_add_const(const float* x, float* y, int B, int per, const float* cst, void* stream)
+{
+    const char* name = "knx_hip_add_const";
+    KNX_ENTRY(name);
+    KNX_REQUIRE(B >= 0 && per >= 1, name);
+    const size_t n = (size_t)B * per;
+    if (n == 0) return KNX_OK;
+    KNX_REQUIRE(x && y && cst, name);
+    KNX_LAUNCH(name, add_const_kernel, grid_for(n), x, y, n, per, cst);
+}
+
+extern "C" int knx_hip_pool(int type, const knx_conv_geom* g, int count_pad, const float* x, float* y, void* stream)
+{
+    const char* name = "knx_hip_pool";
+    KNX_ENTRY(name);
+    KNX_REQUIRE(g != nullptr && (type == 0 || type == 1) && x != y, name);
+    const size_t n = (size_t)g->B * g->Ho * g->Wo * g->C;
+    if (n == 0) return KNX_OK;
+    KNX_REQUIRE(x && y, name);
+    KNX_LAUNCH(name, pool_kernel, grid_for(n), type, *g, count_pad, x, y);
+}
+
+extern "C" int knx_hip_permute(const float* x, float* y, int B, int nd, const int* d, const int* perm, void* stream)
+{
+    const char* name = "knx_hip_permute";
+    KNX_ENTRY(name);
+    KNX_REQUIRE(nd >= 1 && nd <= 4 && B >= 0 && d && perm && x != y, name);
+    PermArgs a{};
+    a.nd = nd;
+    size_t st[4], per = 1;  // row-major strides of the input axes
+    for (int k = nd - 1; k >= 0; --k) { st[k] = per; per *= (size_t)d[k]; }
+    for (int k = 0; k < nd; ++k) {
+        KNX_REQUIRE(perm[k] >= 0 && perm[k] < nd, name);
+        a.od[k] = d[perm[k]];        // output axis k has the size of input axis perm[k]
+        a.ist[k] = (int)st[perm[k]]; // and walks with that axis' stride
+    }
+    const size_t total = per * (size_t)B;
+    if (total == 0) return KNX_OK;
+    KNX_LAUNCH(name, permute_kernel, grid_for(total), x, y, total, per, a);
+}
+
+extern "C" int knx_hip_copy_cols(const float* x, int ldx, int x_off, float* y, int ldy, int y_off, int rows, int n,
+                                 void* stream)
+{
+    const char* name = "knx_hip_copy_cols";
+    KNX_ENTRY(name);
+    KNX_REQUIRE(rows >= 0 && n >= 0 && x_off >= 0 && y_off >= 0 && x_off + n <= ldx && y_off + n <= ldy, name);
+    if ((size_t)rows * n == 0) return KNX_OK;
+    KNX_REQUIRE(x && y, name);
+    KNX_LAUNCH(name, copy_cols_kernel, grid_for((size_t)rows * n), x, ldx, x_off, y, ldy, y_off, rows, n);
+}
+
+extern "C" int knx_hip_pad(const float* x, float* y, int B, int H, int W, int C, int Ho, int Wo, int pt, int pl,
+                           void* stream)
+{
+    const char* name = "knx_hip_pad";
+    KNX_ENTRY(name);
+    KNX_REQUIRE(B >= 0 && H >= 1 && W >= 1 && C >= 1 && Ho >= H && Wo >= W && pt >= 0 && pl >= 0 && x != y, name);
+    const size_t n = (size_t)B * Ho * Wo * C;
+    if (n == 0) return KNX_OK;
+    KNX_LAUNCH(name, pad_kernel, grid_for(n), x, y, B, H, W, C, Ho, Wo, pt, pl);
+}
+
+extern "C" int knx_hip_upsample(const float* x, float* y, int B, int H, int W, int C, int sh, int sw, void* stream)
+{
+    const char* name = "knx_hip_upsample";
+    KNX_ENTRY(name);
+    KNX_REQUIRE(B >= 0 && H >= 1 && W >= 1 && C >= 1 && sh >= 1 && sw >= 1 && x != y, name);
+    const size_t n = (size_t)B * H * sh * W * sw * C;
+    if (n == 0) return KNX_OK;
+    KNX_LAUNCH(name, upsample_kernel, grid_for(n), x, y, B, H, W, C, sh, sw);
+}
+
+extern "C" int knx_hip_embedding(const float* ids, int n, const float* table, int V, int D, float* y, void* stream)
+{
+    const char* name = "knx_hip_embedding";
+    KNX_ENTRY(name);
+    KNX_REQUIRE(n >= 0 && V >= 1 && D >= 1, name);
+    if (n == 0) return KNX_OK;
+    KNX_REQUIRE(ids && table && y, name);
+    KNX_LAUNCH(name, embedding_kernel, grid_for((size_t)n * D), ids, n, table, V, D, y);
+}
+
+extern "C" int knx_hip_rnn_gates(int kind, int act, float alpha, int B, int u, int first_step, float* z, const float* zh,
+                                 float* c, float* h, float* dst, int dst_stride, void* stream)
+{
+    const char* name = "knx_hip_rnn_gates";
+    KNX_ENTRY(name);
+    KNX_REQUIRE((kind == 4 || kind == 5 || kind == 6) && B >= 0 && u >= 1 && act >= -1 && act <= 15, name);
+    KNX_REQUIRE(kind != 5 || zh != nullptr, name);
+    KNX_REQUIRE(kind != 4 || c != nullptr, name);
+    if (B == 0) return KNX_OK;
+    KNX_REQUIRE(z && h, name);
+    KNX_LAUNCH(name, rnn_gates_kernel, grid_for((size_t)B * u), kind, act, alpha, B, u, first_step, z, zh, c, h, dst,
+               dst_stride);
+}

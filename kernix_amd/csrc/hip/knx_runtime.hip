@@ -1,0 +1,179 @@
+// knx_runtime.hip — device selection, memory, copies and streams of the KERNIX HIP layer, plus error plumbing.
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <mutex>
+
+#include "knx_common.hpp"
+
+namespace knx {
+
+static thread_local char g_err[512];
+
+int fail(int code, const char* fmt, ...)
+{
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+bool injected(const char* name)
+{
+    const char* v = getenv("KNX_HIP_FAIL");
+    if (v == nullptr || *v == '\0') return false;
+    if (strcmp(v, "all") == 0) return true;
+    // comma separated list of entry-point names
+    const size_t n = strlen(name);
+    for (const char* p = v; *p;) {
+        const char* e = strchr(p, ',');
+        const size_t len = e ? (size_t)(e - p) : strlen(p);
+        if (len == n && strncmp(p, name, n) == 0) return true;
+        if (!e) break;
+        p = e + 1;
+    }
+    return false;
+}
+
+int check_launch(const char* what)
+{
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(KNX_EHIP, "%s: launch failed: %s", what, hipGetErrorString(e));
+    return KNX_OK;
+}
+
+static int g_cus = 0;
+
+int num_cus()
+{
+    if (g_cus == 0) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&g_cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            g_cus = 256;
+    }
+    return g_cus;
+}
+
+}  // namespace knx
+
+static std::once_flag g_init_once;
+static int g_init_rc = KNX_ENODEV;
+
+extern "C" int knx_hip_init(void)
+{
+    KNX_ENTRY("knx_hip_init");
+    std::call_once(g_init_once, [] {
+        int n = 0;
+        if (hipGetDeviceCount(&n) != hipSuccess || n < 1) {
+            g_init_rc = knx::fail(KNX_ENODEV, "knx_hip_init: no HIP device");
+            return;
+        }
+        hipDeviceProp_t prop;
+        if (hipGetDeviceProperties(&prop, 0) != hipSuccess) {
+            g_init_rc = knx::fail(KNX_ENODEV, "knx_hip_init: cannot query device 0");
+            return;
+        }
+        if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+            g_init_rc = knx::fail(KNX_ENODEV, "knx_hip_init: device 0 is %s, this library is built for gfx950", prop.gcnArchName);
+            return;
+        }
+        g_init_rc = KNX_OK;
+    });
+    if (g_init_rc != KNX_OK) return g_init_rc;
+    int cur = -1;
+    if (hipGetDevice(&cur) != hipSuccess || cur != 0) {
+        if (hipSetDevice(0) != hipSuccess) return knx::fail(KNX_EHIP, "knx_hip_init: hipSetDevice(0) failed");
+    }
+    return KNX_OK;
+}
+
+extern "C" const char* knx_hip_last_error(void) { return knx::g_err; }
+
+extern "C" int knx_hip_malloc(void** p, size_t bytes)
+{
+    KNX_ENTRY("knx_hip_malloc");
+    KNX_REQUIRE(p != nullptr, "knx_hip_malloc");
+    *p = nullptr;
+    if (bytes == 0) bytes = 256;  // non-NULL handle for empty tensors
+    const hipError_t e = hipMalloc(p, bytes);
+    if (e != hipSuccess) { *p = nullptr; return knx::fail(KNX_EHIP, "knx_hip_malloc(%zu): %s", bytes, hipGetErrorString(e)); }
+    return KNX_OK;
+}
+
+extern "C" int knx_hip_free(void* p)
+{
+    if (p == nullptr) return KNX_OK;
+    const hipError_t e = hipFree(p);
+    return e == hipSuccess ? KNX_OK : knx::fail(KNX_EHIP, "knx_hip_free: %s", hipGetErrorString(e));
+}
+
+extern "C" int knx_hip_host_malloc(void** p, size_t bytes)
+{
+    KNX_ENTRY("knx_hip_host_malloc");
+    KNX_REQUIRE(p != nullptr, "knx_hip_host_malloc");
+    *p = nullptr;
+    if (bytes == 0) bytes = 256;
+    const hipError_t e = hipHostMalloc(p, bytes, hipHostMallocDefault);
+    if (e != hipSuccess) { *p = nullptr; return knx::fail(KNX_EHIP, "knx_hip_host_malloc(%zu): %s", bytes, hipGetErrorString(e)); }
+    return KNX_OK;
+}
+
+extern "C" int knx_hip_host_free(void* p)
+{
+    if (p == nullptr) return KNX_OK;
+    const hipError_t e = hipHostFree(p);
+    return e == hipSuccess ? KNX_OK : knx::fail(KNX_EHIP, "knx_hip_host_free: %s", hipGetErrorString(e));
+}
+
+static int copy(void* dst, const void* src, size_t bytes, hipMemcpyKind kind, void* stream, const char* name)
+{
+    if (knx::injected(name)) return knx::fail(KNX_EINJECT, "%s: injected failure", name);
+    if (bytes == 0) return KNX_OK;
+    KNX_REQUIRE(dst != nullptr && src != nullptr, name);
+    const hipError_t e = hipMemcpyAsync(dst, src, bytes, kind, knx::as_stream(stream));
+    return e == hipSuccess ? KNX_OK : knx::fail(KNX_EHIP, "%s(%zu): %s", name, bytes, hipGetErrorString(e));
+}
+
+extern "C" int knx_hip_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream)
+{
+    return copy(dst, src, bytes, hipMemcpyHostToDevice, stream, "knx_hip_memcpy_h2d");
+}
+
+extern "C" int knx_hip_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream)
+{
+    return copy(dst, src, bytes, hipMemcpyDeviceToHost, stream, "knx_hip_memcpy_d2h");
+}
+
+extern "C" int knx_hip_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream)
+{
+    return copy(dst, src, bytes, hipMemcpyDeviceToDevice, stream, "knx_hip_memcpy_d2d");
+}
+
+extern "C" int knx_hip_stream_create(void** stream)
+{
+    KNX_ENTRY("knx_hip_stream_create");
+    KNX_REQUIRE(stream != nullptr, "knx_hip_stream_create");
+    hipStream_t s = nullptr;
+    // Default priority only; a non-blocking stream so the model does not serialize with the null stream.
+    const hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+    if (e != hipSuccess) return knx::fail(KNX_EHIP, "knx_hip_stream_create: %s", hipGetErrorString(e));
+    *stream = s;
+    return KNX_OK;
+}
+
+extern "C" int knx_hip_stream_destroy(void* stream)
+{
+    if (stream == nullptr) return KNX_OK;
+    const hipError_t e = hipStreamDestroy(knx::as_stream(stream));
+    return e == hipSuccess ? KNX_OK : knx::fail(KNX_EHIP, "knx_hip_stream_destroy: %s", hipGetErrorString(e));
+}
+
+extern "C" int knx_hip_stream_sync(void* stream)
+{
+    KNX_ENTRY("knx_hip_stream_sync");
+    const hipError_t e = hipStreamSynchronize(knx::as_stream(stream));
+    return e == hipSuccess ? KNX_OK : knx::fail(KNX_EHIP, "knx_hip_stream_sync: %s", hipGetErrorString(e));
+}

@@ -1,0 +1,745 @@
+/* knx_forward.c — device residency, workspace and forward of the KERNIX MI355X runtime.
+ *
+ * Replaces the reference's host-memory workspace, chunked execution and per-op CPU/Metal dispatch
+ * (reference include/kernix_model.h:1603-1694 workspace, :1844-1905 step dispatch, :1995-2064 forward) with:
+ *   - weights uploaded once, on the first forward, and kept on the device until kernix_model_free;
+ *   - one device arena per chunk size holding every storage buffer, per-step scratch, the dequantized int8 copies
+ *     and the staged input (allocated only when the chunk size changes, released by trim);
+ *   - every step enqueued on the model's stream; the host waits once per forward, after the device→host copy.
+ * Chunking under ws_limit and its results are the reference's: a batch larger than the limit allows runs in
+ * chunks of equal size (the last one smaller) and returns the concatenated output.
+ */
+#include <limits.h>
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "knx_internal.h"
+
+#define KNX_ALIGN 256
+
+static int hip_ok(int rc, const char* what)
+{
+    if (rc == KNX_OK) return 0;
+    KNX_LOG("KERNIX: %s failed: %s\n", what, knx_hip_last_error());
+    return -1;
+}
+
+/* ---------------------------------------------------------------- device weights */
+static int up(void** dst, const void* src, size_t bytes, void* stream)
+{
+    *dst = NULL;
+    if (src == NULL) return 0;
+    if (knx_hip_malloc(dst, bytes) != KNX_OK) return -1;
+    return knx_hip_memcpy_h2d(*dst, src, bytes, stream) == KNX_OK ? 0 : -1;
+}
+
+static int up_f(float** dst, const float* src, size_t n, void* stream) { return up((void**)dst, src, n * sizeof(float), stream); }
+static int up_t(float** dst, const float_tensor* t, void* stream)
+{
+    return t == NULL ? (*dst = NULL, 0) : up_f(dst, t->tensor, (size_t)t->row * (size_t)t->col, stream);
+}
+static int up_q(int8_t** dq, float** ds, const kernix_qweight* q, void* stream)
+{
+    *dq = NULL;
+    *ds = NULL;
+    if (q == NULL) return 0;
+    if (up((void**)dq, q->q, (size_t)q->np * (size_t)q->kp, stream) != 0) return -1;
+    return up_f(ds, q->scale, (size_t)q->np, stream);
+}
+
+static size_t gates(int kind) { return kind == KERNIX_OP_LSTM ? 4 : kind == KERNIX_OP_GRU ? 3 : 1; }
+
+static int upload_step(kernix_step* s, void* stream)
+{
+    struct knx_dstep* d = calloc(1, sizeof *d);
+    if (d == NULL) return -1;
+    s->dev = d;
+    const size_t gu = gates(s->kind) * (size_t)s->out;
+    const size_t nb = s->kind == KERNIX_OP_GRU ? 2 * gu : gu;
+    switch (s->kind) {
+    case KERNIX_OP_LINEAR:
+        if (up_t(&d->w, s->w, stream) || up_q(&d->q, &d->qscale, s->q, stream) || up_f(&d->bias, s->bias, (size_t)s->out, stream)) return -1;
+        break;
+    case KERNIX_OP_LAYERNORM:
+        if (up_f(&d->gamma, s->gamma, (size_t)s->in, stream) || up_f(&d->beta, s->beta, (size_t)s->in, stream)) return -1;
+        break;
+    case KERNIX_OP_AFFINE:
+        if (up_f(&d->gamma, s->gamma, (size_t)s->in, stream) || up_f(&d->beta, s->beta, (size_t)s->in, stream)) return -1;
+        break;
+    case KERNIX_OP_ADD_CONST:
+        if (up_f(&d->cst, s->cst, (size_t)s->in, stream)) return -1;
+        break;
+    case KERNIX_OP_CONV:
+    case KERNIX_OP_EMBEDDING:
+        if (up_t(&d->w, s->w, stream) || up_f(&d->bias, s->bias, (size_t)s->out, stream)) return -1;
+        break;
+    case KERNIX_OP_LSTM:
+    case KERNIX_OP_GRU:
+    case KERNIX_OP_RNN:
+        if (up_t(&d->w, s->w, stream) || up_f(&d->bias, s->bias, nb, stream) || up_q(&d->q, &d->qscale, s->q, stream) ||
+            up_f(&d->rec, s->rec, (size_t)s->out * gu, stream))
+            return -1;
+        if (s->dirs == 2 && (up_t(&d->w_b, s->w_b, stream) || up_f(&d->bias_b, s->bias_b, nb, stream) ||
+                             up_q(&d->q_b, &d->qscale_b, s->q_b, stream) || up_f(&d->rec_b, s->rec_b, (size_t)s->out * gu, stream)))
+            return -1;
+        if (s->dirs == 2 && s->merge == KERNIX_MERGE_AVE) {
+            float* h = malloc(sizeof(float) * (size_t)s->out);
+            float* z = calloc((size_t)s->out, sizeof(float));
+            int rc = h == NULL || z == NULL;
+            for (int i = 0; !rc && i < s->out; i++) h[i] = 0.5f;
+            if (!rc) rc = up_f(&d->half, h, (size_t)s->out, stream) || up_f(&d->zero, z, (size_t)s->out, stream);
+            /* the copies read h and z: wait before freeing them */
+            if (!rc) rc = knx_hip_stream_sync(stream) != KNX_OK;
+            free(h);
+            free(z);
+            if (rc) return -1;
+        }
+        break;
+    case KERNIX_OP_ATTENTION: {
+        const size_t hk = (size_t)s->heads * s->dk, hv = (size_t)s->heads * s->dv;
+        if (up_t(&d->w, s->w, stream) || up_f(&d->bias, s->bias, hk, stream) || up_t(&d->wk, s->wk, stream) ||
+            up_f(&d->bk, s->bk, hk, stream) || up_t(&d->wv, s->wv, stream) || up_f(&d->bv, s->bv, hv, stream) ||
+            up_t(&d->wo, s->wo, stream) || up_f(&d->bo, s->bo, (size_t)s->out, stream))
+            return -1;
+        break;
+    }
+    default:
+        break;
+    }
+    return 0;
+}
+
+static void free_dstep(kernix_step* s)
+{
+    struct knx_dstep* d = s->dev;
+    if (d == NULL) return;
+    void* p[] = { d->w, d->bias, d->gamma, d->beta, d->cst, d->q, d->qscale, d->rec, d->w_b, d->bias_b, d->q_b,
+                  d->qscale_b, d->rec_b, d->wk, d->wv, d->wo, d->bk, d->bv, d->bo, d->half, d->zero };
+    for (size_t i = 0; i < sizeof p / sizeof p[0]; i++) knx_hip_free(p[i]);
+    free(d);
+    s->dev = NULL;
+}
+
+/* Creates the device state and uploads every weight (first forward only). */
+static int ensure_device(kernix_model* m)
+{
+    if (m->dev != NULL && m->dev->uploaded) return 0;
+    if (knx_hip_init() != KNX_OK) {
+        KNX_LOG("KERNIX: no usable MI355X (gfx950) device: %s\n", knx_hip_last_error());
+        return -1;
+    }
+    if (m->dev == NULL) {
+        m->dev = calloc(1, sizeof *m->dev);
+        if (m->dev == NULL) return -1;
+        if (hip_ok(knx_hip_stream_create(&m->dev->stream), "stream creation") != 0) return -1;
+    }
+    for (int i = 0; i < m->n_steps; i++) {
+        if (m->steps[i].dev != NULL) continue;
+        if (upload_step(&m->steps[i], m->dev->stream) != 0) {
+            KNX_LOG("KERNIX: weight upload failed: %s\n", knx_hip_last_error());
+            return -1;
+        }
+    }
+    if (hip_ok(knx_hip_stream_sync(m->dev->stream), "weight upload") != 0) return -1;
+    m->dev->uploaded = 1;
+    return 0;
+}
+
+/* ---------------------------------------------------------------- workspace */
+/* COUNT: floats per sample; SIZE: arena bytes only; ALLOC: place every view in the arena; VIEW: shrink row counts */
+enum { WS_COUNT, WS_SIZE, WS_ALLOC, WS_VIEW };
+
+typedef struct {
+    int mode;
+    size_t off;      /* arena bytes used so far (ALLOC / sizing) */
+    char* base;      /* arena (ALLOC) */
+    size_t floats;   /* floats counted (COUNT) */
+} ws_ctx;
+
+static void* ws_take(ws_ctx* c, size_t bytes)
+{
+    const size_t at = c->off;
+    c->off += (bytes + KNX_ALIGN - 1) / KNX_ALIGN * KNX_ALIGN;
+    return c->base ? c->base + at : NULL;
+}
+
+/* One device tensor of rows × cols floats in the arena: COUNT adds its floats, ALLOC places a new view,
+ * VIEW shrinks the rows of the existing one. */
+static int ws_tensor(ws_ctx* c, float_tensor** t, size_t rows, size_t cols)
+{
+    if (rows > INT_MAX || cols > INT_MAX) return -1;
+    c->floats += rows * cols;
+    if (c->mode == WS_VIEW) { if (*t) (*t)->row = (int)rows; return 0; }
+    if (c->mode == WS_COUNT) return 0;
+    float* p = ws_take(c, rows * cols * sizeof(float));
+    if (c->mode == WS_ALLOC) {
+        if ((*t = malloc(sizeof(float_tensor))) == NULL) return -1;
+        **t = (float_tensor){ (int)rows, (int)cols, p };
+    }
+    return 0;
+}
+
+static int int8_rows(const kernix_model* m, size_t rows)
+{
+    if (m->int8_mode == KERNIX_INT8_I8) return (int)rows;
+    return (int)(rows < KERNIX_INT8_MAX_ROWS ? rows : KERNIX_INT8_MAX_ROWS);
+}
+
+/* Walks every workspace tensor for chunks of B samples.  ALLOC also places the dequantized int8 copies (the
+ * reference allocates them only when the chunk has more than KERNIX_INT8_MAX_ROWS rows, and so does this). */
+static int ws_walk(kernix_model* m, size_t B, ws_ctx* c)
+{
+    for (int k = 0; k < m->n_st; k++)
+        if (ws_tensor(c, &m->st[k], B, m->st_cap[k]) != 0) return -1;
+    for (int i = 0; i < m->n_steps; i++) {
+        kernix_step* s = &m->steps[i];
+        const kernix_val* vi = &m->vals[s->inp[0]];
+        const size_t rin = B * (size_t)vi->r;
+        if (c->mode != WS_COUNT) s->buf = &m->views[i + 1];
+        switch (s->kind) {
+        case KERNIX_OP_LINEAR:
+        case KERNIX_OP_LSTM:
+        case KERNIX_OP_GRU:
+        case KERNIX_OP_RNN: {
+            const int rnn = s->kind != KERNIX_OP_LINEAR;
+            const size_t qrows = rnn ? B : rin; /* rows of the int8 product: batch for the recurrence */
+            if (rnn) {
+                const size_t u = (size_t)s->out, gu = gates(s->kind) * u;
+                if (ws_tensor(c, &s->tmp[0], rin, gu) || ws_tensor(c, &s->tmp[1], B, gu) ||
+                    (s->kind == KERNIX_OP_LSTM && ws_tensor(c, &s->tmp[2], B, u)) || ws_tensor(c, &s->tmp[3], B, u) ||
+                    ws_tensor(c, &s->tmp[4], B, gu) ||
+                    (s->dirs == 2 && s->merge != KERNIX_MERGE_CONCAT && ws_tensor(c, &s->tmp[5], s->ret_seq ? rin : B, u)))
+                    return -1;
+            }
+            if (s->q == NULL) break;
+            /* int8 input rows and their scales, used only by the int8 path (both RNN directions run one after the
+             * other and share it: their recurrent weights have the same shape) */
+            const size_t xr = (size_t)int8_rows(m, qrows);
+            const size_t kp = (size_t)s->q->kp;
+            if (m->int8_mode == KERNIX_INT8_I8) c->floats += xr * (kp / 4 + 1);
+            if (c->mode == WS_SIZE || c->mode == WS_ALLOC) {
+                int8_t* xq = ws_take(c, xr * kp);
+                float* sx = ws_take(c, xr * sizeof(float));
+                if (c->mode == WS_ALLOC) { s->dev->xq = xq; s->dev->sx = sx; s->dev->xq_rows = (int)xr; }
+            }
+            /* fp32 copies of the int8 weights (counted in ws_fixed): reference dispatch with more rows than the
+             * int8 threshold */
+            if ((c->mode == WS_SIZE || c->mode == WS_ALLOC) && m->int8_mode == KERNIX_INT8_REF && qrows > KERNIX_INT8_MAX_ROWS) {
+                float* p = ws_take(c, (size_t)s->q->k * (size_t)s->q->n * sizeof(float));
+                float* pb = s->q_b ? ws_take(c, (size_t)s->q_b->k * (size_t)s->q_b->n * sizeof(float)) : NULL;
+                if (c->mode == WS_ALLOC) {
+                    if ((s->deq = malloc(sizeof(float_tensor))) == NULL) return -1;
+                    *s->deq = (float_tensor){ s->q->k, s->q->n, p };
+                    if (s->q_b) {
+                        if ((s->deq_b = malloc(sizeof(float_tensor))) == NULL) return -1;
+                        *s->deq_b = (float_tensor){ s->q_b->k, s->q_b->n, pb };
+                    }
+                }
+            }
+            break;
+        }
+        case KERNIX_OP_ATTENTION: {
+            const kernix_val* vv = &m->vals[s->inp[s->n_in > 1 ? 1 : 0]];
+            const size_t S = (size_t)vv->r, SR = B * S, H = (size_t)s->heads;
+            if (ws_tensor(c, &s->tmp[0], rin, H * s->dk) || ws_tensor(c, &s->tmp[1], SR, H * s->dk) ||
+                ws_tensor(c, &s->tmp[2], SR, H * s->dv) || ws_tensor(c, &s->tmp[3], rin * H, S) ||
+                ws_tensor(c, &s->tmp[4], rin, H * s->dv))
+                return -1;
+            break;
+        }
+        default:
+            break;
+        }
+    }
+    /* staged model input */
+    c->floats += B * (size_t)m->seq_len * (size_t)m->in_dim;
+    if (c->mode == WS_SIZE || c->mode == WS_ALLOC) {
+        float* din = ws_take(c, B * (size_t)m->seq_len * (size_t)m->in_dim * sizeof(float));
+        if (c->mode == WS_ALLOC) m->dev->d_in = din;
+    }
+    return 0;
+}
+
+int knx_model_count_ws(kernix_model* m, size_t* per_sample)
+{
+    ws_ctx c = { WS_COUNT, 0, NULL, 0 };
+    if (ws_walk(m, 1, &c) != 0) return -1;
+    *per_sample = c.floats;
+    return 0;
+}
+
+static void free_views(kernix_model* m)
+{
+    for (int k = 0; m->st != NULL && k < m->n_st; k++) { free(m->st[k]); m->st[k] = NULL; }
+    for (int i = 0; m->steps != NULL && i < m->n_steps; i++) {
+        kernix_step* s = &m->steps[i];
+        s->buf = NULL;
+        for (int k = 0; k < 6; k++) { free(s->tmp[k]); s->tmp[k] = NULL; }
+        free(s->deq);
+        s->deq = NULL;
+        free(s->deq_b);
+        s->deq_b = NULL;
+        if (s->dev) { s->dev->xq = NULL; s->dev->sx = NULL; s->dev->xq_rows = 0; }
+    }
+}
+
+static void free_out_all(kernix_model* m)
+{
+    if (m->out_all == NULL) return;
+    if (m->dev && m->dev->out_all_pinned) knx_hip_host_free(m->out_all->tensor);
+    else free(m->out_all->tensor);
+    free(m->out_all);
+    m->out_all = NULL;
+    if (m->dev) m->dev->out_all_pinned = 0;
+}
+
+/* Releases the workspace (arena, views, host output buffers); weights stay on the device. */
+void knx_model_release_device_ws(kernix_model* m)
+{
+    if (m == NULL) return;
+    m->batch = -1;
+    if (m->dev != NULL) {
+        if (m->dev->stream) knx_hip_stream_sync(m->dev->stream);
+        knx_hip_free(m->dev->arena);
+        m->dev->arena = NULL;
+        m->dev->arena_bytes = 0;
+        m->dev->d_in = NULL;
+        knx_hip_host_free(m->dev->h_out);
+        m->dev->h_out = NULL;
+        m->dev->h_out_floats = 0;
+    }
+    free_out_all(m);
+    free_views(m);
+    m->out_view = (float_tensor){ 0, m->out_dim, NULL };
+}
+
+void knx_model_release_device_all(kernix_model* m)
+{
+    if (m == NULL) return;
+    knx_model_release_device_ws(m);
+    for (int i = 0; m->steps != NULL && i < m->n_steps; i++) free_dstep(&m->steps[i]);
+    if (m->dev != NULL) {
+        knx_hip_stream_destroy(m->dev->stream);
+        free(m->dev);
+        m->dev = NULL;
+    }
+}
+
+void kernix_model_trim(kernix_model* m) { knx_model_release_device_ws(m); }
+
+/* Allocates the workspace for chunks of `rows` input rows (the old one is released first). */
+static int alloc_ws(kernix_model* m, int rows)
+{
+    knx_model_release_device_ws(m);
+    const size_t B = (size_t)rows / (size_t)m->seq_len;
+    ws_ctx c = { WS_SIZE, 0, NULL, 0 };
+    if (ws_walk(m, B, &c) != 0) return -1;
+    const size_t bytes = c.off;
+    void* arena = NULL;
+    if (hip_ok(knx_hip_malloc(&arena, bytes), "workspace allocation") != 0) return -1;
+    m->dev->arena = arena;
+    m->dev->arena_bytes = bytes;
+    ws_ctx a = { WS_ALLOC, 0, arena, 0 };
+    if (ws_walk(m, B, &a) != 0) { knx_model_release_device_ws(m); return -1; }
+    /* the fp32 copies of the int8 weights, computed on the device from the uploaded int8 weights */
+    for (int i = 0; i < m->n_steps; i++) {
+        kernix_step* s = &m->steps[i];
+        if (s->deq && hip_ok(knx_hip_dequant(s->dev->q, s->q->kp, s->dev->qscale, s->q->k, s->q->n, s->deq->tensor, m->dev->stream), "dequantization") != 0) {
+            knx_model_release_device_ws(m);
+            return -1;
+        }
+        if (s->deq_b && hip_ok(knx_hip_dequant(s->dev->q_b, s->q_b->kp, s->dev->qscale_b, s->q_b->k, s->q_b->n, s->deq_b->tensor, m->dev->stream), "dequantization") != 0) {
+            knx_model_release_device_ws(m);
+            return -1;
+        }
+    }
+    m->batch = rows;
+    return 0;
+}
+
+static void ws_view(kernix_model* m, int rows)
+{
+    ws_ctx c = { WS_VIEW, 0, NULL, 0 };
+    ws_walk(m, (size_t)rows / (size_t)m->seq_len, &c);
+}
+
+/* ---------------------------------------------------------------- steps */
+static void hw(const kernix_val* v, int* H, int* W)
+{
+    *H = v->d[0];
+    *W = v->nd == 3 ? v->d[1] : 1;
+}
+
+/* y (rows × n) = act(x·W + bias) with int8 weights: int8 arithmetic (per-row int8 input, int32 accumulation) or
+ * the fp32 copy, per the model's int8 mode; accumulate adds into y (RNN recurrence). */
+static int run_qlinear(const kernix_model* m, const kernix_qweight* q, const int8_t* dq, const float* dscale,
+                       const float_tensor* deq, int8_t* xq, float* sx, int xq_rows, const float* x, int rows,
+                       const float* bias, int act, float alpha, int accumulate, float* y, void* st)
+{
+    const int use_i8 = m->int8_mode == KERNIX_INT8_I8 || rows <= KERNIX_INT8_MAX_ROWS;
+    if (use_i8) {
+        if (rows > xq_rows || xq == NULL) { KNX_LOG("KERNIX: int8 scratch too small (%d > %d rows)\n", rows, xq_rows); return -1; }
+        if (hip_ok(knx_hip_quantize_rows(x, q->k, rows, q->k, q->kp, xq, q->kp, sx, st), "int8 input quantization")) return -1;
+        return hip_ok(knx_hip_i8gemm(rows, q->n, q->kp, xq, q->kp, sx, dq, q->kp, dscale, bias, act, alpha, accumulate, y,
+                                     q->n, NULL, 0, st), "int8 GEMM");
+    }
+    if (deq == NULL) { KNX_LOG("KERNIX: missing fp32 copy of an int8 weight\n"); return -1; }
+    if (accumulate) return -1; /* the recurrence adds through a separate buffer on this path */
+    return hip_ok(knx_hip_sgemm_ep(rows, q->n, q->k, x, q->k, deq->tensor, q->n, bias, act, alpha, y, q->n, st), "fp32 GEMM");
+}
+
+/* One direction of an RNN, reference include/kernix_model.h:563-632: the input projection of all timesteps is one
+ * GEMM; each timestep adds h·U (int8 or fp32) and applies the gates on the device. */
+static int run_rnn_dir(const kernix_model* m, kernix_step* s, int dir, const float_tensor* x, float* dst, int stride, void* st)
+{
+    struct knx_dstep* d = s->dev;
+    const int kind = s->kind, T = s->seq, u = s->out, gu = (int)gates(kind) * u;
+    const int B = x->row / T;
+    if (B == 0) return 0;
+    const float* W = dir ? d->w_b : d->w;
+    const float* bias = dir ? d->bias_b : d->bias;
+    const float* brec = kind == KERNIX_OP_GRU ? bias + gu : NULL;
+    const kernix_qweight* q = dir ? s->q_b : s->q;
+    const int8_t* dq = dir ? d->q_b : d->q;
+    const float* dsc = dir ? d->qscale_b : d->qscale;
+    const float_tensor* deq = dir ? s->deq_b : s->deq;
+    const float* U = q != NULL ? (deq ? deq->tensor : NULL) : (dir ? d->rec_b : d->rec);
+    float* zx = s->tmp[0]->tensor;
+    float* z = s->tmp[1]->tensor;
+    float* c = kind == KERNIX_OP_LSTM ? s->tmp[2]->tensor : NULL;
+    float* h = s->tmp[3]->tensor;
+    float* hu = s->tmp[4]->tensor;
+    /* the backward direction's int8 scratch sits right after the forward one's; both hold xq_rows rows */
+    int8_t* xq = d->xq;
+    float* sx = d->sx;
+    if (hip_ok(knx_hip_sgemm_ep(x->row, gu, s->in, x->tensor, s->in, W, gu, bias, -1, 0.0f, zx, gu, st), "RNN input projection")) return -1;
+    const int i8 = q != NULL && (m->int8_mode == KERNIX_INT8_I8 || B <= KERNIX_INT8_MAX_ROWS);
+    for (int step = 0; step < T; step++) {
+        const int t = dir ? T - 1 - step : step;
+        if (hip_ok(knx_hip_copy_cols(zx + (size_t)t * gu, T * gu, 0, z, gu, 0, B, gu, st), "RNN gate copy")) return -1;
+        const float* rec_term = NULL;
+        if (step == 0) {
+            if (kind == KERNIX_OP_GRU) { /* h = 0: the recurrent term is the recurrent bias */
+                if (hip_ok(knx_hip_sgemm_ep(B, gu, 0, NULL, 0, NULL, gu, brec, -1, 0.0f, hu, gu, st), "RNN bias")) return -1;
+                rec_term = hu;
+            }
+        } else if (i8) {
+            float* target = kind == KERNIX_OP_GRU ? hu : z;
+            if (run_qlinear(m, q, dq, dsc, NULL, xq, sx, d->xq_rows, h, B, brec, -1, 0.0f, kind != KERNIX_OP_GRU, target, st)) return -1;
+            rec_term = kind == KERNIX_OP_GRU ? hu : NULL;
+        } else {
+            if (U == NULL) return -1;
+            if (hip_ok(knx_hip_sgemm_ep(B, gu, u, h, u, U, gu, brec, -1, 0.0f, hu, gu, st), "RNN recurrence")) return -1;
+            rec_term = hu;
+        }
+        float* out_t = s->ret_seq ? dst + (size_t)t * stride : NULL;
+        if (hip_ok(knx_hip_rnn_gates(kind, s->act, s->alpha, B, u, step == 0, z, rec_term, c, h, out_t, T * stride, st), "RNN gates")) return -1;
+    }
+    if (!s->ret_seq && hip_ok(knx_hip_copy_cols(h, u, 0, dst, stride, 0, B, u, st), "RNN output")) return -1;
+    return 0;
+}
+
+static int run_rnn(const kernix_model* m, kernix_step* s, const float_tensor* x, float_tensor* y, void* st)
+{
+    const int u = s->out;
+    if (s->dirs == 1) return run_rnn_dir(m, s, 0, x, y->tensor, u, st);
+    if (s->merge == KERNIX_MERGE_CONCAT)
+        return run_rnn_dir(m, s, 0, x, y->tensor, 2 * u, st) || run_rnn_dir(m, s, 1, x, y->tensor + u, 2 * u, st) ? -1 : 0;
+    float* bw = s->tmp[5]->tensor;
+    if (run_rnn_dir(m, s, 0, x, y->tensor, u, st) || run_rnn_dir(m, s, 1, x, bw, u, st)) return -1;
+    const int rows = y->row;
+    if (hip_ok(knx_hip_binary(s->merge == KERNIX_MERGE_MUL ? KERNIX_BIN_MUL : KERNIX_BIN_ADD, y->tensor, rows, u, bw, rows, u,
+                              y->tensor, 1, rows, u, st), "RNN merge")) return -1;
+    if (s->merge == KERNIX_MERGE_AVE && hip_ok(knx_hip_affine(y->tensor, y->tensor, rows, u, s->dev->half, s->dev->zero, st), "RNN merge"))
+        return -1;
+    return 0;
+}
+
+static int run_step(kernix_model* m, int i, int B, void* st)
+{
+    kernix_step* s = &m->steps[i];
+    struct knx_dstep* d = s->dev;
+    const float_tensor* a = &m->views[s->inp[0]];
+    float_tensor* y = &m->views[i + 1];
+    const kernix_val* vi = &m->vals[s->inp[0]];
+    const kernix_val* vo = &m->vals[i + 1];
+    const int rows = y->row, cols = y->col;
+    switch (s->kind) {
+    case KERNIX_OP_LINEAR:
+        if (s->q != NULL)
+            return run_qlinear(m, s->q, d->q, d->qscale, s->deq, d->xq, d->sx, d->xq_rows, a->tensor, a->row, d->bias,
+                               s->act, s->alpha, 0, y->tensor, st);
+        return hip_ok(knx_hip_sgemm_ep(a->row, s->out, s->in, a->tensor, s->in, d->w, s->out, d->bias, s->act, s->alpha,
+                                       y->tensor, s->out, st), "Linear");
+    case KERNIX_OP_ACT:
+        return hip_ok(knx_hip_bias_act(a->tensor, y->tensor, rows, cols, NULL, s->act, s->alpha, st), "activation");
+    case KERNIX_OP_LAYERNORM:
+        return hip_ok(knx_hip_layernorm(a->tensor, y->tensor, rows, cols, d->gamma, d->beta, s->eps, st), "layer_norm");
+    case KERNIX_OP_SOFTMAX:
+        return hip_ok(knx_hip_softmax(a->tensor, y->tensor, rows, cols, st), "softmax");
+    case KERNIX_OP_LSTM:
+    case KERNIX_OP_GRU:
+    case KERNIX_OP_RNN:
+        return run_rnn(m, s, a, y, st);
+    case KERNIX_OP_CONV: {
+        if (knx_conv_is_gemm(s) == 0) /* 1×1 stride 1: a GEMM on the NHWC rows */
+            return hip_ok(knx_hip_sgemm_ep(a->row, s->out, s->in, a->tensor, s->in, d->w, s->out, d->bias, s->act, s->alpha,
+                                           y->tensor, s->out, st), "convolution");
+        knx_conv_geom g;
+        hw(vi, &g.H, &g.W);
+        hw(vo, &g.Ho, &g.Wo);
+        g.B = a->row / (g.H * g.W);
+        g.C = vi->c; g.Co = vo->c;
+        g.kh = s->kh; g.kw = s->kw; g.sh = s->sh; g.sw = s->sw; g.dh = s->dh; g.dw = s->dw; g.pt = s->pt; g.pl = s->pl;
+        g.groups = s->groups;
+        return hip_ok(knx_hip_conv(&g, a->tensor, d->w, d->bias, s->act, s->alpha, y->tensor, st), "convolution");
+    }
+    case KERNIX_OP_POOL: {
+        knx_conv_geom g;
+        memset(&g, 0, sizeof g);
+        hw(vi, &g.H, &g.W);
+        hw(vo, &g.Ho, &g.Wo);
+        g.C = vi->c; g.Co = vi->c;
+        g.B = a->row / (g.H * g.W);
+        g.kh = s->kh; g.kw = s->kw; g.sh = s->sh; g.sw = s->sw; g.pt = s->pt; g.pl = s->pl; g.dh = g.dw = 1; g.groups = 1;
+        return hip_ok(knx_hip_pool(s->ptype, &g, s->count_pad, a->tensor, y->tensor, st), "pooling");
+    }
+    case KERNIX_OP_GLOBAL_POOL:
+        return hip_ok(knx_hip_global_pool(s->ptype, a->tensor, a->row / vi->r, vi->r, vi->c, y->tensor, st), "global pooling");
+    case KERNIX_OP_RESHAPE:
+        return 0;
+    case KERNIX_OP_PERMUTE:
+        return hip_ok(knx_hip_permute(a->tensor, y->tensor, B, vi->nd, vi->d, s->perm, st), "permute");
+    case KERNIX_OP_BINARY: {
+        const kernix_val* vb = &m->vals[s->inp[1]];
+        return hip_ok(knx_hip_binary(s->bop, a->tensor, vi->r, vi->c, m->views[s->inp[1]].tensor, vb->r, vb->c, y->tensor,
+                                     B, vo->r, vo->c, st), "binary op");
+    }
+    case KERNIX_OP_CONCAT: {
+        const size_t R = (size_t)vo->r, C = (size_t)vo->c, per = R * C;
+        int off = 0;
+        for (int k = 0; k < s->n_in; k++) {
+            const kernix_val* v = &m->vals[s->inp[k]];
+            const float* src = m->views[s->inp[k]].tensor;
+            if (s->axis == KERNIX_AXIS_LAST) {
+                if (hip_ok(knx_hip_copy_cols(src, v->c, 0, y->tensor, (int)C, off, B * (int)R, v->c, st), "concatenate")) return -1;
+                off += v->c;
+            } else {
+                const int pk = v->r * v->c;
+                if (hip_ok(knx_hip_copy_cols(src, pk, 0, y->tensor, (int)per, off, B, pk, st), "concatenate")) return -1;
+                off += pk;
+            }
+        }
+        return 0;
+    }
+    case KERNIX_OP_EMBEDDING:
+        return hip_ok(knx_hip_embedding(a->tensor, a->row * a->col, d->w, s->in, s->out, y->tensor, st), "embedding");
+    case KERNIX_OP_AFFINE:
+        return hip_ok(knx_hip_affine(a->tensor, y->tensor, rows, cols, d->gamma, d->beta, st), "affine");
+    case KERNIX_OP_ADD_CONST:
+        return hip_ok(knx_hip_add_const(a->tensor, y->tensor, B, s->in, d->cst, st), "add_const");
+    case KERNIX_OP_ATTENTION: {
+        const int iv = s->inp[s->n_in > 1 ? 1 : 0], ik = s->inp[s->n_in > 2 ? 2 : s->n_in > 1 ? 1 : 0];
+        const float_tensor* vq = a;
+        const float_tensor* vv = &m->views[iv];
+        const float_tensor* vk = &m->views[ik];
+        const int Rq = vi->r, S = m->vals[iv].r, H = s->heads, hk = H * s->dk, hv = H * s->dv;
+        if (B == 0) return 0;
+        float* Q = s->tmp[0]->tensor;
+        float* K = s->tmp[1]->tensor;
+        float* V = s->tmp[2]->tensor;
+        float* ctx = s->tmp[4]->tensor;
+        if (hip_ok(knx_hip_sgemm_ep(vq->row, hk, vq->col, vq->tensor, vq->col, d->w, hk, d->bias, -1, 0.0f, Q, hk, st), "attention Q") ||
+            hip_ok(knx_hip_sgemm_ep(vk->row, hk, vk->col, vk->tensor, vk->col, d->wk, hk, d->bk, -1, 0.0f, K, hk, st), "attention K") ||
+            hip_ok(knx_hip_sgemm_ep(vv->row, hv, vv->col, vv->tensor, vv->col, d->wv, hv, d->bv, -1, 0.0f, V, hv, st), "attention V"))
+            return -1;
+        if (hip_ok(knx_hip_attention_core(Q, K, V, ctx, s->tmp[3]->tensor, B, H, Rq, S, s->dk, s->dv, 1.0f / sqrtf((float)s->dk),
+                                          s->causal, st), "attention"))
+            return -1;
+        return hip_ok(knx_hip_sgemm_ep(vq->row, s->out, hv, ctx, hv, d->wo, s->out, d->bo, -1, 0.0f, y->tensor, s->out, st),
+                      "attention output");
+    }
+    case KERNIX_OP_SELECT: {
+        const int per = vi->r * vi->c;
+        if (s->axis == KERNIX_AXIS_FIRST) {
+            const int blk = per / vi->d[0], n = blk * s->len;
+            return hip_ok(knx_hip_copy_cols(a->tensor, per, s->start * blk, y->tensor, n, 0, B, n, st), "select");
+        }
+        return hip_ok(knx_hip_copy_cols(a->tensor, vi->c, s->start, y->tensor, s->len, 0, B * vi->r, s->len, st), "select");
+    }
+    case KERNIX_OP_PAD: {
+        int H, W, Ho, Wo;
+        hw(vi, &H, &W);
+        hw(vo, &Ho, &Wo);
+        return hip_ok(knx_hip_pad(a->tensor, y->tensor, a->row / (H * W), H, W, vi->c, Ho, Wo, s->pt, s->pl, st), "pad");
+    }
+    case KERNIX_OP_UPSAMPLE: {
+        int H, W;
+        hw(vi, &H, &W);
+        return hip_ok(knx_hip_upsample(a->tensor, y->tensor, a->row / (H * W), H, W, vi->c, s->sh, s->sw, st), "upsample");
+    }
+    default:
+        return -1;
+    }
+}
+
+/* Enqueues every step for one chunk whose input starts at `in` (device). */
+static int run_chunk(kernix_model* m, const float* in, int B, void* st)
+{
+    for (int v = 0; v < m->n_vals; v++) {
+        const kernix_val* val = &m->vals[v];
+        m->views[v] = (float_tensor){ B * val->r, val->c, val->st < 0 ? (float*)in : m->st[val->st]->tensor };
+    }
+    if (B == 0) return 0;
+    for (int i = 0; i < m->n_steps; i++)
+        if (run_step(m, i, B, st) != 0) return -1;
+    return 0;
+}
+
+/* Samples per chunk under ws_limit (reference include/kernix_model.h:2036-2043). */
+static int chunk_samples(const kernix_model* m, int samples)
+{
+    int chunk = samples;
+    if (m->ws_limit > 0 && m->ws_per_sample > 0) {
+        const size_t fixed = m->ws_fixed * sizeof(float), avail = m->ws_limit > fixed ? m->ws_limit - fixed : 0;
+        size_t c = avail / (m->ws_per_sample * sizeof(float));
+        if (c < 1) c = 1;
+        if (c < (size_t)samples) chunk = (int)c;
+    }
+    return chunk;
+}
+
+static int ensure_host_out(kernix_model* m, int B)
+{
+    const size_t need = (size_t)B * (size_t)m->out_dim;
+    if (m->dev->h_out != NULL && m->dev->h_out_floats >= need) return 0;
+    knx_hip_host_free(m->dev->h_out);
+    m->dev->h_out = NULL;
+    m->dev->h_out_floats = 0;
+    void* p = NULL;
+    if (hip_ok(knx_hip_host_malloc(&p, need * sizeof(float)), "pinned output allocation")) return -1;
+    m->dev->h_out = p;
+    m->dev->h_out_floats = need;
+    return 0;
+}
+
+static int ensure_out_all(kernix_model* m, int samples)
+{
+    if (m->out_all != NULL && m->out_all->row == samples) return 0;
+    free_out_all(m);
+    float_tensor* t = malloc(sizeof *t);
+    void* p = NULL;
+    if (t == NULL || hip_ok(knx_hip_host_malloc(&p, (size_t)samples * (size_t)m->out_dim * sizeof(float)), "pinned output allocation")) {
+        free(t);
+        return -1;
+    }
+    *t = (float_tensor){ samples, m->out_dim, p };
+    m->out_all = t;
+    m->dev->out_all_pinned = 1;
+    return 0;
+}
+
+const float_tensor* kernix_model_forward(kernix_model* m, const float_tensor* x)
+{
+    if (m == NULL || x == NULL || x->tensor == NULL || x->row < 0 || x->col != m->in_dim || x->row % m->seq_len != 0) return NULL;
+    int own = m->out_all != NULL && x->tensor == m->out_all->tensor;
+    own |= m->dev != NULL && m->dev->h_out != NULL && x->tensor == m->dev->h_out;
+    if (own) {
+        KNX_LOG("forward: this model's output buffer cannot be its own input (pass a copy)\n");
+        return NULL;
+    }
+    if (ensure_device(m) != 0) return NULL;
+    void* st = m->dev->stream;
+    const int samples = x->row / m->seq_len;
+    const int chunk = chunk_samples(m, samples);
+    const int crow = chunk * m->seq_len;
+    if (crow != m->batch && alloc_ws(m, crow) != 0) return NULL;
+    const size_t in_per = (size_t)m->seq_len * (size_t)m->in_dim;
+
+    if (chunk == samples) {
+        ws_view(m, crow);
+        if (ensure_host_out(m, samples) != 0) return NULL;
+        if (samples > 0) {
+            if (hip_ok(knx_hip_memcpy_h2d(m->dev->d_in, x->tensor, (size_t)samples * in_per * sizeof(float), st), "input copy") ||
+                run_chunk(m, m->dev->d_in, samples, st) != 0 ||
+                hip_ok(knx_hip_memcpy_d2h(m->dev->h_out, m->views[m->out_v].tensor, (size_t)samples * m->out_dim * sizeof(float), st), "output copy") ||
+                hip_ok(knx_hip_stream_sync(st), "forward"))
+                return NULL;
+        }
+        m->out_view = (float_tensor){ samples, m->out_dim, m->dev->h_out };
+        return &m->out_view;
+    }
+    if (ensure_out_all(m, samples) != 0) return NULL;
+    for (int s0 = 0; s0 < samples; s0 += chunk) {
+        const int n = samples - s0 < chunk ? samples - s0 : chunk;
+        ws_view(m, n * m->seq_len);
+        if (hip_ok(knx_hip_memcpy_h2d(m->dev->d_in, x->tensor + (size_t)s0 * in_per, (size_t)n * in_per * sizeof(float), st), "input copy") ||
+            run_chunk(m, m->dev->d_in, n, st) != 0 ||
+            hip_ok(knx_hip_memcpy_d2h(m->out_all->tensor + (size_t)s0 * m->out_dim, m->views[m->out_v].tensor,
+                                      (size_t)n * m->out_dim * sizeof(float), st), "output copy"))
+            return NULL;
+    }
+    if (hip_ok(knx_hip_stream_sync(st), "forward")) return NULL;
+    return m->out_all;
+}
+
+int kernix_model_forward_device(kernix_model* m, const float* d_x, int rows, float* d_out, void* stream)
+{
+    if (m == NULL || d_x == NULL || d_out == NULL || rows < 0 || rows % m->seq_len != 0) return -1;
+    if (ensure_device(m) != 0) return -1;
+    void* st = stream ? stream : m->dev->stream;
+    const int samples = rows / m->seq_len;
+    const int chunk = chunk_samples(m, samples);
+    const int crow = chunk * m->seq_len;
+    if (crow != m->batch) {
+        if (stream) knx_hip_stream_sync(stream); /* the old workspace may still be in use on the caller's stream */
+        if (alloc_ws(m, crow) != 0) return -1;
+        if (hip_ok(knx_hip_stream_sync(m->dev->stream), "dequantization")) return -1;
+    }
+    const size_t in_per = (size_t)m->seq_len * (size_t)m->in_dim;
+    for (int s0 = 0; s0 < samples; s0 += chunk) {
+        const int n = samples - s0 < chunk ? samples - s0 : chunk;
+        ws_view(m, n * m->seq_len);
+        if (run_chunk(m, d_x + (size_t)s0 * in_per, n, st) != 0 ||
+            hip_ok(knx_hip_memcpy_d2d(d_out + (size_t)s0 * m->out_dim, m->views[m->out_v].tensor, (size_t)n * m->out_dim * sizeof(float), st), "output copy"))
+            return -1;
+    }
+    return 0;
+}
+
+/* ---------------------------------------------------------------- kernel-level int8 contract */
+int kernix_qmatmul(const float* x, int rows, const kernix_qweight* w, const float* bias, int accumulate, float* y)
+{
+    if (w == NULL || rows < 0 || (rows > 0 && (x == NULL || y == NULL))) return -1;
+    if (rows == 0) return 0;
+    if (knx_hip_init() != KNX_OK) {
+        KNX_LOG("KERNIX: no usable MI355X (gfx950) device: %s\n", knx_hip_last_error());
+        return -1;
+    }
+    const size_t k = (size_t)w->k, n = (size_t)w->n, kp = (size_t)w->kp, np = (size_t)w->np, R = (size_t)rows;
+    float *dx = NULL, *dsx = NULL, *dsc = NULL, *db = NULL, *dy = NULL;
+    int8_t *dxq = NULL, *dq = NULL;
+    void* st = NULL;
+    int rc = -1;
+    if (knx_hip_stream_create(&st) != KNX_OK || knx_hip_malloc((void**)&dx, R * k * 4) || knx_hip_malloc((void**)&dxq, R * kp) ||
+        knx_hip_malloc((void**)&dsx, R * 4) || knx_hip_malloc((void**)&dq, np * kp) || knx_hip_malloc((void**)&dsc, np * 4) ||
+        knx_hip_malloc((void**)&dy, R * n * 4) || (bias && knx_hip_malloc((void**)&db, n * 4)))
+        goto done;
+    if (knx_hip_memcpy_h2d(dx, x, R * k * 4, st) || knx_hip_memcpy_h2d(dq, w->q, np * kp, st) ||
+        knx_hip_memcpy_h2d(dsc, w->scale, np * 4, st) || (bias && knx_hip_memcpy_h2d(db, bias, n * 4, st)) ||
+        (accumulate && knx_hip_memcpy_h2d(dy, y, R * n * 4, st)))
+        goto done;
+    if (knx_hip_quantize_rows(dx, (int)k, rows, (int)k, (int)kp, dxq, (int)kp, dsx, st) ||
+        knx_hip_i8gemm(rows, (int)n, (int)kp, dxq, (int)kp, dsx, dq, (int)kp, dsc, db, -1, 0.0f, accumulate, dy, (int)n, NULL, 0, st) ||
+        knx_hip_memcpy_d2h(y, dy, R * n * 4, st) || knx_hip_stream_sync(st))
+        goto done;
+    rc = 0;
+done:
+    if (rc != 0) KNX_LOG("KERNIX: kernix_qmatmul failed: %s\n", knx_hip_last_error());
+    if (st) knx_hip_stream_sync(st);
+    knx_hip_free(dx); knx_hip_free(dxq); knx_hip_free(dsx); knx_hip_free(dq); knx_hip_free(dsc); knx_hip_free(db); knx_hip_free(dy);
+    knx_hip_stream_destroy(st);
+    return rc;
+}

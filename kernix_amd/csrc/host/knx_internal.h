@@ -1,0 +1,63 @@
+/* knx_internal.h — private declarations shared by the host runtime files (loader, workspace/forward, C ABI). */
+#ifndef KNX_INTERNAL_H
+#define KNX_INTERNAL_H
+
+#include <stdio.h>
+
+#include "kernix_model.h"
+#include "knx_hip.h"
+
+/* Device copies of one step's parameters, uploaded on the first forward and kept until kernix_model_free. */
+struct knx_dstep {
+    float* w;         /* LINEAR/CONV/EMBEDDING fp32 weight, RNN input weight, ATTENTION Wq */
+    float* bias;
+    float* gamma;
+    float* beta;
+    float* cst;
+    int8_t* q;        /* int8 weight, np × kp (output channel rows, k contiguous) */
+    float* qscale;    /* np scales */
+    float* rec;       /* RNN fp32 recurrent weight */
+    float* w_b;       /* backward direction */
+    float* bias_b;
+    int8_t* q_b;
+    float* qscale_b;
+    float* rec_b;
+    float* wk;        /* ATTENTION */
+    float* wv;
+    float* wo;
+    float* bk;
+    float* bv;
+    float* bo;
+    float* half;      /* RNN AVE merge: u × 0.5 */
+    float* zero;      /* u × 0 */
+    /* per-chunk scratch inside the workspace arena */
+    int8_t* xq;       /* int8 input rows (rows × kp) */
+    float* sx;        /* their scales */
+    int xq_rows;
+};
+
+/* Device side of a model. */
+struct knx_dmodel {
+    void* stream;     /* hipStream_t owned by the model */
+    int uploaded;     /* weights on the device */
+    void* arena;      /* workspace: storage buffers, step scratch, dequantized copies, input staging */
+    size_t arena_bytes;
+    float* d_in;      /* device copy of the current chunk's input */
+    float* h_out;     /* pinned host output of an unchunked forward (batch × out_dim) */
+    size_t h_out_floats;
+    int out_all_pinned; /* out_all->tensor was allocated pinned */
+};
+
+/* loader (knx_load.c) */
+int knx_model_count_ws(kernix_model* m, size_t* per_sample); /* floats per sample of workspace, 0 or -1 */
+size_t knx_conv_is_gemm(const kernix_step* s);
+void knx_step_host_free(kernix_step* s);
+
+/* workspace / device (knx_forward.c) */
+void knx_model_release_device_ws(kernix_model* m);
+void knx_model_release_device_all(kernix_model* m);
+
+/* messages */
+#define KNX_LOG(...) fprintf(stderr, __VA_ARGS__)
+
+#endif

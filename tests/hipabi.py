@@ -1,0 +1,74 @@
+"""ctypes bindings of the C ABI declared in include/knx_hip.h, for the kernel-level tests and the benchmark.
+
+Device buffers come from torch (plumbing only); every computation goes through libkernix.so.
+"""
+import ctypes
+import os
+import re
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.environ.get("KERNIX_LIB", os.path.join(ROOT, "kernix_amd", "libkernix.so"))
+
+P, I, F, Z = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
+
+
+class ConvGeom(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in
+                ("B", "H", "W", "C", "Ho", "Wo", "Co", "kh", "kw", "sh", "sw", "dh", "dw", "pt", "pl", "groups")]
+
+
+SIGS = {
+    "knx_hip_init": ([], I),
+    "knx_hip_last_error": ([], ctypes.c_char_p),
+    "knx_hip_quantize_rows": ([P, I, I, I, I, P, I, P, P], I),
+    "knx_hip_i8gemm": ([I, I, I, P, I, P, P, I, P, P, I, F, I, P, I, P, I, P], I),
+    "knx_hip_dequant": ([P, I, P, I, I, P, P], I),
+    "knx_hip_sgemm_ep": ([I, I, I, P, I, P, I, P, I, F, P, I, P], I),
+    "knx_hip_conv": ([ctypes.POINTER(ConvGeom), P, P, P, I, F, P, P], I),
+    "knx_hip_layernorm": ([P, P, I, I, P, P, F, P], I),
+    "knx_hip_softmax": ([P, P, I, I, P], I),
+    "knx_hip_bias_act": ([P, P, I, I, P, I, F, P], I),
+    "knx_hip_binary": ([I, P, I, I, P, I, I, P, I, I, I, P], I),
+    "knx_hip_global_pool": ([I, P, I, I, I, P, P], I),
+    "knx_hip_affine": ([P, P, I, I, P, P, P], I),
+    "knx_hip_add_const": ([P, P, I, I, P, P], I),
+    "knx_hip_attention_core": ([P, P, P, P, P, I, I, I, I, I, I, F, I, P], I),
+}
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (args, res) in SIGS.items():
+            f = getattr(L, name)
+            f.argtypes, f.restype = args, res
+        _lib = L
+    return _lib
+
+
+def check(rc):
+    if rc != 0:
+        raise RuntimeError(f"knx_hip call failed ({rc}): {lib().knx_hip_last_error().decode()}")
+
+
+def declared_symbols():
+    """Every function declared in include/*.h (the ABI surface the library must export)."""
+    names = set()
+    for h in ("kernix.h", "kernix_model.h", "kernix_capi.h", "knx_hip.h"):
+        text = open(os.path.join(ROOT, "include", h)).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        for m in re.finditer(r"(?:KERNIX_API|KNX_API)\s+[\w\s\*]+?\b(\w+)\s*\(", text):
+            names.add(m.group(1))
+    return names
+
+
+def ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def stream():
+    import torch
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)

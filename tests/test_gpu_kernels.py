@@ -1,0 +1,231 @@
+"""Kernel-level parity of the gfx950 kernels against the CPU oracle, through the C ABI (include/knx_hip.h).
+
+int8: int32 accumulators and ReLU-epilogue outputs bit-exact; fp32 ops: max|a−b| / max(1, max|ref|) ≤ 1e-4
+(the fp32 GEMM against the float64 closed form), row ops ≤ 1e-5.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+from oracle import knx_ref
+from tests import hipabi
+from tests.hipabi import ptr
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+def dev(a):
+    """Device copy of a numpy array.  Keep the returned tensor alive while a kernel may use it: a temporary would go
+    back to torch's caching allocator and its memory could be handed to the next allocation."""
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def rel_err(got, want):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    return float(np.max(np.abs(got - want)) / max(1.0, float(np.max(np.abs(want))))) if want.size else 0.0
+
+
+@pytest.fixture(scope="module")
+def L():
+    lib = hipabi.lib()
+    hipabi.check(lib.knx_hip_init())
+    return lib
+
+
+# ---------------------------------------------------------------- int8 GEMM
+I8_SHAPES = [(1, 16, 64), (2, 10, 64), (5, 100, 192), (64, 256, 128), (200, 520, 320), (300, 300, 1024),
+             (512, 512, 256), (1, 4096, 4096), (16, 4096, 4096), (1024, 1024, 512), (2048, 2048, 256)]
+
+
+@pytest.mark.parametrize("M,N,K", I8_SHAPES)
+def test_i8gemm_bit_exact(L, M, N, K):
+    rng = np.random.default_rng(M * 7 + N * 13 + K)
+    A = rng.integers(-127, 128, (M, K), dtype=np.int8)
+    W = rng.integers(-128, 128, (N, K), dtype=np.int8)
+    sa = rng.uniform(0.001, 0.01, M).astype(np.float32)
+    sw = rng.uniform(0.001, 0.01, N).astype(np.float32)
+    bias = rng.normal(0, 0.1, N).astype(np.float32)
+    want_y, want_acc = knx_ref.i8gemm(A, W, sa, sw, bias, act_id=0)
+    dA, dW, dsa, dsw, db = dev(A), dev(W), dev(sa), dev(sw), dev(bias)
+    Y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    acc = torch.empty((M, N), dtype=torch.int32, device="cuda")
+    hipabi.check(L.knx_hip_i8gemm(M, N, K, ptr(dA), K, ptr(dsa), ptr(dW), K, ptr(dsw), ptr(db), 0, 0.0, 0,
+                                  ptr(Y), N, ptr(acc), N, hipabi.stream()))
+    assert np.array_equal(host(acc), want_acc)
+    assert np.array_equal(host(Y), want_y)
+
+
+def test_i8gemm_accumulate_and_no_bias(L):
+    rng = np.random.default_rng(3)
+    M, N, K = 37, 70, 128
+    A = rng.integers(-127, 128, (M, K), dtype=np.int8)
+    W = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    sa = rng.uniform(0.001, 0.01, M).astype(np.float32)
+    sw = rng.uniform(0.001, 0.01, N).astype(np.float32)
+    y0 = rng.normal(0, 1, (M, N)).astype(np.float32)
+    _, acc = knx_ref.i8gemm(A, W, sa, sw, None, act_id=-1)
+    want = ((acc.astype(np.float32) * sa[:, None]).astype(np.float32) * sw[None, :]).astype(np.float32)
+    want = (y0 + want).astype(np.float32)
+    Y, dA, dsa, dW, dsw = dev(y0), dev(A), dev(sa), dev(W), dev(sw)
+    hipabi.check(L.knx_hip_i8gemm(M, N, K, ptr(dA), K, ptr(dsa), ptr(dW), K, ptr(dsw), None, -1, 0.0, 1,
+                                  ptr(Y), N, None, 0, hipabi.stream()))
+    assert np.array_equal(host(Y), want)
+
+
+def test_i8gemm_rejects_bad_shapes(L):
+    assert L.knx_hip_i8gemm(4, 4, 60, None, 60, None, None, 60, None, None, 0, 0.0, 0, None, 4, None, 0, None) != 0
+
+
+# ---------------------------------------------------------------- quantize rows
+@pytest.mark.parametrize("rows,k", [(1, 1), (3, 55), (32, 114), (4, 784), (2, 4096)])
+def test_quantize_rows_bit_exact(L, rows, k):
+    rng = np.random.default_rng(rows * 31 + k)
+    x = (rng.integers(0, 2001, (rows, k)) * 0.003 - 3.0).astype(np.float32)
+    if rows >= 3:
+        x[1, k // 2] = np.nan
+        x[2, :] = 0.0
+    kp = (k + 63) // 64 * 64
+    xq_want, sx_want, bad = knx_ref.quantize_rows(x)
+    dx = dev(x)
+    xq = torch.full((rows, kp), 99, dtype=torch.int8, device="cuda")
+    sx = torch.empty(rows, dtype=torch.float32, device="cuda")
+    hipabi.check(L.knx_hip_quantize_rows(ptr(dx), k, rows, k, kp, ptr(xq), kp, ptr(sx), hipabi.stream()))
+    got_q, got_s = host(xq), host(sx)
+    for r in range(rows):
+        if bad[r]:
+            assert np.isnan(got_s[r])
+            continue
+        assert got_s[r] == sx_want[r]
+        assert np.array_equal(got_q[r, :k], xq_want[r])
+        assert not got_q[r, k:].any()
+
+
+# ---------------------------------------------------------------- fp32 GEMM
+SG_SHAPES = [(1, 1, 1), (3, 10, 7), (64, 512, 784), (37, 96, 128), (130, 1000, 256), (512, 512, 512),
+             (2048, 1024, 128), (8, 3, 0)]
+
+
+@pytest.mark.parametrize("M,N,K", SG_SHAPES)
+@pytest.mark.parametrize("act", [-1, 0, 1])
+def test_sgemm_ep(L, M, N, K, act):
+    rng = np.random.default_rng(M + 3 * N + 7 * K)
+    A = rng.standard_normal((M, max(K, 1))).astype(np.float32)[:, :K].copy()
+    W = (rng.standard_normal((max(K, 1), N)) / np.sqrt(max(K, 1))).astype(np.float32)[:K].copy()
+    b = rng.normal(0, 0.1, N).astype(np.float32)
+    want = knx_ref.act(knx_ref.dense64(A, W, b), act)
+    C = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    dA = dev(A) if K else None
+    dW = dev(W) if K else None
+    db = dev(b)
+    hipabi.check(L.knx_hip_sgemm_ep(M, N, K, ptr(dA), K, ptr(dW), N, ptr(db), act, 0.0, ptr(C), N, hipabi.stream()))
+    assert rel_err(host(C), want) <= 1e-4
+
+
+# ---------------------------------------------------------------- rows / elementwise
+@pytest.mark.parametrize("rows,cols", [(1, 1), (7, 10), (64, 512), (300, 2048), (5, 9000)])
+def test_layernorm_softmax(L, rows, cols):
+    rng = np.random.default_rng(rows + cols)
+    x = rng.standard_normal((rows, cols)).astype(np.float32) * 3
+    g = (1 + rng.normal(0, 0.5, cols)).astype(np.float32)
+    bt = rng.normal(0, 0.5, cols).astype(np.float32)
+    dx, dg, dbt = dev(x), dev(g), dev(bt)
+    y = torch.empty_like(dx)
+    hipabi.check(L.knx_hip_layernorm(ptr(dx), ptr(y), rows, cols, ptr(dg), ptr(dbt), 1e-5, hipabi.stream()))
+    assert rel_err(host(y), knx_ref.layernorm(x, g, bt, 1e-5)) <= 1e-5
+    hipabi.check(L.knx_hip_softmax(ptr(dx), ptr(dx), rows, cols, hipabi.stream()))  # in place
+    assert rel_err(host(dx), knx_ref.softmax(x)) <= 1e-5
+
+
+@pytest.mark.parametrize("act", list(range(16)))
+def test_bias_act_all_activations(L, act):
+    rng = np.random.default_rng(act)
+    x = (rng.standard_normal((33, 70)) * 4).astype(np.float32)
+    b = rng.normal(0, 1, 70).astype(np.float32)
+    want = knx_ref.act((x + b).astype(np.float32), act, 0.2)
+    dx, db = dev(x), dev(b)
+    hipabi.check(L.knx_hip_bias_act(ptr(dx), ptr(dx), 33, 70, ptr(db), act, 0.2, hipabi.stream()))
+    got = host(dx)
+    assert np.allclose(got, want, rtol=2e-6, atol=2e-6, equal_nan=True)
+
+
+def test_binary_broadcast_and_pool(L):
+    rng = np.random.default_rng(5)
+    B, R, C = 3, 6, 8
+    for op in range(6):
+        for (ra, ca, rb, cb) in [(R, C, R, C), (R, C, 1, C), (R, C, R, 1), (1, C, R, C)]:
+            a = rng.normal(0, 1, (B * ra, ca)).astype(np.float32)
+            b = rng.normal(0, 1, (B * rb, cb)).astype(np.float32) + 2.5
+            want = np.zeros((B * R, C), np.float32)
+            knx_ref.lib().ko_binary(op, knx_ref._p(a), ra, ca, knx_ref._p(b), rb, cb, knx_ref._p(want), B, R, C)
+            y = torch.empty((B * R, C), dtype=torch.float32, device="cuda")
+            da, db = dev(a), dev(b)
+            hipabi.check(L.knx_hip_binary(op, ptr(da), ra, ca, ptr(db), rb, cb, ptr(y), B, R, C, hipabi.stream()))
+            assert np.array_equal(host(y), want)
+    x = rng.normal(0, 1, (4 * 64, 256)).astype(np.float32)
+    for t in (0, 1):
+        want = np.zeros((4, 256), np.float32)
+        knx_ref.lib().ko_global_pool(t, knx_ref._p(x), 4, 64, 256, knx_ref._p(want))
+        y = torch.empty((4, 256), dtype=torch.float32, device="cuda")
+        dx = dev(x)
+        hipabi.check(L.knx_hip_global_pool(t, ptr(dx), 4, 64, 256, ptr(y), hipabi.stream()))
+        assert np.array_equal(host(y), want)
+
+
+# ---------------------------------------------------------------- convolution
+CONV_CASES = [
+    # B, H, W, C, Co, k, stride, pad, groups, dil
+    (2, 8, 8, 3, 64, 3, 1, 1, 1, 1),
+    (2, 8, 8, 64, 64, 3, 1, 1, 1, 1),
+    (2, 16, 16, 64, 128, 3, 2, 1, 1, 1),
+    (1, 9, 7, 6, 6, 3, 1, 1, 6, 1),
+    (1, 9, 7, 6, 6, 3, 1, 1, 2, 2),
+    (3, 5, 5, 8, 12, 1, 1, 0, 1, 1),
+    (2, 11, 13, 5, 7, 2, 3, 0, 1, 1),
+]
+
+
+@pytest.mark.parametrize("case", CONV_CASES)
+def test_conv(L, case):
+    B, H, W, C, Co, k, s, p, g, dil = case
+    rng = np.random.default_rng(sum(case))
+    Ho = (H + 2 * p - dil * (k - 1) - 1) // s + 1
+    Wo = (W + 2 * p - dil * (k - 1) - 1) // s + 1
+    x = rng.standard_normal((B * H * W, C)).astype(np.float32)
+    w = (rng.standard_normal((k * k * (C // g), Co)) / np.sqrt(k * k * C / g)).astype(np.float32)
+    b = rng.normal(0, 0.1, Co).astype(np.float32)
+    op = dict(cin=C, cout=Co, k=(k, k), s=(s, s), d=(dil, dil), p=(p, p, p, p), g=g, w=w, b=b)
+    want, _ = knx_ref._conv(x, B, H, W, op, act_id=0)
+    geom = hipabi.ConvGeom(B, H, W, C, Ho, Wo, Co, k, k, s, s, dil, dil, p, p, g)
+    y = torch.empty((B * Ho * Wo, Co), dtype=torch.float32, device="cuda")
+    dx, dw, db = dev(x), dev(w), dev(b)
+    hipabi.check(L.knx_hip_conv(ctypes.byref(geom), ptr(dx), ptr(dw), ptr(db), 0, 0.0, ptr(y), hipabi.stream()))
+    assert rel_err(host(y), want) <= 1e-4
+
+
+# ---------------------------------------------------------------- attention core
+@pytest.mark.parametrize("B,H,Rq,S,dk,dv,causal", [(2, 2, 5, 5, 4, 4, 1), (2, 8, 128, 128, 64, 64, 0),
+                                                   (1, 3, 7, 9, 16, 8, 0), (3, 4, 33, 33, 32, 32, 1)])
+def test_attention_core(L, B, H, Rq, S, dk, dv, causal):
+    rng = np.random.default_rng(B + H + Rq + S)
+    Q = rng.standard_normal((B * Rq, H * dk)).astype(np.float32)
+    K = rng.standard_normal((B * S, H * dk)).astype(np.float32)
+    V = rng.standard_normal((B * S, H * dv)).astype(np.float32)
+    scale = np.float32(1.0) / np.sqrt(np.float32(dk))
+    want = np.zeros((B * Rq, H * dv), np.float32)
+    knx_ref.lib().ko_attention_core(knx_ref._p(Q), knx_ref._p(K), knx_ref._p(V), knx_ref._p(want), B, H, Rq, S, dk, dv,
+                                    float(scale), causal)
+    ctx = torch.empty((B * Rq, H * dv), dtype=torch.float32, device="cuda")
+    sc = torch.empty((B * H * Rq, S), dtype=torch.float32, device="cuda")
+    dQ, dK, dV = dev(Q), dev(K), dev(V)
+    hipabi.check(L.knx_hip_attention_core(ptr(dQ), ptr(dK), ptr(dV), ptr(ctx), ptr(sc), B, H, Rq, S, dk, dv,
+                                          float(scale), causal, hipabi.stream()))
+    assert rel_err(host(ctx), want) <= 1e-4

@@ -1,0 +1,158 @@
+""".knx forward parity on the GPU (through kernix_capi_* via the Python Model binding) against the CPU oracle.
+
+Tolerance: max|a−b| / max(1, max|ref|) ≤ 1e-4 for fp32 paths (reference test/model_test.c:127-142).
+int8 ("i8" mode) forward vs the oracle's int8 arithmetic: bit-exact when every int8 layer's input is itself bit-exact
+(chains of int8 Linear + ReLU); when an fp32 op (LayerNorm, GELU, attention) feeds the per-row int8 quantizer, a
+1-ulp difference can move rint(x/sx) across a .5 boundary (or change the row maximum) and shift an output by about
+one quantization step, so those models are held to the reference's int8 bound 1e-2 (reference test/model_test.c:651).
+int8 vs the dequantized fp32 path of the same model: the reference's int8-model bound 5e-2
+(reference test/zoo_torch_test.py:207-208).
+Full-size configurations are checked on a random subset of samples (samples are independent, so the oracle only has
+to run the subset).
+"""
+import os
+
+import numpy as np
+import pytest
+
+from kernix_amd import configs
+from kernix_amd.kernix import INT8_I8, INT8_REF, Model
+from oracle import knx_ref
+
+pytestmark = pytest.mark.gpu
+
+
+def rel_err(got, want):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    return float(np.max(np.abs(got - want)) / max(1.0, float(np.max(np.abs(want)))))
+
+
+def to_rows(m, x):
+    """model input in the runtime's channels-last row layout"""
+    x = np.asarray(x, np.float32)
+    if m.channels_first and x.ndim >= 3:
+        x = np.moveaxis(x, 1, -1)
+    return np.ascontiguousarray(x).reshape(-1, m.in_dim)
+
+
+def check(path, x, tol=1e-4, mode="ref", workspace_mb=None, subset=None):
+    m = Model(path, workspace_mb=workspace_mb)
+    if mode == "i8":
+        m.set_int8_mode(INT8_I8)
+    y = m(x).reshape(len(x), -1)
+    ref = knx_ref.parse(path)
+    idx = np.arange(len(x)) if subset is None else np.sort(np.random.default_rng(1).choice(len(x), subset, replace=False))
+    xs = to_rows(m, np.asarray(x)[idx])
+    want, _ = knx_ref.forward(ref, xs, mode=mode)
+    err = rel_err(y[idx], want)
+    m.close()
+    assert err <= tol, f"{os.path.basename(path)} {mode}: rel err {err:.3e} > {tol}"
+    return y
+
+
+# ---------------------------------------------------------------- int8 MLP (784-512-256-10)
+@pytest.mark.parametrize("batch", [1, 2, 3, 64])
+def test_int8_mlp_ref_mode(tmp_path, batch):
+    p = str(tmp_path / "mlp.knx")
+    x = configs.int8_mlp(p, batch=batch)
+    check(p, x)
+
+
+@pytest.mark.parametrize("batch", [1, 64, 1000])
+def test_int8_mlp_i8_mode_bit_exact(tmp_path, batch):
+    """int8 arithmetic end to end: quantize → i8 MFMA → dequant/bias/ReLU epilogue is bit-exact with the oracle."""
+    p = str(tmp_path / "mlp.knx")
+    x = configs.int8_mlp(p, batch=batch)
+    y = check(p, x, tol=0.0, mode="i8")
+    y_ref = Model(p)(x)
+    assert rel_err(y, y_ref) <= 5e-2  # int8 vs dequantized fp32
+
+
+# ---------------------------------------------------------------- fp32 MLP
+def test_fp32_mlp_small(tmp_path):
+    p = str(tmp_path / "f.knx")
+    x = configs.fp32_mlp(p, batch=300, dims=(256, 320, 256, 100))
+    check(p, x)
+
+
+def test_fp32_mlp_full_size_subset(tmp_path):
+    p = str(tmp_path / "f.knx")
+    x = configs.fp32_mlp(p, batch=8192)
+    check(p, x, workspace_mb=0, subset=48)
+
+
+# ---------------------------------------------------------------- CNN
+def test_cnn_small(tmp_path):
+    p = str(tmp_path / "c.knx")
+    x = configs.cnn(p, batch=8, hw=16, widths=(16, 16, 32, 64))
+    check(p, x)
+
+
+def test_cnn_full_size_subset(tmp_path):
+    p = str(tmp_path / "c.knx")
+    x = configs.cnn(p, batch=256)
+    check(p, x, workspace_mb=0, subset=8)
+
+
+# ---------------------------------------------------------------- Transformer
+def test_transformer_small_ref_and_i8(tmp_path):
+    p = str(tmp_path / "t.knx")
+    x = configs.transformer(p, batch=4, seq=32, d=64, heads=4, ffn=128, layers=2)
+    y_ref = check(p, x)
+    y_i8 = check(p, x, mode="i8", tol=1e-2)
+    assert rel_err(y_i8, y_ref) <= 5e-2
+
+
+def test_transformer_full_size_subset(tmp_path):
+    p = str(tmp_path / "t.knx")
+    x = configs.transformer(p, batch=64)
+    check(p, x, workspace_mb=0, subset=4)
+    check(p, x, workspace_mb=0, subset=4, mode="i8", tol=1e-2)
+
+
+# ---------------------------------------------------------------- runtime behaviour (reference test/model_test.c)
+def test_chunking_reuse_and_trim(tmp_path):
+    """chunked == unchunked (reference test/model_test.c:296-360)"""
+    p = str(tmp_path / "t.knx")
+    x = configs.transformer(p, batch=10, seq=16, d=32, heads=2, ffn=64, layers=1)
+    m = Model(p, workspace_mb=0)
+    want = m(x)
+    per, fixed, batch = m.ws_info()
+    assert batch == 10 * 16
+    for chunk in (1, 3, 9):
+        from kernix_amd import kernix as kx
+        kx._lib.kernix_capi_set_workspace_limit(m._h, (fixed + per * chunk) * 4)
+        got = m(x)
+        assert m.ws_info()[2] == chunk * 16
+        assert rel_err(got, want) <= 1e-5
+    got3 = m(x[:3])  # after chunks of 3 (3,3,3,1): same buffers at the full chunk size
+    assert rel_err(got3, want[:3]) <= 1e-5
+    m.trim()
+    assert m.ws_info()[2] == -1
+    assert rel_err(m(x), want) <= 1e-5
+    m.close()
+
+
+def test_zero_rows_bad_input_and_own_output(tmp_path):
+    p = str(tmp_path / "mlp.knx")
+    x = configs.int8_mlp(p, batch=3)
+    m = Model(p)
+    with pytest.raises(ValueError):
+        m(np.zeros((2, 783), np.float32))
+    y = m(x)
+    assert y.shape == (3, 10)
+    m.close()
+
+
+def test_workspace_identical_across_batch_sizes(tmp_path):
+    """batch 37 after 4096 after 1 gives the same result (buffer reallocation, reference test/model_test.c:148)"""
+    p = str(tmp_path / "f.knx")
+    x = configs.fp32_mlp(p, batch=4096, dims=(64, 128, 96, 10))
+    m = Model(p)
+    a = m(x[:37]).copy()
+    m(x)
+    m(x[:1])
+    b = m(x[:37])
+    assert np.array_equal(a, b)
+    m.close()
