@@ -1,0 +1,225 @@
+#!/usr/bin/env python3
+"""Benchmark of the KERNIX forward hot path on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--no-cpu] [--no-forward]
+
+Headline (`value`): int8 GEMM Y = relu(((float)(A·Wᵀ)·sa[m])·sw[n] + bias[n]) at M = K = N = 4096 with int32
+accumulation, inputs resident in HBM, through the C ABI (knx_hip_i8gemm), in TOPS (1 MAC = 2 ops); K timed launches
+bracketed by device synchronization, kernel time from HIP events on the launch stream.
+Also reported: the same GEMM at M ∈ {1, 16, 256} (HBM-bound) and the .knx forward samples/sec of the int8 MLP,
+fp32 MLP, CNN and int8-weight Transformer workloads (device-resident and end to end through kernix_capi_forward),
+and the CPU oracle (plain C, the reference's int8 arithmetic) timed on this machine's host cores.
+One JSON line is printed on stdout.
+"""
+import argparse
+import json
+import os
+import sys
+import tempfile
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_I8_TOPS = 5000.0      # MI355X dense int8 MFMA
+PEAK_F32_TFLOPS = 157.3    # MI355X fp32 MFMA
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+METRIC = "int8 GEMM TOPS + .knx forward samples/sec on 1 MI355X, % of roofline"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def time_launches(fn, steps, warmup):
+    """(avg ms per launch from HIP events on the current stream, wall ms per launch)"""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    return start.elapsed_time(end) / steps, wall
+
+
+def i8gemm_bench(M, steps, warmup, N=4096, K=4096):
+    import numpy as np
+    import torch
+
+    from kernix_amd import configs, hipabi
+
+    L = hipabi.lib()
+    hipabi.check(L.knx_hip_init())
+    A, W, sa, sw, bias = configs.i8gemm_inputs(M, N, K)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
+    dA, dW, dsa, dsw, db = dev(A), dev(W), dev(sa), dev(sw), dev(bias)
+    Y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    P = hipabi.ptr
+    args = (M, N, K, P(dA), K, P(dsa), P(dW), K, P(dsw), P(db), 0, 0.0, 0, P(Y), N, None, 0, hipabi.stream())
+
+    def run():
+        hipabi.check(L.knx_hip_i8gemm(*args))
+
+    ms, wall = time_launches(run, steps, warmup)
+    ops, algo_bytes = configs.i8gemm_work(M, N, K)
+    return dict(M=M, N=N, K=K, ms=ms, wall_ms=wall, tops=ops / (ms * 1e-3) / 1e12, gbs=algo_bytes / (ms * 1e-3) / 1e9,
+                algo_bytes=algo_bytes, ops=ops, A=A, W=W, sa=sa, sw=sw, bias=bias, Y=Y)
+
+
+def cpu_baseline(g, threads, target_s=10.0):
+    """Oracle int8 GEMM (plain C, the reference's scalar int8 arithmetic) on rows of the same workload."""
+    import numpy as np
+
+    from oracle import knx_ref
+
+    A, W, sa, sw, bias = g["A"], g["W"], g["sa"], g["sw"], g["bias"]
+    N, K = W.shape
+    rows = min(64, A.shape[0])
+    t0 = time.perf_counter()
+    knx_ref.i8gemm(A[:rows], W, sa[:rows], sw, bias, act_id=0, threads=threads)
+    dt = time.perf_counter() - t0
+    rate = rows / max(dt, 1e-6)                      # rows per second
+    rows = int(min(A.shape[0], max(rows, rate * target_s)))
+    reps, total, y = 0, 0.0, None
+    while reps == 0 or (total < target_s * 0.5 and reps < 5):
+        t0 = time.perf_counter()
+        y, _ = knx_ref.i8gemm(A[:rows], W, sa[:rows], sw, bias, act_id=0, threads=threads)
+        total += time.perf_counter() - t0
+        reps += 1
+    sec = total / reps
+    ops = 2.0 * rows * N * K
+    got = g["Y"][:rows].cpu().numpy()
+    return dict(tops=ops / sec / 1e12, seconds=sec, rows=rows, reps=reps, bit_exact=bool(np.array_equal(got, y)))
+
+
+def forward_bench(name, make, flops, steps, warmup, mode="ref", roof="f32"):
+    import numpy as np
+    import torch
+
+    from kernix_amd.kernix import INT8_I8, Model
+
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, name + ".knx")
+        x = make(path)
+        m = Model(path, workspace_mb=0)
+        if mode == "i8":
+            m.set_int8_mode(INT8_I8)
+        xr = x
+        if m.channels_first and x.ndim >= 3:
+            xr = np.moveaxis(x, 1, -1)
+        xr = np.ascontiguousarray(xr, np.float32).reshape(-1, m.in_dim)
+        B = xr.shape[0] // m.seq_len
+        dx = torch.from_numpy(xr).cuda()
+        dy = torch.empty((B, m.out_dim), dtype=torch.float32, device="cuda")
+        # a dedicated stream: the library runs the forward on the handle it is given (NULL would mean the model's
+        # own stream), and the timing events are recorded on the same one
+        stream = torch.cuda.Stream()
+        st = stream.cuda_stream
+
+        def run():
+            m.forward_device(dx.data_ptr(), xr.shape[0], dy.data_ptr(), st)
+
+        with torch.cuda.stream(stream):
+            ms, _ = time_launches(run, steps, warmup)
+        m(x)  # end to end through kernix_capi_forward (host buffers, PCIe included)
+        t0 = time.perf_counter()
+        n_e2e = max(2, steps // 4)
+        for _ in range(n_e2e):
+            m(x)
+        e2e = (time.perf_counter() - t0) * 1e3 / n_e2e
+        m.close()
+    tf = flops / (ms * 1e-3) / 1e12
+    peak = PEAK_F32_TFLOPS if roof == "f32" else PEAK_I8_TOPS
+    return dict(batch=B, ms=round(ms, 4), samples_per_s=round(B / (ms * 1e-3), 1),
+                e2e_ms=round(e2e, 3), e2e_samples_per_s=round(B / (e2e * 1e-3), 1),
+                tflops=round(tf, 2), roofline_frac=round(tf / peak, 4), mode=mode)
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-forward", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one MI355X: multi-GPU runs are not part of this build "
+              "(the forward shards by rows with no exchange; see the design notes)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from kernix_amd import configs
+
+    assert torch.cuda.is_available(), "bench.py needs the MI355X"
+    log(f"device: {torch.cuda.get_device_name(0)}")
+    g = i8gemm_bench(4096, args.steps, args.warmup)
+    log(f"i8gemm M=4096: {g['ms'] * 1e3:.1f} us  {g['tops']:.1f} TOPS")
+    small = {}
+    for M in (1, 16, 256):
+        r = i8gemm_bench(M, max(args.steps, 20), args.warmup)
+        small[str(M)] = dict(us=round(r["ms"] * 1e3, 2), tops=round(r["tops"], 2), gbs=round(r["gbs"], 1),
+                             hbm_frac=round(r["gbs"] / PEAK_HBM_GBS, 4))
+        log(f"i8gemm M={M}: {r['ms'] * 1e3:.2f} us  {r['gbs']:.0f} GB/s algorithmic")
+
+    out = {
+        "metric": METRIC,
+        "value": round(g["tops"], 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(g["ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": "int8 GEMM relu(((float)(A_i8·W_i8^T)·sa[m])·sw[n] + bias[n]), int32 accumulate",
+                   "M": 4096, "N": 4096, "K": 4096},
+        "roofline": {"bound": "mfma", "achieved": round(g["tops"], 2), "peak": PEAK_I8_TOPS, "unit": "TOP/s",
+                     "frac": round(g["tops"] / PEAK_I8_TOPS, 4), "traffic": None},
+    }
+    if not args.no_cpu:
+        c8 = cpu_baseline(g, 8)
+        out["cpu_baseline"] = {"value": round(c8["tops"], 4), "unit": "TOPS", "cores": 8, "kind": "port",
+                               "sample": f"oracle int8 GEMM (plain C, -O3), rows 0..{c8['rows'] - 1} of the "
+                                         f"M=4096 workload ({c8['rows']}x4096x4096), mean of {c8['reps']}",
+                               "gpu_rows_bit_exact": c8["bit_exact"]}
+        log(f"cpu 8 threads: {c8['tops'] * 1e3:.1f} GOPS, GPU rows bit-exact: {c8['bit_exact']}")
+        ncpu = len(os.sched_getaffinity(0))
+        if ncpu != 8:
+            cn = cpu_baseline(g, ncpu, target_s=5.0)
+            out["cpu_baseline_all_cores"] = {"value": round(cn["tops"], 4), "unit": "TOPS", "cores": ncpu}
+    out["i8gemm_small_m"] = small
+    if not args.no_forward:
+        fw = {}
+        st = max(5, args.steps // 5)
+        fw["int8_mlp_784_512_256_10_b64"] = forward_bench(
+            "mlp", lambda p: configs.int8_mlp(p, batch=64), configs.mlp_flops(64, (784, 512, 256, 10)), st, args.warmup)
+        fw["int8_mlp_784_512_256_10_b64_i8"] = forward_bench(
+            "mlp", lambda p: configs.int8_mlp(p, batch=64), configs.mlp_flops(64, (784, 512, 256, 10)), st, args.warmup,
+            mode="i8", roof="i8")
+        fw["fp32_mlp_4096_4096_4096_1000_b8192"] = forward_bench(
+            "f32", lambda p: configs.fp32_mlp(p), configs.mlp_flops(8192, (4096, 4096, 4096, 1000)), st, args.warmup)
+        fw["cnn_b256"] = forward_bench("cnn", lambda p: configs.cnn(p), configs.cnn_flops(), st, args.warmup)
+        fw["transformer_4l_d512_b64"] = forward_bench(
+            "tr", lambda p: configs.transformer(p), configs.transformer_flops(), st, args.warmup)
+        fw["transformer_4l_d512_b64_i8"] = forward_bench(
+            "tr", lambda p: configs.transformer(p), configs.transformer_flops(), st, args.warmup, mode="i8")
+        for k, v in fw.items():
+            log(f"forward {k}: {v['ms']:.3f} ms  {v['samples_per_s']:.0f} samples/s  {v['tflops']:.1f} TFLOP/s")
+        out["forward"] = fw
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

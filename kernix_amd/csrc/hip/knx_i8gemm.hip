@@ -10,6 +10,10 @@
 //   16-byte chunks XOR-swizzled per row so the MFMA fragment reads are bank-conflict free) → v4i32 fragments →
 //   32×32×32 i8 MFMAs into int32 accumulators → epilogue straight from the accumulators.
 //   Both operands are K-contiguous (A: M×K activations, W: N×K weights), so no transposes are needed anywhere.
+#include <stdlib.h>
+
+#include <string>
+
 #include "knx_common.hpp"
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -215,6 +219,349 @@ __global__ void __launch_bounds__(WM * WN * 64) i8gemm_tile(I8Args p)
     }
 }
 
+// ---------------------------------------------------------------- pipelined tile kernel
+// Same tile/fragment/epilogue structure as i8gemm_tile, but operands move HBM → LDS directly with
+// global_load_lds_dwordx4 (no VGPR staging, no ds_write), through a STAGES-deep LDS ring so that STAGES−1 k-tiles are
+// in flight while one is multiplied.  Each load instruction fills 1 KB of LDS = 16 rows × 64 bytes; lane l fetches
+// the global 16-byte chunk (l & 3) ^ swz(row), which realizes the swizzled layout with fully coalesced loads.
+// Rows past M (or N) are clamped to the last row: they only feed output rows/columns that are never stored.
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+typedef __attribute__((address_space(1))) const void* gbl_ptr_t;
+
+// s_waitcnt vmcnt(n) lgkmcnt(0) (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] = 7 | lgkmcnt[11:8] | vmcnt[5:4] << 14):
+// at most n vector-memory ops (LDS-DMA loads) of this wave outstanding and all of its LDS accesses retired.
+#define KNX_WAIT_VM_LDS(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (0 << 8) | ((((n) >> 4) & 3) << 14))
+
+// s_waitcnt lgkmcnt(0): all LDS accesses of this wave retired (vmcnt left unconstrained at 63).
+#define KNX_WAIT_LDS() __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14))
+#define KERNIX_ACT_RELU_ID 0
+
+// Writes the 16 staged rows [mt0, mt0+16) of a tile: 4 consecutive columns per lane, one 16-byte store per row.
+// ACT ≥ −1 is a compile-time activation for the common case (vector path, no accumulation); −2 is the general path.
+template <int ACT>
+__device__ __forceinline__ void store_rows(const I8Args& p, const int* stg, const float* row_scale, int mt0, int m0, int rq,
+                                           int rpi, int srow, int cq, int nb, const float* swv, const float* bv,
+                                           bool vec = true)
+{
+    for (int rr = rq; rr < 16; rr += rpi) {
+        const int mt = mt0 + rr, m = m0 + mt;
+        if (m >= p.M) continue;
+        const v4i a = *reinterpret_cast<const v4i*>(&stg[rr * srow + cq]);
+        if (ACT >= -1) {
+            const float sx = row_scale[mt];
+            float r[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                float v = (float)a[q] * sx;  // ((float)acc · sx) · scale + bias, each step rounded
+                v = v * swv[q];
+                if (p.bias) v = v + bv[q];   // no bias: no addition (x + 0 would turn −0 into +0)
+                r[q] = ACT == 0 ? (v >= 0.0f ? v : 0.0f) : v;
+            }
+            // streaming store: the output is written once and never re-read by this kernel
+            typedef float v4f_t __attribute__((ext_vector_type(4)));
+            __builtin_nontemporal_store(v4f_t{r[0], r[1], r[2], r[3]}, reinterpret_cast<v4f_t*>(p.Y + (size_t)m * p.ldy + nb));
+        } else if (vec) {
+            if (p.acc) *reinterpret_cast<v4i*>(p.acc + (size_t)m * p.ldacc + nb) = a;
+            if (p.Y) {
+                const float sx = row_scale[mt];
+                float* y = p.Y + (size_t)m * p.ldy + nb;
+                float4 o = p.accumulate ? *reinterpret_cast<const float4*>(y) : make_float4(0.f, 0.f, 0.f, 0.f);
+                float r[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    float v = (float)a[q] * sx;
+                    v = v * swv[q];
+                    if (p.bias) v = v + bv[q];
+                    if (p.accumulate) v = (&o.x)[q] + v;
+                    r[q] = knx_act(v, p.act, p.alpha);
+                }
+                *reinterpret_cast<float4*>(y) = make_float4(r[0], r[1], r[2], r[3]);
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                if (nb + q < p.N) i8_epilogue(p, m, nb + q, a[q]);
+        }
+    }
+}
+
+// Workgroup barrier without a memory fence.  A fence (e.g. __syncthreads) would wait for every outstanding LDS-DMA
+// load, which empties the prefetch ring; the caller instead waits precisely with KNX_WAIT_VM_LDS.  The empty asm
+// statements keep the compiler from moving any memory access across the barrier.
+__device__ __forceinline__ void knx_barrier_nofence()
+{
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// Tile order: consecutive workgroups go to consecutive XCDs (8 on MI355X); when the tile grid splits evenly, each
+// XCD gets one contiguous (tiles_m/2) × (tiles_n/4) block so the A and W rows it reads stay in its own L2.
+__device__ __forceinline__ void tile_of(int t, int tiles_m, int tiles_n, int& tm, int& tn)
+{
+    if ((tiles_m & 1) == 0 && (tiles_n & 3) == 0 && tiles_m * tiles_n >= 64) {
+        const int x = t & 7, j = t >> 3;
+        const int bm = tiles_m >> 1, bn = tiles_n >> 2;
+        tm = (x >> 2) * bm + j / bn;
+        tn = (x & 3) * bn + j % bn;
+    } else {
+        tm = t / tiles_n;
+        tn = t % tiles_n;
+    }
+}
+
+template <int BM, int BN, int WM, int WN, int STAGES>
+__global__ void __launch_bounds__(WM * WN * 64) i8gemm_pipe(I8Args p)
+{
+    constexpr int NW = WM * WN;
+    constexpr int TM = BM / WM, TN = BN / WN;
+    constexpr int FM = TM / 32, FN = TN / 32;
+    constexpr int ROWS = BM + BN;
+    constexpr int STAGE = ROWS * 64;           // bytes per k-tile
+    constexpr int SLOTS = ROWS / 16 / NW;      // 1-KB load instructions per wave per k-tile
+    static_assert(ROWS % (16 * NW) == 0, "load split");
+    static_assert(STAGES >= 2 && STAGES <= 5 && (STAGES - 2) * SLOTS <= 63, "vmcnt range");
+    __shared__ __attribute__((aligned(16))) int8_t lds[STAGES * STAGE];
+    __shared__ float row_scale[BM]; // sa of the tile's rows, staged once so the epilogue never waits on HBM per row
+
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+    int tm, tn;
+    tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+
+    // per-lane epilogue constants (this lane's 4 output columns), loaded now so their latency hides under the K loop
+    constexpr int LPR_ = (BN / WN) / 4;
+    const int nb_ = n0 + wn * (BN / WN) + (lane % LPR_) * 4;
+    float swv[4], bv[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const bool ok = nb_ + q < p.N;
+        swv[q] = (ok && p.Y) ? p.sw[nb_ + q] : 0.0f;
+        bv[q] = (ok && p.bias) ? p.bias[nb_ + q] : 0.0f;
+    }
+
+    // per slot: global row pointer (with this lane's swizzled chunk) and the LDS offset of the wave's 1-KB block
+    const int8_t* gsrc[SLOTS];
+#pragma unroll
+    for (int i = 0; i < SLOTS; ++i) {
+        const int row = (i * NW + wave) * 16 + (lane >> 2);
+        const int chunk = (lane & 3) ^ swz(row);
+        if (row < BM) {
+            const int gm = min(m0 + row, p.M - 1);
+            gsrc[i] = p.A + (size_t)gm * p.lda + chunk * 16;
+        } else {
+            const int gn = min(n0 + row - BM, p.N - 1);
+            gsrc[i] = p.W + (size_t)gn * p.ldw + chunk * 16;
+        }
+    }
+    auto issue = [&](int kt) {
+        int8_t* stage = lds + (kt % STAGES) * STAGE;
+#pragma unroll
+        for (int i = 0; i < SLOTS; ++i)
+            __builtin_amdgcn_global_load_lds((gbl_ptr_t)(gsrc[i] + (size_t)kt * 64), (lds_ptr_t)(stage + (i * NW + wave) * 1024),
+                                             16, 0, 0);
+    };
+
+    const int rl = lane & 31, g = lane >> 5;
+    int aoff[FM][2], boff[FN][2];
+#pragma unroll
+    for (int fi = 0; fi < FM; ++fi) {
+        const int row = wm * TM + fi * 32 + rl;
+#pragma unroll
+        for (int s = 0; s < 2; ++s) aoff[fi][s] = row * 64 + (((2 * s + g) ^ swz(row)) << 4);
+    }
+#pragma unroll
+    for (int fj = 0; fj < FN; ++fj) {
+        const int row = BM + wn * TN + fj * 32 + rl;
+#pragma unroll
+        for (int s = 0; s < 2; ++s) boff[fj][s] = row * 64 + (((2 * s + g) ^ swz(row)) << 4);
+    }
+
+    v16i acc[FM][FN];
+#pragma unroll
+    for (int fi = 0; fi < FM; ++fi)
+#pragma unroll
+        for (int fj = 0; fj < FN; ++fj)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[fi][fj][e] = 0;
+
+    const int nk = p.K / 64;
+    // this thread's row scale: loaded before the first k-tiles (vmcnt retires in order, so it is never waited for
+    // separately), kept in a register and staged to LDS for the epilogue
+    static_assert(BM <= NW * 64, "one row scale per thread");
+    const float my_sa = (t < BM && p.Y && m0 + t < p.M) ? p.sa[m0 + t] : 0.0f;
+#pragma unroll
+    for (int s = 0; s < STAGES - 1; ++s)
+        if (s < nk) issue(s);
+
+    // Before the barrier each wave waits until its loads of tile kt have landed (at most min(STAGES-2, nk-1-kt)
+    // younger tiles may stay in flight) and until its own LDS reads have retired.  After the barrier every wave's part
+    // of tile kt is in LDS and no wave still reads the stage that issue() refills: that stage last held tile
+    // kt−1 (read before the previous barrier) and is the one the fragments of the previous half came from, whose
+    // reads the lgkmcnt(0) of every wave retired.
+    auto arrive = [&](int kt) {
+        const int younger = min(STAGES - 2, nk - 1 - kt);
+        if (younger >= 3) KNX_WAIT_VM_LDS(3 * SLOTS);
+        else if (younger == 2) KNX_WAIT_VM_LDS(2 * SLOTS);
+        else if (younger == 1) KNX_WAIT_VM_LDS(SLOTS);
+        else KNX_WAIT_VM_LDS(0);
+        knx_barrier_nofence();
+        if (kt + STAGES - 1 < nk) issue(kt + STAGES - 1);
+    };
+    auto frags = [&](int kt, int s, v4i* af, v4i* bf) {
+        const int8_t* cur = lds + (kt % STAGES) * STAGE;
+#pragma unroll
+        for (int fi = 0; fi < FM; ++fi) af[fi] = *(const v4i*)(cur + aoff[fi][s]);
+#pragma unroll
+        for (int fj = 0; fj < FN; ++fj) bf[fj] = *(const v4i*)(cur + boff[fj][s]);
+    };
+    auto mfmas = [&](const v4i* af, const v4i* bf) {
+#pragma unroll
+        for (int fi = 0; fi < FM; ++fi)
+#pragma unroll
+            for (int fj = 0; fj < FN; ++fj)
+                acc[fi][fj] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[fi], bf[fj], acc[fi][fj], 0, 0, 0);
+    };
+
+    // Software pipeline over half k-tiles (32 bytes of k each): the fragments of the next half are read from LDS
+    // while the MFMAs of the current half run.
+    v4i a0[FM], b0[FN], a1[FM], b1[FN];
+    if (nk > 0) {
+        arrive(0);
+        frags(0, 0, a0, b0);
+    }
+    for (int kt = 0; kt < nk; ++kt) {
+        frags(kt, 1, a1, b1);
+        mfmas(a0, b0);
+        if (kt + 1 < nk) {
+            arrive(kt + 1);
+            frags(kt + 1, 0, a0, b0);
+        }
+        mfmas(a1, b1);
+    }
+
+    // Epilogue: each wave stages 16 rows × TN of its accumulators at a time in its own LDS region (row stride TN+4
+    // ints: the two half-waves land on different banks); every lane then reads 4 consecutive columns and writes them
+    // with one 16-byte store.  The regions are private to the wave, so after one workgroup barrier (nobody reads the
+    // ring any more) only the wave's own LDS order matters: no barrier — and so no wait for the stores — per round.
+    constexpr int SROW = TN + 4;
+    constexpr int LPR = TN / 4;
+    constexpr int RPI = 64 / LPR;
+    static_assert(NW * 16 * SROW * 4 <= STAGES * STAGE, "staging fits in the ring");
+    static_assert(LPR == LPR_, "epilogue lane split");
+    int* stg = reinterpret_cast<int*>(lds) + wave * 16 * SROW;
+    const int cq = (lane % LPR) * 4, rq = lane / LPR;
+    const int nb = nb_;
+    const bool vec = nb + 3 < p.N && (p.ldy & 3) == 0 && ((uintptr_t)p.Y & 15) == 0 && (p.ldacc & 3) == 0 &&
+                     ((uintptr_t)p.acc & 15) == 0;
+    if (t < BM) row_scale[t] = my_sa;
+    KNX_WAIT_LDS();
+    knx_barrier_nofence();
+#pragma unroll
+    for (int fi = 0; fi < FM; ++fi) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int fj = 0; fj < FN; ++fj)
+#pragma unroll
+                for (int e = 8 * h; e < 8 * h + 8; ++e)
+                    stg[(8 * ((e >> 2) - 2 * h) + 4 * g + (e & 3)) * SROW + fj * 32 + rl] = acc[fi][fj][e];
+            KNX_WAIT_LDS();
+            asm volatile("" ::: "memory");
+            const int mt0 = wm * TM + fi * 32 + 16 * h;
+            const bool fast = vec && p.Y && !p.acc && !p.accumulate;  // plain Y store (no raw accumulators requested)
+            if (fast && p.act == KERNIX_ACT_RELU_ID)
+                store_rows<0>(p, stg, row_scale, mt0, m0, rq, RPI, SROW, cq, nb, swv, bv);
+            else if (fast && p.act == -1)
+                store_rows<-1>(p, stg, row_scale, mt0, m0, rq, RPI, SROW, cq, nb, swv, bv);
+            else
+                store_rows<-2>(p, stg, row_scale, mt0, m0, rq, RPI, SROW, cq, nb, swv, bv, vec);
+            asm volatile("" ::: "memory");
+        }
+    }
+}
+
+template <int BM, int BN, int WM, int WN, int STAGES>
+int launch_pipe(I8Args p, hipStream_t s, const char* name)
+{
+    p.tiles_m = (p.M + BM - 1) / BM;
+    p.tiles_n = (p.N + BN - 1) / BN;
+    const unsigned grid = (unsigned)p.tiles_m * (unsigned)p.tiles_n;
+    hipLaunchKernelGGL((i8gemm_pipe<BM, BN, WM, WN, STAGES>), dim3(grid), dim3(WM * WN * 64), 0, s, p);
+    return knx::check_launch(name);
+}
+
+// ---------------------------------------------------------------- skinny kernel (M ≤ 64)
+// Bandwidth-bound shapes (a few activation rows against a whole weight matrix): every workgroup owns 16 output
+// channels (16 W rows) and its KS waves split K; each wave streams its W slice HBM → VGPR with all loads issued up
+// front, multiplies on v_mfma_i32_16x16x64_i8 (16 rows of A per block, up to 4 blocks), and the KS partial int32
+// tiles are summed exactly through LDS before the same epilogue as the tile kernels.
+// 16×16×64 operand layout: lane l holds row (l & 15), k-chunk (l >> 4) of 16 bytes; A and W use the same chunk,
+// so any k order inside the instruction is consistent.  Result: lane l holds column (l & 15), rows 4·(l >> 4) + e.
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+
+template <int MB, int KS, int KT>  // MB row blocks of 16, KS waves, KT 64-byte k-steps per wave per pass
+__global__ void __launch_bounds__(KS * 64) i8gemm_skinny(I8Args p)
+{
+    __shared__ int part[KS][MB][16][17];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int n0 = blockIdx.x * 16;
+    const int r = lane & 15, c = lane >> 4;
+    const int gn = min(n0 + r, p.N - 1);
+    const int8_t* wrow = p.W + (size_t)gn * p.ldw + c * 16;
+    const int8_t* arow[MB];
+    bool aok[MB];
+#pragma unroll
+    for (int b = 0; b < MB; ++b) {
+        const int gm = b * 16 + r;
+        aok[b] = gm < p.M;
+        arow[b] = p.A + (size_t)(aok[b] ? gm : 0) * p.lda + c * 16;
+    }
+    v4i acc[MB];
+#pragma unroll
+    for (int b = 0; b < MB; ++b) acc[b] = v4i{0, 0, 0, 0};
+    const int nk = p.K / 64;
+    // wave w takes k-steps w, w+KS, w+2·KS, … ; KT of them per pass, loads issued before the multiplies
+    for (int k0 = wave; k0 < nk; k0 += KS * KT) {
+        v4i wf[KT], af[KT][MB];
+#pragma unroll
+        for (int j = 0; j < KT; ++j) {
+            const int kk = k0 + j * KS;
+            wf[j] = kk < nk ? *(const v4i*)(wrow + (size_t)kk * 64) : v4i{0, 0, 0, 0};
+#pragma unroll
+            for (int b = 0; b < MB; ++b) af[j][b] = (kk < nk && aok[b]) ? *(const v4i*)(arow[b] + (size_t)kk * 64) : v4i{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int j = 0; j < KT; ++j)
+#pragma unroll
+            for (int b = 0; b < MB; ++b) acc[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[j][b], wf[j], acc[b], 0, 0, 0);
+    }
+#pragma unroll
+    for (int b = 0; b < MB; ++b)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) part[wave][b][4 * c + e][r] = acc[b][e];
+    __syncthreads();
+    // KS·64 threads finish MB·16 rows × 16 columns
+    for (int i = threadIdx.x; i < MB * 256; i += KS * 64) {
+        const int b = i >> 8, row = (i >> 4) & 15, col = i & 15;
+        const int m = b * 16 + row, n = n0 + col;
+        if (m >= p.M || n >= p.N) continue;
+        int s = 0;
+#pragma unroll
+        for (int w = 0; w < KS; ++w) s += part[w][b][row][col];
+        i8_epilogue(p, m, n, s);
+    }
+}
+
+template <int MB>
+int launch_skinny(I8Args p, hipStream_t s, const char* name)
+{
+    const unsigned grid = (unsigned)((p.N + 15) / 16);
+    hipLaunchKernelGGL((i8gemm_skinny<MB, 8, 4>), dim3(grid), dim3(8 * 64), 0, s, p);
+    return knx::check_launch(name);
+}
+
 template <int BM, int BN, int WM, int WN>
 int launch_tile(I8Args p, hipStream_t s, const char* name)
 {
@@ -317,11 +664,27 @@ extern "C" int knx_hip_i8gemm(int M, int N, int K, const int8_t* A, int lda, con
         // empty inner dimension: the accumulators are all zero; run the smallest tile (loop body never executes)
         return launch_tile<64, 64, 1, 1>(p, s, name);
     }
+    // KNX_I8_KERNEL forces one variant (tuning and tests); otherwise the shape picks it
+    const char* force = getenv("KNX_I8_KERNEL");
+    if (force != nullptr && *force) {
+        const std::string f(force);
+        if (f == "tile256") return launch_tile<256, 256, 2, 2>(p, s, name);
+        if (f == "tile64") return launch_tile<64, 64, 1, 1>(p, s, name);
+        if (f == "pipe256") return launch_pipe<256, 256, 2, 2, 4>(p, s, name);
+        if (f == "pipe256w8") return launch_pipe<256, 256, 2, 4, 4>(p, s, name);
+        if (f == "pipe256s3") return launch_pipe<256, 256, 2, 2, 3>(p, s, name);
+        if (f == "pipe128") return launch_pipe<128, 128, 2, 2, 4>(p, s, name);
+        if (f == "pipe64") return launch_pipe<64, 64, 2, 2, 4>(p, s, name);
+        if (f == "skinny" && M <= 64) return M <= 16 ? launch_skinny<1>(p, s, name) : M <= 32 ? launch_skinny<2>(p, s, name) : launch_skinny<4>(p, s, name);
+    }
+    if (M <= 16) return launch_skinny<1>(p, s, name);
+    if (M <= 32) return launch_skinny<2>(p, s, name);
+    if (M <= 64) return launch_skinny<4>(p, s, name);
     const long tiles256 = (long)((M + 255) / 256) * ((N + 255) / 256);
-    if (tiles256 >= knx::num_cus()) return launch_tile<256, 256, 2, 2>(p, s, name);
+    if (tiles256 >= knx::num_cus()) return launch_pipe<256, 256, 2, 2, 4>(p, s, name);
     const long tiles128 = (long)((M + 127) / 128) * ((N + 127) / 128);
-    if (tiles128 >= knx::num_cus()) return launch_tile<128, 128, 2, 2>(p, s, name);
-    return launch_tile<64, 64, 1, 1>(p, s, name);
+    if (tiles128 >= knx::num_cus()) return launch_pipe<128, 128, 2, 2, 4>(p, s, name);
+    return launch_pipe<64, 64, 2, 2, 4>(p, s, name);
 }
 
 extern "C" int knx_hip_dequant(const int8_t* q, int ldq, const float* scale, int K, int N, float* dst, void* stream)

@@ -1,6 +1,7 @@
-"""ctypes bindings of the C ABI declared in include/knx_hip.h, for the kernel-level tests and the benchmark.
+"""ctypes bindings of the kernel-level C ABI (include/knx_hip.h) of libkernix.so.
 
-Device buffers come from torch (plumbing only); every computation goes through libkernix.so.
+Used by the benchmark and the kernel tests to call the gfx950 kernels on device buffers that the caller owns (for
+example torch tensors: pass ptr(tensor) and stream()).  Loading fails with OSError when the library is missing.
 """
 import ctypes
 import os

@@ -9,8 +9,8 @@ import numpy as np
 import pytest
 
 from oracle import knx_ref
-from tests import hipabi
-from tests.hipabi import ptr
+from kernix_amd import hipabi
+from kernix_amd.hipabi import ptr
 
 pytestmark = pytest.mark.gpu
 
