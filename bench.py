@@ -99,6 +99,17 @@ def cpu_baseline(g, threads, target_s=10.0):
     return dict(tops=ops / sec / 1e12, seconds=sec, rows=rows, reps=reps, bit_exact=bool(np.array_equal(got, y)))
 
 
+def measured_traffic():
+    """HBM bytes per launch of the M=N=K=4096 GEMM from the committed rocprofv3 counter summary (FETCH_SIZE and
+    WRITE_SIZE per dispatch, each scaled by the same counter on a kernel of known traffic), or None without it."""
+    path = os.path.join(ROOT, "profiles", "i8gemm_4096_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f)["traffic_bytes"]
+    except (OSError, ValueError, KeyError):
+        return None
+
+
 def forward_bench(name, make, flops, steps, warmup, mode="ref", roof="f32"):
     import numpy as np
     import torch
@@ -149,6 +160,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-forward", action="store_true")
+    ap.add_argument("--no-small", action="store_true", help="skip the small-M GEMM lines")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="also run a 256 MiB read (sum) and a 256 MiB copy: reference kernels of known HBM traffic for "
+                         "scaling the FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: multi-GPU runs are not part of this build "
@@ -163,8 +178,17 @@ def main():
     log(f"device: {torch.cuda.get_device_name(0)}")
     g = i8gemm_bench(4096, args.steps, args.warmup)
     log(f"i8gemm M=4096: {g['ms'] * 1e3:.1f} us  {g['tops']:.1f} TOPS")
+    if args.calibrate:
+        n = 256 << 20
+        src = torch.ones(n // 4, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            src.sum()
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"calibration: {n} byte read (sum) and {n} byte copy issued 3 times")
     small = {}
-    for M in (1, 16, 256):
+    for M in (() if args.no_small else (1, 16, 256)):
         r = i8gemm_bench(M, max(args.steps, 20), args.warmup)
         small[str(M)] = dict(us=round(r["ms"] * 1e3, 2), tops=round(r["tops"], 2), gbs=round(r["gbs"], 1),
                              hbm_frac=round(r["gbs"] / PEAK_HBM_GBS, 4))
@@ -186,7 +210,7 @@ def main():
         "config": {"workload": "int8 GEMM relu(((float)(A_i8·W_i8^T)·sa[m])·sw[n] + bias[n]), int32 accumulate",
                    "M": 4096, "N": 4096, "K": 4096},
         "roofline": {"bound": "mfma", "achieved": round(g["tops"], 2), "peak": PEAK_I8_TOPS, "unit": "TOP/s",
-                     "frac": round(g["tops"] / PEAK_I8_TOPS, 4), "traffic": None},
+                     "frac": round(g["tops"] / PEAK_I8_TOPS, 4), "traffic": measured_traffic()},
     }
     if not args.no_cpu:
         c8 = cpu_baseline(g, 8)

@@ -5,14 +5,17 @@
 //                          fused (reference include/kernix_model.h:143-178 and the activation pass :1854-1856)
 //   knx_hip_dequant        fp32 copy w = q·scale (reference include/kernix_model.h:91-95)
 //
-// GEMM structure (one workgroup per BM×BN output tile, K streamed in 64-byte k-tiles):
-//   global → VGPR (16-byte loads, fully coalesced: 4 lanes per 64-byte row segment) → LDS (double buffered,
-//   16-byte chunks XOR-swizzled per row so the MFMA fragment reads are bank-conflict free) → v4i32 fragments →
-//   32×32×32 i8 MFMAs into int32 accumulators → epilogue straight from the accumulators.
-//   Both operands are K-contiguous (A: M×K activations, W: N×K weights), so no transposes are needed anywhere.
+// GEMM kernels (one workgroup per output tile; both operands K-contiguous — A: M×K activations, W: N×K weights — so
+// no transposes anywhere; int32 accumulation on MFMA, the dequant · bias · act epilogue fused):
+//   i8gemm_k128    the default whenever its tiles fill the chip: 256×256 (or 128×128) tiles, 128-byte k-tiles moved
+//                  HBM → LDS by global_load_lds (two stages, 16-byte chunks XOR-swizzled), 32×32×32 i8 MFMAs
+//   i8gemm_pipe    64-byte k-tiles through a 4-stage LDS ring; any M, N (64×64 tiles for mid-size shapes)
+//   i8gemm_skinny  M ≤ 64: every W byte read once, K split across the waves of a workgroup
+//   i8gemm_tile    VGPR-staged kernel (K == 0, and forced variants for tests)
 #include <stdlib.h>
 
 #include <string>
+#include <type_traits>
 
 #include "knx_common.hpp"
 
@@ -239,13 +242,13 @@ typedef __attribute__((address_space(1))) const void* gbl_ptr_t;
 // Writes the 16 staged rows [mt0, mt0+16) of a tile: 4 consecutive columns per lane, one 16-byte store per row.
 // ACT ≥ −1 is a compile-time activation for the common case (vector path, no accumulation); −2 is the general path.
 template <int ACT>
-__device__ __forceinline__ void store_rows(const I8Args& p, const int* stg, const float* row_scale, int mt0, int m0, int rq,
-                                           int rpi, int srow, int cq, int nb, const float* swv, const float* bv,
-                                           bool vec = true)
+__device__ __forceinline__ void store_rows(const I8Args& p, const int* stg, const float* row_scale, int mt0, int m0, int mlo,
+                                           int nlo, int rq, int rpi, int srow, int cq, int nb, const float* swv,
+                                           const float* bv, bool vec = true)
 {
     for (int rr = rq; rr < 16; rr += rpi) {
         const int mt = mt0 + rr, m = m0 + mt;
-        if (m >= p.M) continue;
+        if (m < mlo || m >= p.M) continue;
         const v4i a = *reinterpret_cast<const v4i*>(&stg[rr * srow + cq]);
         if (ACT >= -1) {
             const float sx = row_scale[mt];
@@ -280,7 +283,7 @@ __device__ __forceinline__ void store_rows(const I8Args& p, const int* stg, cons
         } else {
 #pragma unroll
             for (int q = 0; q < 4; ++q)
-                if (nb + q < p.N) i8_epilogue(p, m, nb + q, a[q]);
+                if (nb + q >= nlo && nb + q < p.N) i8_epilogue(p, m, nb + q, a[q]);
         }
     }
 }
@@ -307,6 +310,54 @@ __device__ __forceinline__ void tile_of(int t, int tiles_m, int tiles_n, int& tm
     } else {
         tm = t / tiles_n;
         tn = t % tiles_n;
+    }
+}
+
+// Epilogue of the pipelined kernels: each wave stages 16 rows × TN of its accumulators at a time in its own LDS
+// region (row stride TN+4 ints: the two half-waves land on different banks); every lane then reads 4 consecutive
+// columns and writes them with one 16-byte store.  The regions are private to the wave, so after one workgroup
+// barrier (nobody reads the operand ring any more) only the wave's own LDS order matters: no barrier — and so no
+// wait for the stores — per round.  nb is this lane's first output column, swv/bv its 4 column scales and biases.
+template <int BM, int BN, int WM, int WN>
+__device__ __forceinline__ void tile_epilogue(const I8Args& p, const v16i (&acc)[BM / WM / 32][BN / WN / 32],
+                                              int8_t* lds, float* row_scale, float my_sa, int m0, int nb,
+                                              const float* swv, const float* bv, int mlo, int nlo)
+{
+    constexpr int TM = BM / WM, TN = BN / WN;
+    constexpr int FM = TM / 32, FN = TN / 32;
+    constexpr int SROW = TN + 4;
+    constexpr int LPR = TN / 4;
+    constexpr int RPI = 64 / LPR;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, wm = wave / WN;
+    const int rl = lane & 31, g = lane >> 5;
+    int* stg = reinterpret_cast<int*>(lds) + wave * 16 * SROW;
+    const int cq = (lane % LPR) * 4, rq = lane / LPR;
+    const bool vec = nb >= nlo && nb + 3 < p.N && (p.ldy & 3) == 0 && ((uintptr_t)p.Y & 15) == 0 &&
+                     (p.ldacc & 3) == 0 && ((uintptr_t)p.acc & 15) == 0;
+    if (t < BM) row_scale[t] = my_sa;
+    KNX_WAIT_LDS();
+    knx_barrier_nofence();
+#pragma unroll
+    for (int fi = 0; fi < FM; ++fi) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int fj = 0; fj < FN; ++fj)
+#pragma unroll
+                for (int e = 8 * h; e < 8 * h + 8; ++e)
+                    stg[(8 * ((e >> 2) - 2 * h) + 4 * g + (e & 3)) * SROW + fj * 32 + rl] = acc[fi][fj][e];
+            KNX_WAIT_LDS();
+            asm volatile("" ::: "memory");
+            const int mt0 = wm * TM + fi * 32 + 16 * h;
+            const bool fast = vec && p.Y && !p.acc && !p.accumulate;  // plain Y store (no raw accumulators requested)
+            if (fast && p.act == KERNIX_ACT_RELU_ID)
+                store_rows<0>(p, stg, row_scale, mt0, m0, mlo, nlo, rq, RPI, SROW, cq, nb, swv, bv);
+            else if (fast && p.act == -1)
+                store_rows<-1>(p, stg, row_scale, mt0, m0, mlo, nlo, rq, RPI, SROW, cq, nb, swv, bv);
+            else
+                store_rows<-2>(p, stg, row_scale, mt0, m0, mlo, nlo, rq, RPI, SROW, cq, nb, swv, bv, vec);
+            asm volatile("" ::: "memory");
+        }
     }
 }
 
@@ -441,45 +492,8 @@ __global__ void __launch_bounds__(WM * WN * 64) i8gemm_pipe(I8Args p)
         mfmas(a1, b1);
     }
 
-    // Epilogue: each wave stages 16 rows × TN of its accumulators at a time in its own LDS region (row stride TN+4
-    // ints: the two half-waves land on different banks); every lane then reads 4 consecutive columns and writes them
-    // with one 16-byte store.  The regions are private to the wave, so after one workgroup barrier (nobody reads the
-    // ring any more) only the wave's own LDS order matters: no barrier — and so no wait for the stores — per round.
-    constexpr int SROW = TN + 4;
-    constexpr int LPR = TN / 4;
-    constexpr int RPI = 64 / LPR;
-    static_assert(NW * 16 * SROW * 4 <= STAGES * STAGE, "staging fits in the ring");
-    static_assert(LPR == LPR_, "epilogue lane split");
-    int* stg = reinterpret_cast<int*>(lds) + wave * 16 * SROW;
-    const int cq = (lane % LPR) * 4, rq = lane / LPR;
-    const int nb = nb_;
-    const bool vec = nb + 3 < p.N && (p.ldy & 3) == 0 && ((uintptr_t)p.Y & 15) == 0 && (p.ldacc & 3) == 0 &&
-                     ((uintptr_t)p.acc & 15) == 0;
-    if (t < BM) row_scale[t] = my_sa;
-    KNX_WAIT_LDS();
-    knx_barrier_nofence();
-#pragma unroll
-    for (int fi = 0; fi < FM; ++fi) {
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-#pragma unroll
-            for (int fj = 0; fj < FN; ++fj)
-#pragma unroll
-                for (int e = 8 * h; e < 8 * h + 8; ++e)
-                    stg[(8 * ((e >> 2) - 2 * h) + 4 * g + (e & 3)) * SROW + fj * 32 + rl] = acc[fi][fj][e];
-            KNX_WAIT_LDS();
-            asm volatile("" ::: "memory");
-            const int mt0 = wm * TM + fi * 32 + 16 * h;
-            const bool fast = vec && p.Y && !p.acc && !p.accumulate;  // plain Y store (no raw accumulators requested)
-            if (fast && p.act == KERNIX_ACT_RELU_ID)
-                store_rows<0>(p, stg, row_scale, mt0, m0, rq, RPI, SROW, cq, nb, swv, bv);
-            else if (fast && p.act == -1)
-                store_rows<-1>(p, stg, row_scale, mt0, m0, rq, RPI, SROW, cq, nb, swv, bv);
-            else
-                store_rows<-2>(p, stg, row_scale, mt0, m0, rq, RPI, SROW, cq, nb, swv, bv, vec);
-            asm volatile("" ::: "memory");
-        }
-    }
+    static_assert(NW * 16 * (TN + 4) * 4 <= STAGES * STAGE, "staging fits in the ring");
+    tile_epilogue<BM, BN, WM, WN>(p, acc, lds, row_scale, my_sa, m0, nb_, swv, bv, m0, n0);
 }
 
 template <int BM, int BN, int WM, int WN, int STAGES>
@@ -490,6 +504,207 @@ int launch_pipe(I8Args p, hipStream_t s, const char* name)
     const unsigned grid = (unsigned)p.tiles_m * (unsigned)p.tiles_n;
     hipLaunchKernelGGL((i8gemm_pipe<BM, BN, WM, WN, STAGES>), dim3(grid), dim3(WM * WN * 64), 0, s, p);
     return knx::check_launch(name);
+}
+
+// ---------------------------------------------------------------- 128-byte k-tile kernel
+// Each operand row contributes one whole 128-byte cache line per k-tile (a 64-byte k-tile fetches half lines, which
+// wastes half of every L2 → CU transfer).  Two LDS stages of (BM+BN)·128 bytes: the loads of tile kt+1 run under the
+// four 32-byte k-steps of tile kt, with one workgroup barrier per 128 bytes of K.
+//
+// LDS layout: a row holds 8 chunks of 16 bytes, global chunk c of row r at position c ^ swz8(r).  The 16 rows that
+// one quarter-wave of a ds_read_b128 touches (same chunk, consecutive rows) then fall on 16 distinct 16-byte bank
+// groups, and any 8 consecutive rows on 8.  swz8(r + 32) = swz8(r) ^ 4, so the fragment of row r + 32·f at k-step s
+// sits at the offset of row r's k-step s ^ 2·(f & 1), plus f·4096: four offset registers per operand cover every
+// fragment.
+//
+// Loads: global_load_lds_dwordx4 with a scalar base (tile row + slot row · ld + k) and a 32-bit lane offset
+// (row-in-slot · ld + chunk).  A tile that would run past M (or N) is moved back to end at row M (column N): it
+// recomputes a few rows of its neighbour and stores only the rows (columns) it owns, so every operand row it reads
+// exists.  A half k-tile at the end (K % 128 == 64) loads its lower 64 bytes twice and multiplies two k-steps only.
+__device__ __forceinline__ int swz8(int row) { return (row ^ (row >> 3)) & 7; }
+
+// LDS-DMA load of 16 bytes per lane, global (base + voff) → LDS (dst + 16·lane), with base and dst wave-uniform.
+// Inline assembly, so that the compiler does not treat it as an LDS store: it cannot tell the two stages apart and
+// would make every later LDS read wait for all outstanding loads.  The loads are waited for explicitly (vmcnt) and
+// published with a workgroup barrier; the compiler's own vmcnt waits stay correct, only stricter (vmcnt retires
+// loads in order, so loads it does not know about only add younger entries).
+__device__ __forceinline__ void dma16(const int8_t* base, unsigned voff, int8_t* dst)
+{
+    const unsigned l = (unsigned)(uintptr_t)(lds_ptr_t)dst;
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(l), "v"(voff), "s"(base) : "memory");
+}
+
+template <int BM, int BN, int WM, int WN>
+__global__ void __launch_bounds__(WM * WN * 64) i8gemm_k128(I8Args p)
+{
+    constexpr int NW = WM * WN;
+    constexpr int TM = BM / WM, TN = BN / WN;
+    constexpr int FM = TM / 32, FN = TN / 32;
+    constexpr int ROWS = BM + BN;
+    constexpr int STAGE = ROWS * 128;      // bytes per k-tile
+    constexpr int SLOTS = ROWS / 8 / NW;   // 1-KB loads (8 rows × 128 bytes) per wave per k-tile
+    constexpr int SA = BM / 8 / NW;        // slots 0..SA-1 load A rows, the rest W rows
+    static_assert(BM % (8 * NW) == 0 && BN % (8 * NW) == 0 && SLOTS <= 63, "load split");
+    static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile");
+    static_assert(NW * 16 * (TN + 4) * 4 <= 2 * STAGE, "staging fits in the stages");
+    static_assert(BM <= NW * 64, "one row scale per thread");
+    __shared__ __attribute__((aligned(16))) int8_t lds[2 * STAGE];
+    __shared__ float row_scale[BM];
+
+    const int t = threadIdx.x, lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int wm = wave / WN, wn = wave % WN;
+    int tm, tn;
+    tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+    const int mlo = tm * BM, nlo = tn * BN;                  // first row / column this tile owns
+    const int m0 = min(mlo, p.M - BM), n0 = min(nlo, p.N - BN);  // first row / column it computes
+
+    // this lane's 4 epilogue columns and its row scale, loaded first so their latency hides under the K loop
+    const int nb = n0 + wn * TN + (lane % (TN / 4)) * 4;
+    float swv[4], bv[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        swv[q] = p.Y ? p.sw[nb + q] : 0.0f;
+        bv[q] = p.bias ? p.bias[nb + q] : 0.0f;
+    }
+    const float my_sa = (t < BM && p.Y) ? p.sa[m0 + t] : 0.0f;
+
+    // slot i covers rows (i·NW + wave)·8 + 0..7 of the tile's A rows then W rows; lane l loads row l >> 3 of the slot,
+    // global chunk (l & 7) ^ swz8(row) = (l & 7) ^ (l >> 3) ^ ((i·NW + wave) & 7) into LDS position l & 7.  The
+    // address is a scalar base (operand tile + slot row · ld + k) plus this lane's 32-bit offset.
+    const int8_t* tile_a = p.A + (size_t)m0 * p.lda;
+    const int8_t* tile_w = p.W + (size_t)n0 * p.ldw;
+    const int cl = (lane & 7) ^ (lane >> 3), rs = lane >> 3;
+    const int nk = (p.K + 127) / 128;
+    const bool half = (p.K & 127) != 0;
+    // load slot i of k-tile kt into its stage
+    auto issue1 = [&](int kt, int i) {
+        const int slot = i * NW + wave;
+        const bool a = i < SA;
+        const int ld = a ? p.lda : p.ldw;
+        int chunk = cl ^ (slot & 7);
+        if (half && kt == nk - 1) chunk &= 3;  // the upper 64 bytes are past K: load the lower ones again (never multiplied)
+        const int8_t* base = (a ? tile_a + (size_t)(slot * 8) * ld : tile_w + (size_t)(slot * 8 - BM) * ld) + kt * 128;
+        dma16(base, (unsigned)(rs * ld + chunk * 16), lds + (kt & 1) * STAGE + slot * 1024);
+    };
+
+    const int rl = lane & 31, g = lane >> 5;
+    int aoff[4], boff[4];
+    {
+        const int ra_ = wm * TM + rl, rb_ = BM + wn * TN + rl;
+        const int sa_ = swz8(ra_), sb_ = swz8(rb_);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            aoff[s] = ra_ * 128 + (((2 * s + g) ^ sa_) << 4);
+            boff[s] = rb_ * 128 + (((2 * s + g) ^ sb_) << 4);
+        }
+    }
+    // fragment j of k-step s of k-tile kt: j < FM an A fragment, else a W fragment
+    v4i fa[2][FM], fb[2][FN];
+    auto read1 = [&](int kt, int s, int j) {
+        const int8_t* cur = lds + (kt & 1) * STAGE;
+        if (j < FM) fa[s & 1][j] = *(const v4i*)(cur + aoff[s ^ (2 * (j & 1))] + j * 4096);
+        else fb[s & 1][j - FM] = *(const v4i*)(cur + boff[s ^ (2 * ((j - FM) & 1))] + (j - FM) * 4096);
+    };
+
+    v16i acc[FM][FN];
+#pragma unroll
+    for (int fi = 0; fi < FM; ++fi)
+#pragma unroll
+        for (int fj = 0; fj < FN; ++fj)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[fi][fj][e] = 0;
+    // multiply j of k-step s (fragment set s & 1)
+    auto mfma1 = [&](int s, int j) {
+        const int fi = j / FN, fj = j % FN;
+        acc[fi][fj] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[s & 1][fi], fb[s & 1][fj], acc[fi][fj], 0, 0, 0);
+    };
+
+    // One k-tile.  K-steps 0..2: multiply fragment set s & 1 while the FM+FN fragments of k-step s+1 are read, one
+    // read after each of the first FM+FN multiplies (the reads hide under the MFMA pipeline).  K-step 3: after the
+    // first PRE multiplies the wave waits for its loads of tile kt+1 and for its own LDS reads (which include the last
+    // ones of stage kt & 1), then the workgroup barrier: tile kt+1 is complete in LDS and nobody reads stage kt & 1
+    // any more, so the remaining multiplies are interleaved with the first fragment reads of tile kt+1 and the loads
+    // of tile kt+2 into stage kt & 1.  ARRIVE / ISSUE are compile-time so the steady-state loop has no branches (a
+    // branch merge makes the compiler wait for every outstanding LDS read at the merge); the sched_barrier(0) calls
+    // pin the interleaving.
+    constexpr int NM = FM * FN, NR = FM + FN, PRE = NM / 4;
+    constexpr int GAPS = NM - PRE;
+    auto ktile = [&](int kt, auto ARRIVE, auto ISSUE, bool upper) {
+        constexpr bool arrive = decltype(ARRIVE)::value, iss = decltype(ISSUE)::value;
+#pragma unroll
+        for (int s = 0; s < 3; ++s) {
+#pragma unroll
+            for (int j = 0; j < NR; ++j) read1(kt, s + 1, j);
+            if (s < 2 || upper)
+#pragma unroll
+                for (int j = 0; j < NM; ++j) mfma1(s, j);
+#pragma unroll
+            for (int j = 0; j < NR; ++j) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, NM - NR, 0);
+        }
+        if (!upper) return;  // a half k-tile: k-steps 2 and 3 are past K
+        if (!arrive) {
+#pragma unroll
+            for (int j = 0; j < NM; ++j) mfma1(3, j);
+            return;
+        }
+#pragma unroll
+        for (int j = 0; j < PRE; ++j) mfma1(3, j);
+        __builtin_amdgcn_sched_barrier(0);
+        KNX_WAIT_VM_LDS(0);
+        knx_barrier_nofence();
+        int r = 0, l = 0;
+#pragma unroll
+        for (int j = PRE; j < NM; ++j) {
+            mfma1(3, j);
+            const int rupto = (NR * (j - PRE + 1) + GAPS - 1) / GAPS;  // reads first: they are needed sooner
+            while (r < rupto) read1(kt + 1, 0, r++);
+            if (iss) {
+                const int upto = (SLOTS * (j - PRE + 1) + GAPS - 1) / GAPS;  // spread the loads over the gaps
+                while (l < upto) issue1(kt + 2, l++);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    using yes = std::integral_constant<bool, true>;
+    using no = std::integral_constant<bool, false>;
+#pragma unroll
+    for (int i = 0; i < SLOTS; ++i) issue1(0, i);
+    KNX_WAIT_VM_LDS(0);
+    knx_barrier_nofence();
+    if (nk > 1)
+#pragma unroll
+        for (int i = 0; i < SLOTS; ++i) issue1(1, i);
+#pragma unroll
+    for (int j = 0; j < NR; ++j) read1(0, 0, j);
+    int kt = 0;
+    for (; kt < nk - 2; ++kt) ktile(kt, yes{}, yes{}, true);
+    if (nk >= 2) ktile(kt++, yes{}, no{}, true);
+    ktile(kt, no{}, no{}, !half);
+
+    tile_epilogue<BM, BN, WM, WN>(p, acc, lds, row_scale, my_sa, m0, nb, swv, bv, mlo, nlo);
+}
+
+template <int BM, int BN, int WM, int WN>
+int launch_k128(I8Args p, hipStream_t s, const char* name)
+{
+    p.tiles_m = (p.M + BM - 1) / BM;
+    p.tiles_n = (p.N + BN - 1) / BN;
+    const unsigned grid = (unsigned)p.tiles_m * (unsigned)p.tiles_n;
+    hipLaunchKernelGGL((i8gemm_k128<BM, BN, WM, WN>), dim3(grid), dim3(WM * WN * 64), 0, s, p);
+    return knx::check_launch(name);
+}
+
+// the 128-byte k-tile kernel needs whole tiles inside the matrices (tiles are moved back, never clipped) and each
+// lane offset (at most 7 rows) inside 32 bits
+template <int BM, int BN>
+bool k128_fits(const I8Args& p)
+{
+    return p.M >= BM && p.N >= BN && (long)8 * p.lda < 0x7fffffffL && (long)8 * p.ldw < 0x7fffffffL;
 }
 
 // ---------------------------------------------------------------- skinny kernel (M ≤ 64)
@@ -664,7 +879,7 @@ extern "C" int knx_hip_i8gemm(int M, int N, int K, const int8_t* A, int lda, con
         // empty inner dimension: the accumulators are all zero; run the smallest tile (loop body never executes)
         return launch_tile<64, 64, 1, 1>(p, s, name);
     }
-    // KNX_I8_KERNEL forces one variant (tuning and tests); otherwise the shape picks it
+    // KNX_I8_KERNEL forces one variant (tuning and tests) where its shape limits allow; otherwise the shape picks it
     const char* force = getenv("KNX_I8_KERNEL");
     if (force != nullptr && *force) {
         const std::string f(force);
@@ -675,15 +890,20 @@ extern "C" int knx_hip_i8gemm(int M, int N, int K, const int8_t* A, int lda, con
         if (f == "pipe256s3") return launch_pipe<256, 256, 2, 2, 3>(p, s, name);
         if (f == "pipe128") return launch_pipe<128, 128, 2, 2, 4>(p, s, name);
         if (f == "pipe64") return launch_pipe<64, 64, 2, 2, 4>(p, s, name);
+        if (f == "k128" && k128_fits<256, 256>(p)) return launch_k128<256, 256, 2, 2>(p, s, name);
+        if (f == "k128w8" && k128_fits<256, 256>(p)) return launch_k128<256, 256, 2, 4>(p, s, name);
+        if (f == "k128w8t" && k128_fits<256, 256>(p)) return launch_k128<256, 256, 4, 2>(p, s, name);
+        if (f == "k128m" && k128_fits<128, 128>(p)) return launch_k128<128, 128, 2, 2>(p, s, name);
         if (f == "skinny" && M <= 64) return M <= 16 ? launch_skinny<1>(p, s, name) : M <= 32 ? launch_skinny<2>(p, s, name) : launch_skinny<4>(p, s, name);
     }
     if (M <= 16) return launch_skinny<1>(p, s, name);
     if (M <= 32) return launch_skinny<2>(p, s, name);
     if (M <= 64) return launch_skinny<4>(p, s, name);
+    // the largest tile that still gives every CU a workgroup
     const long tiles256 = (long)((M + 255) / 256) * ((N + 255) / 256);
-    if (tiles256 >= knx::num_cus()) return launch_pipe<256, 256, 2, 2, 4>(p, s, name);
+    if (tiles256 >= knx::num_cus() && k128_fits<256, 256>(p)) return launch_k128<256, 256, 4, 2>(p, s, name);
     const long tiles128 = (long)((M + 127) / 128) * ((N + 127) / 128);
-    if (tiles128 >= knx::num_cus()) return launch_pipe<128, 128, 2, 2, 4>(p, s, name);
+    if (tiles128 >= knx::num_cus() && k128_fits<128, 128>(p)) return launch_k128<128, 128, 2, 2>(p, s, name);
     return launch_pipe<64, 64, 2, 2, 4>(p, s, name);
 }
 

@@ -64,6 +64,37 @@ def test_i8gemm_bit_exact(L, M, N, K):
     assert np.array_equal(host(Y), want_y)
 
 
+I8_VARIANTS = ["default", "k128", "k128w8", "k128w8t", "k128m", "pipe256", "pipe256w8", "pipe128", "pipe64", "tile64"]
+# tiles moved back at the M/N edges, half k-tiles (K % 128 == 64), N % 4 != 0, one whole 256x256 tile
+I8_EDGE_SHAPES = [(300, 300, 1024), (520, 700, 320), (257, 259, 192), (256, 256, 64), (640, 384, 4096)]
+
+
+@pytest.mark.parametrize("variant", I8_VARIANTS)
+@pytest.mark.parametrize("M,N,K", I8_EDGE_SHAPES)
+def test_i8gemm_variants_y_only(L, monkeypatch, variant, M, N, K):
+    """every kernel variant on the output-only path (relu, no bias; none with accumulate) against the oracle"""
+    monkeypatch.setenv("KNX_I8_KERNEL", variant)
+    rng = np.random.default_rng(M + 3 * N + 5 * K)
+    A = rng.integers(-127, 128, (M, K), dtype=np.int8)
+    W = rng.integers(-128, 128, (N, K), dtype=np.int8)
+    sa = rng.uniform(0.001, 0.01, M).astype(np.float32)
+    sw = rng.uniform(0.001, 0.01, N).astype(np.float32)
+    bias = rng.normal(0, 0.1, N).astype(np.float32)
+    want_y, acc = knx_ref.i8gemm(A, W, sa, sw, bias, act_id=0)
+    dA, dW, dsa, dsw, db = dev(A), dev(W), dev(sa), dev(sw), dev(bias)
+    Y = torch.full((M, N), 7.0, dtype=torch.float32, device="cuda")
+    hipabi.check(L.knx_hip_i8gemm(M, N, K, ptr(dA), K, ptr(dsa), ptr(dW), K, ptr(dsw), ptr(db), 0, 0.0, 0,
+                                  ptr(Y), N, None, 0, hipabi.stream()))
+    assert np.array_equal(host(Y), want_y)
+    # no bias, no activation, accumulate into Y: every output must be added exactly once
+    y0 = rng.normal(0, 1, (M, N)).astype(np.float32)
+    plain = ((acc.astype(np.float32) * sa[:, None]).astype(np.float32) * sw[None, :]).astype(np.float32)
+    Y2 = dev(y0)
+    hipabi.check(L.knx_hip_i8gemm(M, N, K, ptr(dA), K, ptr(dsa), ptr(dW), K, ptr(dsw), None, -1, 0.0, 1,
+                                  ptr(Y2), N, None, 0, hipabi.stream()))
+    assert np.array_equal(host(Y2), (y0 + plain).astype(np.float32))
+
+
 def test_i8gemm_accumulate_and_no_bias(L):
     rng = np.random.default_rng(3)
     M, N, K = 37, 70, 128
