@@ -32,7 +32,9 @@ def log(*a):
 
 
 def time_launches(fn, steps, warmup):
-    """(avg ms per launch from HIP events on the current stream, wall ms per launch)"""
+    """(ms per launch, wall ms per launch): `steps` launches back to back between two HIP events on torch's current
+    stream, which is the stream the launches go to.  An event pair around every single launch would add a
+    system-scope cache flush per launch (≈10 µs for a 64 MB output) that a kernel-trace profile does not see."""
     import torch
 
     for _ in range(warmup):
@@ -210,7 +212,8 @@ def main():
         "config": {"workload": "int8 GEMM relu(((float)(A_i8·W_i8^T)·sa[m])·sw[n] + bias[n]), int32 accumulate",
                    "M": 4096, "N": 4096, "K": 4096},
         "roofline": {"bound": "mfma", "achieved": round(g["tops"], 2), "peak": PEAK_I8_TOPS, "unit": "TOP/s",
-                     "frac": round(g["tops"] / PEAK_I8_TOPS, 4), "traffic": measured_traffic()},
+                     "frac": round(g["tops"] / PEAK_I8_TOPS, 4), "traffic": measured_traffic(),
+                     "kernel_us": round(g["ms"] * 1e3, 2)},
     }
     if not args.no_cpu:
         c8 = cpu_baseline(g, 8)

@@ -699,6 +699,167 @@ int launch_k128(I8Args p, hipStream_t s, const char* name)
     return knx::check_launch(name);
 }
 
+// ---------------------------------------------------------------- ping-pong kernel
+// Same tiles, LDS layout and loads as i8gemm_k128, with the eight waves split in two groups of four (one wave of each
+// group per SIMD) that take turns: while one group multiplies two k-steps from registers, the other reads its
+// fragments of the next two k-steps from LDS (and group 0 also issues the loads), then a workgroup barrier and the
+// roles swap.  The MFMA unit of a SIMD is always fed by the wave whose operands are already in registers, and a wave
+// stalled on issuing loads or on LDS latency never holds back the multiplies of the other.  K-tile t (two halves of two
+// k-steps) runs as four phases:
+//   group 0 multiplies half 0 of t                 group 1 reads half 0 of t, loads its half of k-tile t+1
+//   group 0 reads half 1 of t                      group 1 multiplies half 0 of t
+//   group 0 multiplies half 1 of t                 group 1 reads half 1 of t (last reads of stage t & 1)
+//   group 0 loads its half of k-tile t+2 into stage t & 1, reads half 0 of t+1;   group 1 multiplies half 1 of t
+template <int BM, int BN>
+__global__ void __launch_bounds__(512) i8gemm_pp(I8Args p)
+{
+    constexpr int WM = 4, WN = 2, NW = 8;
+    constexpr int TM = BM / WM, TN = BN / WN;
+    constexpr int FM = TM / 32, FN = TN / 32;
+    constexpr int ROWS = BM + BN;
+    constexpr int STAGE = ROWS * 128;
+    constexpr int SLOTS = ROWS / 8 / NW;   // 1-KB loads per wave per k-tile
+    constexpr int SA = BM / 8 / NW;
+    static_assert(BM % (8 * NW) == 0 && BN % (8 * NW) == 0, "load split");
+    static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile");
+    static_assert(NW * 16 * (TN + 4) * 4 <= 2 * STAGE, "staging fits in the stages");
+    static_assert(BM <= NW * 64, "one row scale per thread");
+    __shared__ __attribute__((aligned(16))) int8_t lds[2 * STAGE];
+    __shared__ float row_scale[BM];
+
+    const int t = threadIdx.x, lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int grp = wave >> 2;
+    const int wm = wave / WN, wn = wave % WN;
+    int tm, tn;
+    tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+    const int mlo = tm * BM, nlo = tn * BN;
+    const int m0 = min(mlo, p.M - BM), n0 = min(nlo, p.N - BN);
+
+    const int nb = n0 + wn * TN + (lane % (TN / 4)) * 4;
+    float swv[4], bv[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        swv[q] = p.Y ? p.sw[nb + q] : 0.0f;
+        bv[q] = p.bias ? p.bias[nb + q] : 0.0f;
+    }
+    const float my_sa = (t < BM && p.Y) ? p.sa[m0 + t] : 0.0f;
+
+    const int8_t* tile_a = p.A + (size_t)m0 * p.lda;
+    const int8_t* tile_w = p.W + (size_t)n0 * p.ldw;
+    const int cl = (lane & 7) ^ (lane >> 3), rs = lane >> 3;
+    const int nk = (p.K + 127) / 128;
+    const bool half = (p.K & 127) != 0;
+    // this wave's share of the loads of k-tile kt
+    auto issue = [&](int kt) {
+#pragma unroll
+        for (int i = 0; i < SLOTS; ++i) {
+            const int slot = i * NW + wave;
+            const bool a = i < SA;
+            const int ld = a ? p.lda : p.ldw;
+            int chunk = cl ^ (slot & 7);
+            if (half && kt == nk - 1) chunk &= 3;
+            const int8_t* base = (a ? tile_a + (size_t)(slot * 8) * ld : tile_w + (size_t)(slot * 8 - BM) * ld) + kt * 128;
+            dma16(base, (unsigned)(rs * ld + chunk * 16), lds + (kt & 1) * STAGE + slot * 1024);
+        }
+    };
+
+    const int rl = lane & 31, g = lane >> 5;
+    int aoff[4], boff[4];
+    {
+        const int ra_ = wm * TM + rl, rb_ = BM + wn * TN + rl;
+        const int sa_ = swz8(ra_), sb_ = swz8(rb_);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            aoff[s] = ra_ * 128 + (((2 * s + g) ^ sa_) << 4);
+            boff[s] = rb_ * 128 + (((2 * s + g) ^ sb_) << 4);
+        }
+    }
+    // the fragments of two k-steps (half h of k-tile kt)
+    v4i fa[2][FM], fb[2][FN];
+    auto read_half = [&](int kt, int h) {
+        const int8_t* cur = lds + (kt & 1) * STAGE;
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            const int k = 2 * h + s;
+#pragma unroll
+            for (int fi = 0; fi < FM; ++fi) fa[s][fi] = *(const v4i*)(cur + aoff[k ^ (2 * (fi & 1))] + fi * 4096);
+#pragma unroll
+            for (int fj = 0; fj < FN; ++fj) fb[s][fj] = *(const v4i*)(cur + boff[k ^ (2 * (fj & 1))] + fj * 4096);
+        }
+    };
+    v16i acc[FM][FN];
+#pragma unroll
+    for (int fi = 0; fi < FM; ++fi)
+#pragma unroll
+        for (int fj = 0; fj < FN; ++fj)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[fi][fj][e] = 0;
+    auto compute_half = [&]() {
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+#pragma unroll
+            for (int fi = 0; fi < FM; ++fi)
+#pragma unroll
+                for (int fj = 0; fj < FN; ++fj)
+                    acc[fi][fj] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[s][fi], fb[s][fj], acc[fi][fj], 0, 0, 0);
+    };
+
+    // Both groups run the same sequence of operations — per k-tile R(t,0) C(t,0) R(t,1) C(t,1), each ending at a
+    // workgroup barrier — with group 1 one barrier behind, so a barrier ends a C of one group and an R of the other and
+    // no branch on the group (which would merge register values) is needed.  R(t,0) also issues the wave's share of
+    // the loads of k-tile t+1 (into the stage last read in R(t-1,1) of group 1, which ended before group 0's R(t,0)
+    // began); every wave waits for its loads (vmcnt) before the barrier that precedes group 0's R(t+1,0): group 0 at
+    // the end of C(t,1), group 1 at the end of R(t,1).
+    // A phase boundary: the accumulators pass through an empty asm statement next to the barrier, so no multiply
+    // moves across it (MFMAs touch no memory, so the barrier's memory clobber alone would not hold them), and the
+    // machine scheduler keeps every instruction on its side.
+    static_assert(FM * FN == 8, "phase boundary pins eight accumulators");
+    auto boundary = [&]() {
+        asm volatile("" : "+v"(acc[0][0]), "+v"(acc[0][1]), "+v"(acc[0][2]), "+v"(acc[0][3]), "+v"(acc[1][0]),
+                     "+v"(acc[1][1]), "+v"(acc[1][2]), "+v"(acc[1][3]));
+        __builtin_amdgcn_sched_barrier(0);
+        knx_barrier_nofence();
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    issue(0);
+    KNX_WAIT_VM_LDS(0);
+    boundary();
+    if (grp == 1) boundary();
+    for (int kt = 0; kt < nk; ++kt) {
+        // R(t,0)
+        if (kt + 1 < nk) issue(kt + 1);
+        read_half(kt, 0);
+        KNX_WAIT_LDS();
+        boundary();
+        // C(t,0)
+        compute_half();
+        boundary();
+        // R(t,1)
+        read_half(kt, 1);
+        if (grp == 1) KNX_WAIT_VM_LDS(0);
+        else KNX_WAIT_LDS();
+        boundary();
+        // C(t,1): a half k-tile (K % 128 == 64, last) has no k-steps 2 and 3
+        if (!(half && kt == nk - 1)) compute_half();
+        if (grp == 0) KNX_WAIT_VM_LDS(0);
+        boundary();
+    }
+    if (grp == 0) boundary();
+
+    tile_epilogue<BM, BN, WM, WN>(p, acc, lds, row_scale, my_sa, m0, nb, swv, bv, mlo, nlo);
+}
+
+template <int BM, int BN>
+int launch_pp(I8Args p, hipStream_t s, const char* name)
+{
+    p.tiles_m = (p.M + BM - 1) / BM;
+    p.tiles_n = (p.N + BN - 1) / BN;
+    const unsigned grid = (unsigned)p.tiles_m * (unsigned)p.tiles_n;
+    hipLaunchKernelGGL((i8gemm_pp<BM, BN>), dim3(grid), dim3(512), 0, s, p);
+    return knx::check_launch(name);
+}
+
 // the 128-byte k-tile kernel needs whole tiles inside the matrices (tiles are moved back, never clipped) and each
 // lane offset (at most 7 rows) inside 32 bits
 template <int BM, int BN>
@@ -894,6 +1055,7 @@ extern "C" int knx_hip_i8gemm(int M, int N, int K, const int8_t* A, int lda, con
         if (f == "k128w8" && k128_fits<256, 256>(p)) return launch_k128<256, 256, 2, 4>(p, s, name);
         if (f == "k128w8t" && k128_fits<256, 256>(p)) return launch_k128<256, 256, 4, 2>(p, s, name);
         if (f == "k128m" && k128_fits<128, 128>(p)) return launch_k128<128, 128, 2, 2>(p, s, name);
+        if (f == "pp" && k128_fits<256, 256>(p)) return launch_pp<256, 256>(p, s, name);
         if (f == "skinny" && M <= 64) return M <= 16 ? launch_skinny<1>(p, s, name) : M <= 32 ? launch_skinny<2>(p, s, name) : launch_skinny<4>(p, s, name);
     }
     if (M <= 16) return launch_skinny<1>(p, s, name);

@@ -64,7 +64,7 @@ def test_i8gemm_bit_exact(L, M, N, K):
     assert np.array_equal(host(Y), want_y)
 
 
-I8_VARIANTS = ["default", "k128", "k128w8", "k128w8t", "k128m", "pipe256", "pipe256w8", "pipe128", "pipe64", "tile64"]
+I8_VARIANTS = ["default", "pp", "k128", "k128w8", "k128w8t", "k128m", "pipe256", "pipe256w8", "pipe128", "pipe64", "tile64"]
 # tiles moved back at the M/N edges, half k-tiles (K % 128 == 64), N % 4 != 0, one whole 256x256 tile
 I8_EDGE_SHAPES = [(300, 300, 1024), (520, 700, 320), (257, 259, 192), (256, 256, 64), (640, 384, 4096)]
 
