@@ -20,7 +20,7 @@
  * Device memory is owned by the model: weights are uploaded on the first forward and kept until free; the workspace
  * (storage buffers, attention scratch, dequantized int8 copies) is allocated per chunk size and released by trim.
  *
- * Differences that a caller can observe (all deliberate, see the design notes of this repository):
+ * Differences that a caller can observe (all deliberate):
  *   - the default workspace limit is KERNIX_WORKSPACE_LIMIT = 1 GiB of device memory (reference: 64 MB of host memory);
  *   - ws_fixed counts only the dequantized int8 copies: convolution is an implicit GEMM and has no im2col buffer;
  *   - steps[i].buf, .tmp[] and .deq point at device memory.
