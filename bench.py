@@ -4,8 +4,10 @@
     python bench.py [--steps K] [--warmup W] [--no-cpu] [--no-forward]
 
 Headline (`value`): int8 GEMM Y = relu(((float)(A·Wᵀ)·sa[m])·sw[n] + bias[n]) at M = K = N = 4096 with int32
-accumulation, inputs resident in HBM, through the C ABI (knx_hip_i8gemm), in TOPS (1 MAC = 2 ops); K timed launches
-bracketed by device synchronization, kernel time from HIP events on the launch stream.
+accumulation, inputs resident in HBM, through the C ABI (knx_hip_i8gemm), in TOPS (1 MAC = 2 ops): K launches back to
+back after W warm-up launches, bracketed by device synchronization and timed by HIP events on the launch stream.
+`roofline` relates the same figure to the int8 MFMA peak and carries the HBM traffic per launch measured with
+rocprofv3 counters (read from profiles/i8gemm_4096_traffic.json).
 Also reported: the same GEMM at M ∈ {1, 16, 256} (HBM-bound) and the .knx forward samples/sec of the int8 MLP,
 fp32 MLP, CNN and int8-weight Transformer workloads (device-resident and end to end through kernix_capi_forward),
 and the CPU oracle (plain C, the reference's int8 arithmetic) timed on this machine's host cores.
@@ -158,8 +160,9 @@ def forward_bench(name, make, flops, steps, warmup, mode="ref", roof="f32"):
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    # the defaults give the clocks time to settle (a GEMM timed right after 5 warm-up launches reads ≈5% slower)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-forward", action="store_true")
     ap.add_argument("--no-small", action="store_true", help="skip the small-M GEMM lines")
@@ -230,18 +233,19 @@ def main():
     if not args.no_forward:
         fw = {}
         st = max(5, args.steps // 5)
+        fwarm = max(3, args.warmup // 10)
         fw["int8_mlp_784_512_256_10_b64"] = forward_bench(
-            "mlp", lambda p: configs.int8_mlp(p, batch=64), configs.mlp_flops(64, (784, 512, 256, 10)), st, args.warmup)
+            "mlp", lambda p: configs.int8_mlp(p, batch=64), configs.mlp_flops(64, (784, 512, 256, 10)), st, fwarm)
         fw["int8_mlp_784_512_256_10_b64_i8"] = forward_bench(
-            "mlp", lambda p: configs.int8_mlp(p, batch=64), configs.mlp_flops(64, (784, 512, 256, 10)), st, args.warmup,
+            "mlp", lambda p: configs.int8_mlp(p, batch=64), configs.mlp_flops(64, (784, 512, 256, 10)), st, fwarm,
             mode="i8", roof="i8")
         fw["fp32_mlp_4096_4096_4096_1000_b8192"] = forward_bench(
-            "f32", lambda p: configs.fp32_mlp(p), configs.mlp_flops(8192, (4096, 4096, 4096, 1000)), st, args.warmup)
-        fw["cnn_b256"] = forward_bench("cnn", lambda p: configs.cnn(p), configs.cnn_flops(), st, args.warmup)
+            "f32", lambda p: configs.fp32_mlp(p), configs.mlp_flops(8192, (4096, 4096, 4096, 1000)), st, fwarm)
+        fw["cnn_b256"] = forward_bench("cnn", lambda p: configs.cnn(p), configs.cnn_flops(), st, fwarm)
         fw["transformer_4l_d512_b64"] = forward_bench(
-            "tr", lambda p: configs.transformer(p), configs.transformer_flops(), st, args.warmup)
+            "tr", lambda p: configs.transformer(p), configs.transformer_flops(), st, fwarm)
         fw["transformer_4l_d512_b64_i8"] = forward_bench(
-            "tr", lambda p: configs.transformer(p), configs.transformer_flops(), st, args.warmup, mode="i8")
+            "tr", lambda p: configs.transformer(p), configs.transformer_flops(), st, fwarm, mode="i8")
         for k, v in fw.items():
             log(f"forward {k}: {v['ms']:.3f} ms  {v['samples_per_s']:.0f} samples/s  {v['tflops']:.1f} TFLOP/s")
         out["forward"] = fw
