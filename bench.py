@@ -14,6 +14,7 @@ and the CPU oracle (plain C, the reference's int8 arithmetic) timed on this mach
 One JSON line is printed on stdout.
 """
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -101,6 +102,79 @@ def cpu_baseline(g, threads, target_s=10.0):
     ops = 2.0 * rows * N * K
     got = g["Y"][:rows].cpu().numpy()
     return dict(tops=ops / sec / 1e12, seconds=sec, rows=rows, reps=reps, bit_exact=bool(np.array_equal(got, y)))
+
+
+def rows_bench(steps, warmup):
+    """The bandwidth-bound kernels at the Transformer / CNN workload shapes: algorithmic bytes (every fp32 input read
+    once, every output written once) per launch ÷ time, against HBM peak.  Working sets of 16–80 MB stay in the
+    256 MB last-level cache across back-to-back launches, so these rates can exceed what HBM alone delivers."""
+    import torch
+
+    from kernix_amd import hipabi
+
+    L = hipabi.lib()
+    hipabi.check(L.knx_hip_init())
+    P, S = hipabi.ptr, hipabi.stream()
+    dev = lambda *shape: torch.randn(*shape, device="cuda", dtype=torch.float32)  # noqa: E731
+    out = {}
+
+    def run(name, fn, nbytes):
+        ms, _ = time_launches(lambda: hipabi.check(fn()), steps, warmup)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[name] = dict(us=round(ms * 1e3, 2), gbs=round(gbs, 1), hbm_frac=round(gbs / PEAK_HBM_GBS, 4),
+                         bytes=int(nbytes))
+        log(f"{name}: {ms * 1e3:.2f} us  {gbs:.0f} GB/s")
+
+    x, y, g, b = dev(8192, 512), dev(8192, 512), dev(512), dev(512)
+    run("layernorm_8192x512", lambda: L.knx_hip_layernorm(P(x), P(y), 8192, 512, P(g), P(b), 1e-5, S),
+        2 * 8192 * 512 * 4 + 2 * 512 * 4)
+    sc = dev(65536, 128)
+    run("softmax_65536x128_inplace", lambda: L.knx_hip_softmax(P(sc), P(sc), 65536, 128, S), 2 * 65536 * 128 * 4)
+    h, hb = dev(8192, 2048), dev(2048)
+    run("bias_gelu_8192x2048_inplace", lambda: L.knx_hip_bias_act(P(h), P(h), 8192, 2048, P(hb), 1, 0.0, S),
+        2 * 8192 * 2048 * 4 + 2048 * 4)
+    r = dev(8192, 512)
+    run("binary_add_8192x512", lambda: L.knx_hip_binary(0, P(x), 512, 512, P(y), 512, 512, P(r), 16, 512, 512, S),
+        3 * 8192 * 512 * 4)
+    c, gp = dev(256 * 64, 256), torch.empty(256, 256, device="cuda")
+    run("global_avg_pool_256x64x256", lambda: L.knx_hip_global_pool(1, P(c), 256, 64, 256, P(gp), S),
+        256 * 64 * 256 * 4 + 256 * 256 * 4)
+    xq = torch.empty(8192, 2048, dtype=torch.int8, device="cuda")
+    sx = torch.empty(8192, device="cuda")
+    run("quantize_rows_8192x2048", lambda: L.knx_hip_quantize_rows(P(h), 2048, 8192, 2048, 2048, P(xq), 2048, P(sx), S),
+        8192 * 2048 * 5 + 8192 * 4)
+    return out
+
+
+def conv_bench(steps, warmup):
+    """The four convolutions of the CNN configuration (batch 256, NHWC, 3×3, pad 1, bias + ReLU fused) through
+    knx_hip_conv: algorithmic flops 2·B·Ho·Wo·Co·9·Cin per launch against the fp32 MFMA peak, and the minimum HBM
+    bytes (input + weights + output once)."""
+    import torch
+
+    from kernix_amd import hipabi
+
+    L = hipabi.lib()
+    hipabi.check(L.knx_hip_init())
+    P, S = hipabi.ptr, hipabi.stream()
+    out = {}
+    for name, (h, cin, cout, st) in {"c1_3to64_s1": (32, 3, 64, 1), "c2_64to64_s1": (32, 64, 64, 1),
+                                     "c3_64to128_s2": (32, 64, 128, 2), "c4_128to256_s2": (16, 128, 256, 2)}.items():
+        ho = (h + 2 - 3) // st + 1
+        g = hipabi.ConvGeom(256, h, h, cin, ho, ho, cout, 3, 3, st, st, 1, 1, 1, 1, 1)
+        x = torch.randn(256, h, h, cin, device="cuda")
+        w = torch.randn(9 * cin, cout, device="cuda") * (2.0 / (9 * cin)) ** 0.5
+        b = torch.randn(cout, device="cuda") * 0.01
+        y = torch.empty(256, ho, ho, cout, device="cuda")
+        ms, _ = time_launches(lambda: hipabi.check(L.knx_hip_conv(ctypes.byref(g), P(x), P(w), P(b), 0, 0.0, P(y), S)),
+                              steps, warmup)
+        flops = 2.0 * 256 * ho * ho * cout * 9 * cin
+        nbytes = 4 * (x.numel() + w.numel() + cout + y.numel())
+        tf = flops / (ms * 1e-3) / 1e12
+        out[name] = dict(us=round(ms * 1e3, 2), tflops=round(tf, 2), mfma_frac=round(tf / PEAK_F32_TFLOPS, 4),
+                         gbs=round(nbytes / (ms * 1e-3) / 1e9, 1))
+        log(f"conv {name}: {ms * 1e3:.1f} us  {tf:.1f} TFLOP/s  {nbytes / (ms * 1e-3) / 1e9:.0f} GB/s")
+    return out
 
 
 def measured_traffic():
@@ -230,6 +304,9 @@ def main():
             cn = cpu_baseline(g, ncpu, target_s=5.0)
             out["cpu_baseline_all_cores"] = {"value": round(cn["tops"], 4), "unit": "TOPS", "cores": ncpu}
     out["i8gemm_small_m"] = small
+    if not args.no_small:
+        out["row_kernels"] = rows_bench(max(args.steps, 20), args.warmup)
+        out["conv_layers"] = conv_bench(max(args.steps // 4, 10), max(args.warmup // 10, 3))
     if not args.no_forward:
         fw = {}
         st = max(5, args.steps // 5)

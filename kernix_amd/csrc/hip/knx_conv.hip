@@ -63,47 +63,65 @@ __global__ void __launch_bounds__(WM * WN * 64) conv_tile(ConvArgs p)
         six[i] = ox * g.sw - g.pl;
     }
 
-    auto gather = [&](int i, int gk) -> float {
-        if (gk >= K) return 0.0f;
-        const int seg = gk / cg, ci = gk - seg * cg;
-        const int ky = seg / g.kw, kx = seg - ky * g.kw;
+    // The k index of this thread's first gathered element is k0 + kc (kc = 4·(t & 3), the same for every load
+    // slot); its tap (ky, kx) and channel ci are tracked incrementally as k0 advances, so the K loop does no integer
+    // division.
+    const int kc0 = (t & 3) * 4;
+    int tci, tkx, tky;
+    {
+        const int seg = kc0 / cg;
+        tci = kc0 - seg * cg;
+        tky = seg / g.kw;
+        tkx = seg - tky * g.kw;
+    }
+    auto advance = [&](int& ci, int& kx, int& ky, int d) {
+        ci += d;
+        while (ci >= cg) {
+            ci -= cg;
+            if (++kx == g.kw) { kx = 0; ++ky; }
+        }
+    };
+    auto tap = [&](int i, int ci, int kx, int ky) -> const float* {
         const int iy = siy[i] + ky * g.dh, ix = six[i] + kx * g.dw;
-        if (iy < 0 || iy >= g.H || ix < 0 || ix >= g.W) return 0.0f;
-        return p.x[(((size_t)sb[i] * g.H + iy) * g.W + ix) * g.C + cbase + ci];
+        if (iy < 0 || iy >= g.H || ix < 0 || ix >= g.W) return nullptr;
+        return p.x + (((size_t)sb[i] * g.H + iy) * g.W + ix) * g.C + cbase + ci;
     };
 
     float4 ra[LA], rb[LB];
-    auto gload = [&](int k0) {
+    auto gload = [&](int k0) {  // k0: first k of the tile; (tci, tkx, tky) describe k0 + kc0 on entry
+        const int gk = k0 + kc0;
 #pragma unroll
         for (int i = 0; i < LA; ++i) {
-            const int kc = ((i * NT + t) & 3) * 4, gk = k0 + kc;
             float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
             if (sok[i]) {
                 if (VEC) {
                     // cg % 4 == 0: the 4 consecutive k share one (ky, kx) tap and are 4 consecutive channels
                     if (gk < K) {
-                        const int seg = gk / cg, ci = gk - seg * cg;
-                        const int ky = seg / g.kw, kx = seg - ky * g.kw;
-                        const int iy = siy[i] + ky * g.dh, ix = six[i] + kx * g.dw;
-                        if (iy >= 0 && iy < g.H && ix >= 0 && ix < g.W)
-                            v = *reinterpret_cast<const float4*>(p.x + (((size_t)sb[i] * g.H + iy) * g.W + ix) * g.C + cbase + ci);
+                        const float* src = tap(i, tci, tkx, tky);
+                        if (src) v = *reinterpret_cast<const float4*>(src);
                     }
                 } else {
-                    v.x = gather(i, gk);
-                    v.y = gather(i, gk + 1);
-                    v.z = gather(i, gk + 2);
-                    v.w = gather(i, gk + 3);
+                    int ci = tci, kx = tkx, ky = tky;
+                    float e[4];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const float* src = gk + u < K ? tap(i, ci, kx, ky) : nullptr;
+                        e[u] = src ? *src : 0.0f;
+                        advance(ci, kx, ky, 1);
+                    }
+                    v = make_float4(e[0], e[1], e[2], e[3]);
                 }
             }
             ra[i] = v;
         }
+        advance(tci, tkx, tky, BK);
 #pragma unroll
         for (int i = 0; i < LB; ++i) {
             const int idx = i * NT + t, k = idx / (BN / 4), nc = (idx % (BN / 4)) * 4;
-            const int gk = k0 + k, gn = n0 + nc;
+            const int gkb = k0 + k, gn = n0 + nc;
             float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (gk < K) {
-                const float* src = W + (size_t)gk * g.Co + gn;
+            if (gkb < K) {
+                const float* src = W + (size_t)gkb * g.Co + gn;
                 if (b_vec && gn + 3 < N) v = *reinterpret_cast<const float4*>(src);
                 else {
                     if (gn + 0 < N) v.x = src[0];
@@ -219,6 +237,8 @@ extern "C" int knx_hip_conv(const knx_conv_geom* g, const float* x, const float*
     hipStream_t s = knx::as_stream(stream);
     const long tiles = (long)((p.M + 127) / 128) * g->groups;
     if (tiles >= knx::num_cus()) {
+        // narrow outputs: 256 pixels × 64 channels, each wave 64 × 64 (four MFMAs per four fragment reads)
+        if (vec && p.N <= 64 && tiles >= 2L * knx::num_cus()) return launch<256, 64, 4, 1>(p, vec, s, name);
         if (p.N <= 64) return launch<128, 64, 2, 2>(p, vec, s, name);
         return launch<128, 128, 2, 2>(p, vec, s, name);
     }

@@ -984,6 +984,60 @@ __global__ void __launch_bounds__(256) quantize_rows_kernel(const float* __restr
     if (lane == 0) sx[row] = s;
 }
 
+// Register-resident variant (k % 4 == 0, k ≤ 256·NV, 16-byte aligned fp32 rows, 4-byte aligned int8 rows): x is read
+// once with 16-byte loads and four int8 values are written per 32-bit store; same arithmetic as quantize_rows_kernel.
+__device__ __forceinline__ float q4e(const float4& v, int e) { return e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w; }
+
+template <int NV>
+__global__ void __launch_bounds__(256) quantize_rows_vec(const float* __restrict__ x, int ldx, int rows, int k, int kp,
+                                                          int8_t* __restrict__ xq, int ldq, float* __restrict__ sx)
+{
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const float4* xr = reinterpret_cast<const float4*>(x + (size_t)row * ldx);
+    const int nq = k >> 2, nqp = kp >> 2;
+    float4 v[NV];
+    float m = 0.0f;
+    int bad = 0;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int q = i * 64 + lane;
+        v[i] = q < nq ? xr[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float a = fabsf(q4e(v[i], e));
+            if (!(a <= 3.402823466e38f)) bad = 1;  // NaN or ±inf
+            else m = a > m ? a : m;
+        }
+    }
+    m = knx_wave_max(m);
+    bad = __any(bad);
+    int* qr = reinterpret_cast<int*>(xq + (size_t)row * ldq);
+    if (bad) {
+        for (int q = lane; q < nqp; q += 64) qr[q] = 0;
+        if (lane == 0) sx[row] = __int_as_float(0x7fc00000);
+        return;
+    }
+    const float s = m > 0.0f ? __fdiv_rn(m, 127.0f) : 1.0f;
+    const float inv = __fdiv_rn(1.0f, s);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int q = i * 64 + lane;
+        if (q >= nq) continue;
+        unsigned w = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float r = rintf(q4e(v[i], e) * inv);
+            const int b = (int)(r > 127.0f ? 127.0f : r < -127.0f ? -127.0f : r);
+            w |= (unsigned)(b & 0xff) << (8 * e);
+        }
+        qr[q] = (int)w;
+    }
+    for (int q = nq + lane; q < nqp; q += 64) qr[q] = 0;
+    if (lane == 0) sx[row] = s;
+}
+
 // ---- dequantized copy: dst[k][n] = (float)q[n][k] · scale[n], 32×32 tiles transposed through LDS ----
 __global__ void __launch_bounds__(256) dequant_kernel(const int8_t* __restrict__ q, int ldq, const float* __restrict__ scale,
                                                        int K, int N, float* __restrict__ dst)
@@ -1014,8 +1068,17 @@ extern "C" int knx_hip_quantize_rows(const float* x, int ldx, int rows, int k, i
     KNX_REQUIRE(rows >= 0 && k >= 1 && kp >= k && kp % 64 == 0 && ldq >= kp && ldx >= k, name);
     if (rows == 0) return KNX_OK;
     KNX_REQUIRE(x != nullptr && xq != nullptr && sx != nullptr, name);
-    hipLaunchKernelGGL(quantize_rows_kernel, dim3((rows + 3) / 4), dim3(256), 0, knx::as_stream(stream), x, ldx, rows, k,
-                       kp, xq, ldq, sx);
+    hipStream_t st = knx::as_stream(stream);
+    const dim3 grid((rows + 3) / 4), block(256);
+    if (k % 4 == 0 && ldx % 4 == 0 && ((uintptr_t)x & 15) == 0 && ldq % 4 == 0 && ((uintptr_t)xq & 3) == 0 && k <= 4096) {
+        if (k <= 256) hipLaunchKernelGGL(quantize_rows_vec<1>, grid, block, 0, st, x, ldx, rows, k, kp, xq, ldq, sx);
+        else if (k <= 512) hipLaunchKernelGGL(quantize_rows_vec<2>, grid, block, 0, st, x, ldx, rows, k, kp, xq, ldq, sx);
+        else if (k <= 1024) hipLaunchKernelGGL(quantize_rows_vec<4>, grid, block, 0, st, x, ldx, rows, k, kp, xq, ldq, sx);
+        else if (k <= 2048) hipLaunchKernelGGL(quantize_rows_vec<8>, grid, block, 0, st, x, ldx, rows, k, kp, xq, ldq, sx);
+        else hipLaunchKernelGGL(quantize_rows_vec<16>, grid, block, 0, st, x, ldx, rows, k, kp, xq, ldq, sx);
+        return knx::check_launch(name);
+    }
+    hipLaunchKernelGGL(quantize_rows_kernel, grid, block, 0, st, x, ldx, rows, k, kp, xq, ldq, sx);
     return knx::check_launch(name);
 }
 

@@ -55,6 +55,148 @@ __global__ void __launch_bounds__(256) softmax_kernel(const float* __restrict__ 
     for (int j = lane; j < cols; j += 64) yr[j] = expf(xr[j] - m) * inv;
 }
 
+// ---- register-resident row kernels ----
+// G lanes per row (16, 32 or 64), NV float4 per lane: used when cols % 4 == 0, cols ≤ 4·G·NV and the rows are 16-byte
+// aligned.  Each row is read from memory once (16-byte loads) and kept in registers for every pass over it.
+template <int G>
+__device__ __forceinline__ float group_sum(float v)
+{
+#pragma unroll
+    for (int o = G / 2; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+template <int G>
+__device__ __forceinline__ float group_max(float v)
+{
+#pragma unroll
+    for (int o = G / 2; o >= 1; o >>= 1) { const float w = __shfl_xor(v, o, 64); v = w > v ? w : v; }
+    return v;
+}
+__device__ __forceinline__ float f4(const float4& v, int e) { return e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w; }
+
+// layer_norm, same formulas as layernorm_kernel (x may alias y: every lane reads its whole row before writing)
+template <int G, int NV>
+__global__ void __launch_bounds__(256) layernorm_vec(const float* x, float* y, int rows, int cols,
+                                                      const float* __restrict__ gamma, const float* __restrict__ beta,
+                                                      float eps)
+{
+    const int row = blockIdx.x * (256 / G) + (int)threadIdx.x / G, l = threadIdx.x % G;
+    if (row >= rows) return;
+    const float4* xr = reinterpret_cast<const float4*>(x + (size_t)row * cols);
+    const int nq = cols >> 2;
+    float4 v[NV];
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int q = i * G + l;
+        v[i] = q < nq ? xr[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+        s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+    }
+    const float mean = group_sum<G>(s) / (float)cols;
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+        if (i * G + l < nq)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) { const float d = f4(v[i], e) - mean; ss += d * d; }
+    const float rstd = 1.0f / sqrtf(group_sum<G>(ss) / (float)cols + eps);
+    float4* yr = reinterpret_cast<float4*>(y + (size_t)row * cols);
+    const float4* g4 = reinterpret_cast<const float4*>(gamma);  // 16-byte aligned (checked by the caller)
+    const float4* b4 = reinterpret_cast<const float4*>(beta);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int q = i * G + l;
+        if (q >= nq) continue;
+        const float4 gq = gamma ? g4[q] : make_float4(1.f, 1.f, 1.f, 1.f);
+        const float4 bq = beta ? b4[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+        float o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float t = (f4(v[i], e) - mean) * rstd;
+            if (gamma && beta) t = t * f4(gq, e) + f4(bq, e);
+            else if (gamma) t = t * f4(gq, e);
+            else if (beta) t = t + f4(bq, e);
+            o[e] = t;
+        }
+        yr[q] = make_float4(o[0], o[1], o[2], o[3]);
+    }
+}
+
+// softmax, same formulas as softmax_kernel; exp(x − max) is computed once and kept
+template <int G, int NV>
+__global__ void __launch_bounds__(256) softmax_vec(const float* x, float* y, int rows, int cols)
+{
+    const int row = blockIdx.x * (256 / G) + (int)threadIdx.x / G, l = threadIdx.x % G;
+    if (row >= rows) return;
+    const float4* xr = reinterpret_cast<const float4*>(x + (size_t)row * cols);
+    const int nq = cols >> 2;
+    float4 v[NV];
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int q = i * G + l;
+        v[i] = q < nq ? xr[q] : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) m = f4(v[i], e) > m ? f4(v[i], e) : m;
+    }
+    m = group_max<G>(m);
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        if (i * G + l >= nq) continue;
+        v[i] = make_float4(expf(v[i].x - m), expf(v[i].y - m), expf(v[i].z - m), expf(v[i].w - m));
+        s += v[i].x;
+        s += v[i].y;
+        s += v[i].z;
+        s += v[i].w;
+    }
+    const float inv = 1.0f / group_sum<G>(s);
+    float4* yr = reinterpret_cast<float4*>(y + (size_t)row * cols);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int q = i * G + l;
+        if (q < nq) yr[q] = make_float4(v[i].x * inv, v[i].y * inv, v[i].z * inv, v[i].w * inv);
+    }
+}
+
+// picks G and NV for a row of nq float4 (nq ≤ 512) and launches K<G, NV>
+#define KNX_ROWVEC_DISPATCH(K, nq, rows, stream, ...)                                                                \
+    do {                                                                                                            \
+        hipStream_t st_ = knx::as_stream(stream);                                                                   \
+        if ((nq) <= 16) hipLaunchKernelGGL((K<16, 1>), dim3(((rows) + 15) / 16), dim3(256), 0, st_, __VA_ARGS__);   \
+        else if ((nq) <= 32) hipLaunchKernelGGL((K<32, 1>), dim3(((rows) + 7) / 8), dim3(256), 0, st_, __VA_ARGS__); \
+        else if ((nq) <= 64) hipLaunchKernelGGL((K<64, 1>), dim3(((rows) + 3) / 4), dim3(256), 0, st_, __VA_ARGS__); \
+        else if ((nq) <= 128) hipLaunchKernelGGL((K<64, 2>), dim3(((rows) + 3) / 4), dim3(256), 0, st_, __VA_ARGS__); \
+        else if ((nq) <= 256) hipLaunchKernelGGL((K<64, 4>), dim3(((rows) + 3) / 4), dim3(256), 0, st_, __VA_ARGS__); \
+        else hipLaunchKernelGGL((K<64, 8>), dim3(((rows) + 3) / 4), dim3(256), 0, st_, __VA_ARGS__);                \
+    } while (0)
+
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+// ---- bias + activation, 4 consecutive elements per lane (cols % 4 == 0, 16-byte aligned); ACT ≥ −1 compile time ----
+template <int ACT>
+__global__ void __launch_bounds__(256) bias_act_vec(const float* x, float* y, size_t n4, int cols,
+                                                     const float* __restrict__ bias, int act, float alpha)
+{
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    float4* y4 = reinterpret_cast<float4*>(y);
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (size_t)gridDim.x * blockDim.x) {
+        float4 v = x4[i];
+        if (bias) {
+            const float4 b = *reinterpret_cast<const float4*>(bias + (i * 4) % cols);
+            v = make_float4(v.x + b.x, v.y + b.y, v.z + b.z, v.w + b.w);
+        }
+        if (ACT == -2) v = make_float4(knx_act(v.x, act, alpha), knx_act(v.y, act, alpha), knx_act(v.z, act, alpha),
+                                       knx_act(v.w, act, alpha));
+        else if (ACT >= 0) v = make_float4(knx_act(v.x, ACT, alpha), knx_act(v.y, ACT, alpha), knx_act(v.z, ACT, alpha),
+                                           knx_act(v.w, ACT, alpha));
+        y4[i] = v;
+    }
+}
+
+// ---- same-shape binary (no broadcast), 4 elements per lane ----
+__global__ void __launch_bounds__(256) binary_vec(int op, const float* a, const float* b, float* y, size_t n4);
+
 // ---- bias + activation: reference include/kernix_model.h:528-541 ----
 __global__ void __launch_bounds__(256) bias_act_kernel(const float* x, float* y, size_t n, int cols,
                                                         const float* __restrict__ bias, int act, float alpha)
@@ -79,6 +221,17 @@ __device__ __forceinline__ float bin1(int op, float a, float b)
     }
 }
 
+__global__ void __launch_bounds__(256) binary_vec(int op, const float* a, const float* b, float* y, size_t n4)
+{
+    const float4* a4 = reinterpret_cast<const float4*>(a);
+    const float4* b4 = reinterpret_cast<const float4*>(b);
+    float4* y4 = reinterpret_cast<float4*>(y);
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (size_t)gridDim.x * blockDim.x) {
+        const float4 u = a4[i], w = b4[i];
+        y4[i] = make_float4(bin1(op, u.x, w.x), bin1(op, u.y, w.y), bin1(op, u.z, w.z), bin1(op, u.w, w.w));
+    }
+}
+
 __global__ void __launch_bounds__(256) binary_kernel(int op, const float* a, int ra, int ca, const float* b, int rb, int cb,
                                                       float* y, size_t n, int R, int C)
 {
@@ -99,7 +252,16 @@ __global__ void __launch_bounds__(256) global_pool_kernel(int type, const float*
         const size_t b = i / C, c = i % C;
         const float* xp = x + b * (size_t)R * C + c;
         float o = xp[0];
-        for (int r = 1; r < R; ++r) {
+        int r = 1;
+        // eight loads in flight, combined in row order (the reference's sequential order)
+        for (; r + 8 <= R; r += 8) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = xp[(size_t)(r + u) * C];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) o = type == 0 ? (o > v[u] ? o : v[u]) : o + v[u];
+        }
+        for (; r < R; ++r) {
             const float v = xp[(size_t)r * C];
             o = type == 0 ? (o > v ? o : v) : o + v;
         }
@@ -278,6 +440,10 @@ extern "C" int knx_hip_layernorm(const float* x, float* y, int rows, int cols, c
     KNX_REQUIRE(rows >= 0 && cols >= 1, name);
     if (rows == 0) return KNX_OK;
     KNX_REQUIRE(x && y, name);
+    if (cols % 4 == 0 && cols / 4 <= 512 && aligned16(x) && aligned16(y) && aligned16(gamma) && aligned16(beta)) {
+        KNX_ROWVEC_DISPATCH(layernorm_vec, cols / 4, rows, stream, x, y, rows, cols, gamma, beta, eps);
+        return knx::check_launch(name);
+    }
     KNX_LAUNCH(name, layernorm_kernel, (rows + 3) / 4, x, y, rows, cols, gamma, beta, eps);
 }
 
@@ -288,6 +454,10 @@ extern "C" int knx_hip_softmax(const float* x, float* y, int rows, int cols, voi
     KNX_REQUIRE(rows >= 0 && cols >= 1, name);
     if (rows == 0) return KNX_OK;
     KNX_REQUIRE(x && y, name);
+    if (cols % 4 == 0 && cols / 4 <= 512 && aligned16(x) && aligned16(y)) {
+        KNX_ROWVEC_DISPATCH(softmax_vec, cols / 4, rows, stream, x, y, rows, cols);
+        return knx::check_launch(name);
+    }
     KNX_LAUNCH(name, softmax_kernel, (rows + 3) / 4, x, y, rows, cols);
 }
 
@@ -300,6 +470,14 @@ extern "C" int knx_hip_bias_act(const float* x, float* y, int rows, int cols, co
     const size_t n = (size_t)rows * cols;
     if (n == 0) return KNX_OK;
     KNX_REQUIRE(x && y, name);
+    if (cols % 4 == 0 && aligned16(x) && aligned16(y) && (bias == nullptr || aligned16(bias))) {
+        const size_t n4 = n / 4;
+        // activation ids of the file format: 0 relu, 1 gelu
+        if (act == 0) KNX_LAUNCH(name, bias_act_vec<0>, grid_for(n4), x, y, n4, cols, bias, act, alpha);
+        if (act == 1) KNX_LAUNCH(name, bias_act_vec<1>, grid_for(n4), x, y, n4, cols, bias, act, alpha);
+        if (act == -1) KNX_LAUNCH(name, bias_act_vec<-1>, grid_for(n4), x, y, n4, cols, bias, act, alpha);
+        KNX_LAUNCH(name, bias_act_vec<-2>, grid_for(n4), x, y, n4, cols, bias, act, alpha);
+    }
     KNX_LAUNCH(name, bias_act_kernel, grid_for(n), x, y, n, cols, bias, act, alpha);
 }
 
@@ -313,6 +491,8 @@ extern "C" int knx_hip_binary(int op, const float* a, int ra, int ca, const floa
     const size_t n = (size_t)B * R * C;
     if (n == 0) return KNX_OK;
     KNX_REQUIRE(a && b && y, name);
+    if (ra == R && rb == R && ca == C && cb == C && n % 4 == 0 && aligned16(a) && aligned16(b) && aligned16(y))
+        KNX_LAUNCH(name, binary_vec, grid_for(n / 4), op, a, b, y, n / 4);
     KNX_LAUNCH(name, binary_kernel, grid_for(n), op, a, ra, ca, b, rb, cb, y, n, R, C);
 }
 

@@ -8,6 +8,14 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
+# PyTorch-ROCm ships its own HIP runtime (same soname as the system one that libkernix.so links).  Loading torch
+# before any test module loads libkernix.so makes both use torch's copy; the other order leaves torch on the system
+# runtime, and the first HIP call of the library then finds no device.
+try:
+    import torch  # noqa: F401
+except Exception:  # pragma: no cover
+    pass
+
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU; run with -m gpu")

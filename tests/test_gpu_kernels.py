@@ -117,7 +117,7 @@ def test_i8gemm_rejects_bad_shapes(L):
 
 
 # ---------------------------------------------------------------- quantize rows
-@pytest.mark.parametrize("rows,k", [(1, 1), (3, 55), (32, 114), (4, 784), (2, 4096)])
+@pytest.mark.parametrize("rows,k", [(1, 1), (3, 55), (32, 114), (4, 784), (2, 4096), (3, 512), (5, 2048), (4, 4100)])
 def test_quantize_rows_bit_exact(L, rows, k):
     rng = np.random.default_rng(rows * 31 + k)
     x = (rng.integers(0, 2001, (rows, k)) * 0.003 - 3.0).astype(np.float32)
@@ -162,28 +162,38 @@ def test_sgemm_ep(L, M, N, K, act):
 
 
 # ---------------------------------------------------------------- rows / elementwise
-@pytest.mark.parametrize("rows,cols", [(1, 1), (7, 10), (64, 512), (300, 2048), (5, 9000)])
+# scalar kernels (cols % 4 != 0 or > 2048) and every register-resident shape (16/32/64 lanes per row, 1–8 float4)
+@pytest.mark.parametrize("rows,cols", [(1, 1), (7, 10), (64, 512), (300, 2048), (5, 9000), (9, 12), (17, 60),
+                                       (33, 128), (20, 256), (3, 1024), (6, 1000)])
 def test_layernorm_softmax(L, rows, cols):
     rng = np.random.default_rng(rows + cols)
     x = rng.standard_normal((rows, cols)).astype(np.float32) * 3
+    if cols >= 4:
+        x[0, cols // 2:] = -np.inf if rows > 1 else x[0, cols // 2:]  # masked positions of a causal row
     g = (1 + rng.normal(0, 0.5, cols)).astype(np.float32)
     bt = rng.normal(0, 0.5, cols).astype(np.float32)
     dx, dg, dbt = dev(x), dev(g), dev(bt)
     y = torch.empty_like(dx)
+    fin = np.isfinite(x).all(axis=1)  # layer_norm over finite rows only
     hipabi.check(L.knx_hip_layernorm(ptr(dx), ptr(y), rows, cols, ptr(dg), ptr(dbt), 1e-5, hipabi.stream()))
-    assert rel_err(host(y), knx_ref.layernorm(x, g, bt, 1e-5)) <= 1e-5
+    assert rel_err(host(y)[fin], knx_ref.layernorm(x[fin], g, bt, 1e-5)) <= 1e-5
+    xf = torch.from_numpy(np.ascontiguousarray(x[fin])).cuda()
+    hipabi.check(L.knx_hip_layernorm(ptr(xf), ptr(xf), int(fin.sum()), cols, None, None, 1e-5, hipabi.stream()))
+    assert rel_err(host(xf), knx_ref.layernorm(x[fin], None, None, 1e-5)) <= 1e-5  # in place, no affine
     hipabi.check(L.knx_hip_softmax(ptr(dx), ptr(dx), rows, cols, hipabi.stream()))  # in place
     assert rel_err(host(dx), knx_ref.softmax(x)) <= 1e-5
 
 
-@pytest.mark.parametrize("act", list(range(16)))
-def test_bias_act_all_activations(L, act):
-    rng = np.random.default_rng(act)
-    x = (rng.standard_normal((33, 70)) * 4).astype(np.float32)
-    b = rng.normal(0, 1, 70).astype(np.float32)
-    want = knx_ref.act((x + b).astype(np.float32), act, 0.2)
+@pytest.mark.parametrize("act", list(range(-1, 16)))
+@pytest.mark.parametrize("cols", [70, 72])  # scalar kernel, 4-wide kernel
+def test_bias_act_all_activations(L, act, cols):
+    rng = np.random.default_rng(act + 100 * cols)
+    x = (rng.standard_normal((33, cols)) * 4).astype(np.float32)
+    b = rng.normal(0, 1, cols).astype(np.float32)
+    xb = (x + b).astype(np.float32)
+    want = xb if act == -1 else knx_ref.act(xb, act, 0.2)
     dx, db = dev(x), dev(b)
-    hipabi.check(L.knx_hip_bias_act(ptr(dx), ptr(dx), 33, 70, ptr(db), act, 0.2, hipabi.stream()))
+    hipabi.check(L.knx_hip_bias_act(ptr(dx), ptr(dx), 33, cols, ptr(db), act, 0.2, hipabi.stream()))
     got = host(dx)
     assert np.allclose(got, want, rtol=2e-6, atol=2e-6, equal_nan=True)
 
@@ -201,14 +211,15 @@ def test_binary_broadcast_and_pool(L):
             da, db = dev(a), dev(b)
             hipabi.check(L.knx_hip_binary(op, ptr(da), ra, ca, ptr(db), rb, cb, ptr(y), B, R, C, hipabi.stream()))
             assert np.array_equal(host(y), want)
-    x = rng.normal(0, 1, (4 * 64, 256)).astype(np.float32)
-    for t in (0, 1):
-        want = np.zeros((4, 256), np.float32)
-        knx_ref.lib().ko_global_pool(t, knx_ref._p(x), 4, 64, 256, knx_ref._p(want))
-        y = torch.empty((4, 256), dtype=torch.float32, device="cuda")
-        dx = dev(x)
-        hipabi.check(L.knx_hip_global_pool(t, ptr(dx), 4, 64, 256, ptr(y), hipabi.stream()))
-        assert np.array_equal(host(y), want)
+    for R in (64, 13, 1):  # whole groups of eight rows, a remainder, a single row
+        x = rng.normal(0, 1, (4 * R, 256)).astype(np.float32)
+        for t in (0, 1):
+            want = np.zeros((4, 256), np.float32)
+            knx_ref.lib().ko_global_pool(t, knx_ref._p(x), 4, R, 256, knx_ref._p(want))
+            y = torch.empty((4, 256), dtype=torch.float32, device="cuda")
+            dx = dev(x)
+            hipabi.check(L.knx_hip_global_pool(t, ptr(dx), 4, R, 256, ptr(y), hipabi.stream()))
+            assert np.array_equal(host(y), want)
 
 
 # ---------------------------------------------------------------- convolution
@@ -221,6 +232,9 @@ CONV_CASES = [
     (1, 9, 7, 6, 6, 3, 1, 1, 2, 2),
     (3, 5, 5, 8, 12, 1, 1, 0, 1, 1),
     (2, 11, 13, 5, 7, 2, 3, 0, 1, 1),
+    # enough output pixels for the 256 × 64 tile (≥ 512 tiles of 128 on 256 CUs), channel-vector and scalar gathers
+    (64, 32, 32, 64, 64, 3, 1, 1, 1, 1),
+    (65, 32, 32, 3, 64, 3, 1, 1, 1, 1),
 ]
 
 
