@@ -23,7 +23,8 @@
  * Differences that a caller can observe (all deliberate):
  *   - the default workspace limit is KERNIX_WORKSPACE_LIMIT = 1 GiB of device memory (reference: 64 MB of host memory);
  *   - ws_fixed counts only the dequantized int8 copies: convolution is an implicit GEMM and has no im2col buffer;
- *   - steps[i].buf, .tmp[] and .deq point at device memory.
+ *   - steps[i].buf, .tmp[] and .deq point at device memory; .deq holds the weight transposed (out × in, the
+ *     device layout of every fp32 Linear weight: both GEMM operands K-contiguous).
  */
 #ifndef KERNIX_MODEL_H
 #define KERNIX_MODEL_H

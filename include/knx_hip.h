@@ -12,8 +12,9 @@
  *   knx_hip_quantize_rows   per-row int8 input quantization of kernix_qmatmul   include/kernix_model.h:112-142
  *   knx_hip_i8gemm          int32 sdot accumulation + dequant/bias epilogue     include/kernix_model.h:143-178
  *                           with the activation pass fused                      include/kernix_model.h:1854-1856
- *   knx_hip_dequant         kernix_qweight_unpack into the fp32 copy            include/kernix_model.h:91-95, :1616-1622
- *   knx_hip_sgemm_ep        kernix_matmul_ep_into (MPS+AMX row split)          src/kernix_metal.m:161-265,
+ *   knx_hip_dequant(_t)     kernix_qweight_unpack into the fp32 copy            include/kernix_model.h:91-95, :1616-1622
+ *   knx_hip_sgemm_ep /      kernix_matmul_ep_into (MPS+AMX row split)          src/kernix_metal.m:161-265,
+ *   knx_hip_sgemm_nt_ep
  *                           + kernix_bias_act epilogue                          include/kernix.h:951-977,
  *                                                                               include/kernix_model.h:528-550
  *   knx_hip_conv            kernix_conv_run (im2col → sgemm → bias_act)         include/kernix_model.h:711-771
@@ -85,12 +86,18 @@ KNX_API int knx_hip_i8gemm(int M, int N, int K, const int8_t* A, int lda, const 
 
 /* dst (K×N row-major fp32) = (float)q[n][k] · scale[n]; q is N×K int8 with row stride ldq bytes. */
 KNX_API int knx_hip_dequant(const int8_t* q, int ldq, const float* scale, int K, int N, float* dst, void* stream);
+/* dst (N×K row-major fp32, the layout of the fp32 weights used with knx_hip_sgemm_nt_ep) = (float)q[n][k] · scale[n]. */
+KNX_API int knx_hip_dequant_t(const int8_t* q, int ldq, const float* scale, int K, int N, float* dst, void* stream);
 
 /* ---- fp32 GEMM ---- */
 /* C = act(A·W + bias): A M×K (stride lda), W K×N row-major (stride ldw), C M×N (stride ldc), all fp32.
  * K may be 0 (then C = act(bias)). */
 KNX_API int knx_hip_sgemm_ep(int M, int N, int K, const float* A, int lda, const float* W, int ldw,
                              const float* bias, int act, float alpha, float* C, int ldc, void* stream);
+/* Same with the weight stored transposed: Wt N×K row-major (stride ldwt ≥ K), the device layout of Linear weights
+ * (both GEMM operands K-contiguous, as in kernix_matmul_ep_into with a transposed B, include/kernix.h:951-977). */
+KNX_API int knx_hip_sgemm_nt_ep(int M, int N, int K, const float* A, int lda, const float* Wt, int ldwt,
+                                const float* bias, int act, float alpha, float* C, int ldc, void* stream);
 
 /* ---- convolution (NHWC, groups, dilation, zero padding) ---- */
 typedef struct {

@@ -17,7 +17,7 @@
 #include <string>
 #include <type_traits>
 
-#include "knx_common.hpp"
+#include "knx_pipe.hpp"
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
@@ -228,15 +228,6 @@ __global__ void __launch_bounds__(WM * WN * 64) i8gemm_tile(I8Args p)
 // in flight while one is multiplied.  Each load instruction fills 1 KB of LDS = 16 rows × 64 bytes; lane l fetches
 // the global 16-byte chunk (l & 3) ^ swz(row), which realizes the swizzled layout with fully coalesced loads.
 // Rows past M (or N) are clamped to the last row: they only feed output rows/columns that are never stored.
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
-typedef __attribute__((address_space(1))) const void* gbl_ptr_t;
-
-// s_waitcnt vmcnt(n) lgkmcnt(0) (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] = 7 | lgkmcnt[11:8] | vmcnt[5:4] << 14):
-// at most n vector-memory ops (LDS-DMA loads) of this wave outstanding and all of its LDS accesses retired.
-#define KNX_WAIT_VM_LDS(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (0 << 8) | ((((n) >> 4) & 3) << 14))
-
-// s_waitcnt lgkmcnt(0): all LDS accesses of this wave retired (vmcnt left unconstrained at 63).
-#define KNX_WAIT_LDS() __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14))
 #define KERNIX_ACT_RELU_ID 0
 
 // Writes the 16 staged rows [mt0, mt0+16) of a tile: 4 consecutive columns per lane, one 16-byte store per row.
@@ -285,31 +276,6 @@ __device__ __forceinline__ void store_rows(const I8Args& p, const int* stg, cons
             for (int q = 0; q < 4; ++q)
                 if (nb + q >= nlo && nb + q < p.N) i8_epilogue(p, m, nb + q, a[q]);
         }
-    }
-}
-
-// Workgroup barrier without a memory fence.  A fence (e.g. __syncthreads) would wait for every outstanding LDS-DMA
-// load, which empties the prefetch ring; the caller instead waits precisely with KNX_WAIT_VM_LDS.  The empty asm
-// statements keep the compiler from moving any memory access across the barrier.
-__device__ __forceinline__ void knx_barrier_nofence()
-{
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-}
-
-// Tile order: consecutive workgroups go to consecutive XCDs (8 on MI355X); when the tile grid splits evenly, each
-// XCD gets one contiguous (tiles_m/2) × (tiles_n/4) block so the A and W rows it reads stay in its own L2.
-__device__ __forceinline__ void tile_of(int t, int tiles_m, int tiles_n, int& tm, int& tn)
-{
-    if ((tiles_m & 1) == 0 && (tiles_n & 3) == 0 && tiles_m * tiles_n >= 64) {
-        const int x = t & 7, j = t >> 3;
-        const int bm = tiles_m >> 1, bn = tiles_n >> 2;
-        tm = (x >> 2) * bm + j / bn;
-        tn = (x & 3) * bn + j % bn;
-    } else {
-        tm = t / tiles_n;
-        tn = t % tiles_n;
     }
 }
 
@@ -521,19 +487,6 @@ int launch_pipe(I8Args p, hipStream_t s, const char* name)
 // (row-in-slot · ld + chunk).  A tile that would run past M (or N) is moved back to end at row M (column N): it
 // recomputes a few rows of its neighbour and stores only the rows (columns) it owns, so every operand row it reads
 // exists.  A half k-tile at the end (K % 128 == 64) loads its lower 64 bytes twice and multiplies two k-steps only.
-__device__ __forceinline__ int swz8(int row) { return (row ^ (row >> 3)) & 7; }
-
-// LDS-DMA load of 16 bytes per lane, global (base + voff) → LDS (dst + 16·lane), with base and dst wave-uniform.
-// Inline assembly, so that the compiler does not treat it as an LDS store: it cannot tell the two stages apart and
-// would make every later LDS read wait for all outstanding loads.  The loads are waited for explicitly (vmcnt) and
-// published with a workgroup barrier; the compiler's own vmcnt waits stay correct, only stricter (vmcnt retires
-// loads in order, so loads it does not know about only add younger entries).
-__device__ __forceinline__ void dma16(const int8_t* base, unsigned voff, int8_t* dst)
-{
-    const unsigned l = (unsigned)(uintptr_t)(lds_ptr_t)dst;
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(l), "v"(voff), "s"(base) : "memory");
-}
-
 template <int BM, int BN, int WM, int WN>
 __global__ void __launch_bounds__(WM * WN * 64) i8gemm_k128(I8Args p)
 {
@@ -1058,6 +1011,31 @@ __global__ void __launch_bounds__(256) dequant_kernel(const int8_t* __restrict__
     }
 }
 
+// ---- dequantized copy, weight-transposed: dst[n][k] = (float)q[n][k] · scale[n] (4 elements per lane) ----
+__global__ void __launch_bounds__(256) dequant_t_kernel(const int8_t* __restrict__ q, int ldq, const float* __restrict__ scale,
+                                                         int K, int N, float* __restrict__ dst)
+{
+    const size_t n4 = (size_t)N * (K / 4);
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (size_t)gridDim.x * blockDim.x) {
+        const int n = (int)(i / (K / 4)), k = (int)(i % (K / 4)) * 4;
+        const int w = *reinterpret_cast<const int*>(q + (size_t)n * ldq + k);
+        const float s = scale[n];
+        *reinterpret_cast<float4*>(dst + (size_t)n * K + k) =
+            make_float4((float)(int8_t)(w & 0xff) * s, (float)(int8_t)((w >> 8) & 0xff) * s,
+                        (float)(int8_t)((w >> 16) & 0xff) * s, (float)(int8_t)((w >> 24) & 0xff) * s);
+    }
+}
+
+__global__ void __launch_bounds__(256) dequant_t_scalar(const int8_t* __restrict__ q, int ldq, const float* __restrict__ scale,
+                                                         int K, int N, float* __restrict__ dst)
+{
+    const size_t n = (size_t)N * K;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        const int r = (int)(i / K), k = (int)(i % K);
+        dst[i] = (float)q[(size_t)r * ldq + k] * scale[r];
+    }
+}
+
 }  // namespace
 
 extern "C" int knx_hip_quantize_rows(const float* x, int ldx, int rows, int k, int kp, int8_t* xq, int ldq, float* sx,
@@ -1130,6 +1108,26 @@ extern "C" int knx_hip_i8gemm(int M, int N, int K, const int8_t* A, int lda, con
     const long tiles128 = (long)((M + 127) / 128) * ((N + 127) / 128);
     if (tiles128 >= knx::num_cus() && k128_fits<128, 128>(p)) return launch_k128<128, 128, 2, 2>(p, s, name);
     return launch_pipe<64, 64, 2, 2, 4>(p, s, name);
+}
+
+extern "C" int knx_hip_dequant_t(const int8_t* q, int ldq, const float* scale, int K, int N, float* dst, void* stream)
+{
+    const char* name = "knx_hip_dequant_t";
+    KNX_ENTRY(name);
+    KNX_REQUIRE(K >= 0 && N >= 0 && ldq >= K, name);
+    if (K == 0 || N == 0) return KNX_OK;
+    KNX_REQUIRE(q != nullptr && scale != nullptr && dst != nullptr, name);
+    const size_t cap = (size_t)knx::num_cus() * 16;
+    if (K % 4 == 0 && ldq % 4 == 0 && ((uintptr_t)q & 3) == 0 && ((uintptr_t)dst & 15) == 0) {
+        const size_t n4 = (size_t)N * (K / 4), g = (n4 + 255) / 256;
+        hipLaunchKernelGGL(dequant_t_kernel, dim3((unsigned)(g < cap ? g : cap)), dim3(256), 0, knx::as_stream(stream), q, ldq,
+                           scale, K, N, dst);
+    } else {
+        const size_t n = (size_t)N * K, g = (n + 255) / 256;
+        hipLaunchKernelGGL(dequant_t_scalar, dim3((unsigned)(g < cap ? g : cap)), dim3(256), 0, knx::as_stream(stream), q, ldq,
+                           scale, K, N, dst);
+    }
+    return knx::check_launch(name);
 }
 
 extern "C" int knx_hip_dequant(const int8_t* q, int ldq, const float* scale, int K, int N, float* dst, void* stream)

@@ -4,11 +4,20 @@
 // pass (reference src/kernix_metal.m:161-265, include/kernix.h:951-977, include/kernix_model.h:528-550):
 // every output tile is computed by one workgroup and leaves the chip already biased and activated.
 //
-// Tile: BM×BN per workgroup of WM×WN waves, K streamed in 16-float k-tiles through double-buffered LDS.  Both tiles
-// are stored k-major in LDS (As[k][m], Bs[k][n]) so each MFMA operand read is 32 consecutive floats per half-wave.
-// A is M×K row-major; B is K×N row-major (NN, Linear weights as stored in .knx) or N×K row-major (NT, attention
-// keys).  An optional batch index (grid.y) with two-level strides serves the per-(batch, head) attention GEMMs.
-#include "knx_common.hpp"
+// Two kernels:
+//   sgemm_k32   the pipelined kernel for both operands K-contiguous (A M×K, Bt N×K: the device layout of Linear and
+//               attention weights), K % 32 == 0, tiles that fill the chip (256×256 with 8 waves or 128×128 with 4):
+//               128-byte k-tiles moved HBM → LDS by global_load_lds, as the int8 GEMM does;
+//   sgemm_tile  the general kernel (any shape, B K×N or N×K): BM×BN per workgroup of WM×WN waves, K streamed in
+//               16-float k-tiles through double-buffered LDS, both tiles stored k-major (As[k][m], Bs[k][n]) so each
+//               MFMA operand read is 32 consecutive floats per half-wave.  An optional batch index (grid.y) with
+//               two-level strides serves the per-(batch, head) attention GEMMs.
+#include <stdlib.h>
+#include <string.h>
+
+#include <type_traits>
+
+#include "knx_pipe.hpp"
 
 typedef float v16f __attribute__((ext_vector_type(16)));
 
@@ -28,6 +37,7 @@ struct SgArgs {
     float alpha;   // C = alpha·(A·B) before bias
     int causal;    // C[i][j] = −inf for j > i (attention scores)
     int tiles_n;
+    int tiles_m;
     int zh;        // batch index z = zb·zh + zi
     long long sAb, sAh, sBb, sBh, sCb, sCh;
 };
@@ -199,6 +209,227 @@ int dispatch(SgArgs p, int batch, hipStream_t s, const char* name)
     return launch<64, 64, 2, 2, TB>(p, batch, s, name);
 }
 
+// ---------------------------------------------------------------- pipelined fp32 GEMM, K-contiguous operands
+// C = act(alpha·A·Btᵀ + bias) with A M×K and Bt N×K row-major, K % 32 == 0: the int8 128-byte k-tile pipeline applied
+// to fp32.  Each 128-byte k-tile (32 floats) of every operand row moves HBM → LDS with global_load_lds_dwordx4 into
+// one of two stages, 16-byte chunks swizzled per row (chunk c of row r at c ^ swz8(r)).  K order inside a k-tile:
+// lanes 0-31 take floats 0-15 and lanes 32-63 floats 16-31, one per v_mfma_f32_32x32x2_f32 k-step, so a lane reads
+// its 16 operand values of a k-tile as four 16-byte chunks ("quads" of four k-steps).  Tiles that would cross M or N
+// are moved back inside and store only what they own.
+template <int BM, int BN, int WM, int WN>
+__global__ void __launch_bounds__(WM * WN * 64) sgemm_k32(SgArgs p)
+{
+    constexpr int NW = WM * WN;
+    constexpr int TM = BM / WM, TN = BN / WN;
+    constexpr int FM = TM / 32, FN = TN / 32;
+    constexpr int ROWS = BM + BN;
+    constexpr int STAGE = ROWS * 128;
+    constexpr int SLOTS = ROWS / 8 / NW;
+    constexpr int SA = BM / 8 / NW;
+    static_assert(BM % (8 * NW) == 0 && BN % (8 * NW) == 0, "load split");
+    static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile");
+    static_assert(NW * 16 * (TN + 4) * 4 <= 2 * STAGE, "staging fits in the stages");
+    __shared__ __attribute__((aligned(16))) int8_t lds[2 * STAGE];
+
+    const int t = threadIdx.x, lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int wm = wave / WN, wn = wave % WN;
+    int tm, tn;
+    tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+    const int mlo = tm * BM, nlo = tn * BN;
+    const int m0 = min(mlo, p.M - BM), n0 = min(nlo, p.N - BN);
+    const int z = blockIdx.y, zb = z / p.zh, zi = z % p.zh;
+    const float* A = p.A + zb * p.sAb + zi * p.sAh;
+    const float* B = p.B + zb * p.sBb + zi * p.sBh;
+    float* C = p.C + zb * p.sCb + zi * p.sCh;
+
+    const int8_t* tile_a = reinterpret_cast<const int8_t*>(A + (size_t)m0 * p.lda);
+    const int8_t* tile_b = reinterpret_cast<const int8_t*>(B + (size_t)n0 * p.ldb);
+    const int lda4 = p.lda * 4, ldb4 = p.ldb * 4;  // row strides in bytes
+    const int cl = (lane & 7) ^ (lane >> 3), rs = lane >> 3;
+    const int nk = p.K / 32;
+    auto issue1 = [&](int kt, int i) {
+        const int slot = i * NW + wave;
+        const bool a = i < SA;
+        const int ld = a ? lda4 : ldb4;
+        const int chunk = cl ^ (slot & 7);
+        const int8_t* base = (a ? tile_a + (size_t)(slot * 8) * ld : tile_b + (size_t)(slot * 8 - BM) * ld) + kt * 128;
+        dma16(base, (unsigned)(rs * ld + chunk * 16), lds + (kt & 1) * STAGE + slot * 1024);
+    };
+
+    // fragment offsets: row r + 32·f has swizzle swz8(r) ^ 4·(f & 1), i.e. the chunk of half-wave g ^ (f & 1)
+    const int rl = lane & 31, g = lane >> 5;
+    int aoff[2][4], boff[2][4];
+    {
+        const int ra = wm * TM + rl, rb = BM + wn * TN + rl;
+        const int sa_ = swz8(ra), sb_ = swz8(rb);
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                aoff[h][c] = ra * 128 + (((4 * (g ^ h) + c) ^ sa_) << 4);
+                boff[h][c] = rb * 128 + (((4 * (g ^ h) + c) ^ sb_) << 4);
+            }
+    }
+    float4 fa[2][FM], fb[2][FN];
+    auto read1 = [&](int kt, int q, int j) {  // fragment j (A if j < FM) of quad q
+        const int8_t* cur = lds + (kt & 1) * STAGE;
+        if (j < FM) fa[q & 1][j] = *(const float4*)(cur + aoff[j & 1][q] + j * 4096);
+        else fb[q & 1][j - FM] = *(const float4*)(cur + boff[(j - FM) & 1][q] + (j - FM) * 4096);
+    };
+    v16f acc[FM][FN];
+#pragma unroll
+    for (int fi = 0; fi < FM; ++fi)
+#pragma unroll
+        for (int fj = 0; fj < FN; ++fj)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[fi][fj][e] = 0.0f;
+    auto mfma1 = [&](int q, int j) {  // multiply j of quad q: k-step j / (FM·FN), block j % (FM·FN)
+        const int s = j / (FM * FN), b = j % (FM * FN), fi = b / FN, fj = b % FN;
+        acc[fi][fj] = __builtin_amdgcn_mfma_f32_32x32x2f32((&fa[q & 1][fi].x)[s], (&fb[q & 1][fj].x)[s], acc[fi][fj], 0, 0, 0);
+    };
+
+    // One k-tile, as in the int8 kernel with quads in place of k-steps: quads 0..2 multiply set q & 1 while the
+    // fragments of quad q+1 are read; before quad 3's remaining multiplies the wave waits for its loads of tile kt+1
+    // and its own LDS reads, then the barrier hands stage kt & 1 over to the loads of tile kt+2.
+    constexpr int NM = 4 * FM * FN, NR = FM + FN, PRE = NM / 4;
+    constexpr int GAPS = NM - PRE;
+    auto ktile = [&](int kt, auto ARRIVE, auto ISSUE) {
+        constexpr bool arrive = decltype(ARRIVE)::value, iss = decltype(ISSUE)::value;
+#pragma unroll
+        for (int q = 0; q < 3; ++q) {
+#pragma unroll
+            for (int j = 0; j < NR; ++j) read1(kt, q + 1, j);
+#pragma unroll
+            for (int j = 0; j < NM; ++j) mfma1(q, j);
+#pragma unroll
+            for (int j = 0; j < NR; ++j) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, NM - NR, 0);
+        }
+        if (!arrive) {
+#pragma unroll
+            for (int j = 0; j < NM; ++j) mfma1(3, j);
+            return;
+        }
+#pragma unroll
+        for (int j = 0; j < PRE; ++j) mfma1(3, j);
+        __builtin_amdgcn_sched_barrier(0);
+        KNX_WAIT_VM_LDS(0);
+        knx_barrier_nofence();
+        int r = 0, l = 0;
+#pragma unroll
+        for (int j = PRE; j < NM; ++j) {
+            mfma1(3, j);
+            const int rupto = (NR * (j - PRE + 1) + GAPS - 1) / GAPS;
+            while (r < rupto) read1(kt + 1, 0, r++);
+            if (iss) {
+                const int upto = (SLOTS * (j - PRE + 1) + GAPS - 1) / GAPS;
+                while (l < upto) issue1(kt + 2, l++);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    using yes = std::integral_constant<bool, true>;
+    using no = std::integral_constant<bool, false>;
+#pragma unroll
+    for (int i = 0; i < SLOTS; ++i) issue1(0, i);
+    KNX_WAIT_VM_LDS(0);
+    knx_barrier_nofence();
+    if (nk > 1)
+#pragma unroll
+        for (int i = 0; i < SLOTS; ++i) issue1(1, i);
+#pragma unroll
+    for (int j = 0; j < NR; ++j) read1(0, 0, j);
+    int kt = 0;
+    for (; kt < nk - 2; ++kt) ktile(kt, yes{}, yes{});
+    if (nk >= 2) ktile(kt++, yes{}, no{});
+    ktile(kt, no{}, no{});
+
+    // Epilogue: each wave stages 16 rows × TN of its accumulators at a time in its own LDS region (row stride TN+4),
+    // then every lane writes 4 consecutive columns of a row with one 16-byte store.
+    constexpr int SROW = TN + 4, LPR = TN / 4, RPI = 64 / LPR;
+    float* stg = reinterpret_cast<float*>(lds) + wave * 16 * SROW;
+    const int cq = (lane % LPR) * 4, rq = lane / LPR;
+    const int nb = n0 + wn * TN + cq;
+    float bv[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) bv[q] = p.bias ? p.bias[nb + q] : 0.0f;
+    const bool vec = nb >= nlo && (p.ldc & 3) == 0 && ((uintptr_t)C & 15) == 0;
+    KNX_WAIT_LDS();
+    knx_barrier_nofence();  // nobody reads the operand stages any more
+#pragma unroll
+    for (int fi = 0; fi < FM; ++fi) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int fj = 0; fj < FN; ++fj)
+#pragma unroll
+                for (int e = 8 * h; e < 8 * h + 8; ++e)
+                    stg[(8 * ((e >> 2) - 2 * h) + 4 * g + (e & 3)) * SROW + fj * 32 + rl] = acc[fi][fj][e];
+            KNX_WAIT_LDS();
+            asm volatile("" ::: "memory");
+            for (int rr = rq; rr < 16; rr += RPI) {
+                const int m = m0 + wm * TM + fi * 32 + 16 * h + rr;
+                if (m < mlo) continue;
+                const float4 a = *reinterpret_cast<const float4*>(&stg[rr * SROW + cq]);
+                float r[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    float v = (&a.x)[q];
+                    if (p.alpha != 1.0f) v = p.alpha * v;
+                    if (p.bias) v = v + bv[q];
+                    if (p.causal && nb + q > m) v = -INFINITY;
+                    r[q] = knx_act(v, p.act, p.act_alpha);
+                }
+                float* y = C + (size_t)m * p.ldc + nb;
+                if (vec) {
+                    *reinterpret_cast<float4*>(y) = make_float4(r[0], r[1], r[2], r[3]);
+                } else {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        if (nb + q >= nlo) y[q] = r[q];
+                }
+            }
+            asm volatile("" ::: "memory");
+        }
+    }
+}
+
+template <int BM, int BN, int WM, int WN>
+int launch_k32(SgArgs p, int batch, hipStream_t s, const char* name)
+{
+    p.tiles_m = (p.M + BM - 1) / BM;
+    p.tiles_n = (p.N + BN - 1) / BN;
+    const unsigned tiles = (unsigned)p.tiles_m * (unsigned)p.tiles_n;
+    hipLaunchKernelGGL((sgemm_k32<BM, BN, WM, WN>), dim3(tiles, batch), dim3(WM * WN * 64), 0, s, p);
+    return knx::check_launch(name);
+}
+
+// the pipelined kernel needs K % 32 == 0, 16-byte aligned rows and whole tiles inside M and N
+bool k32_ok(const SgArgs& p, int bm, int bn)
+{
+    return p.K > 0 && p.K % 32 == 0 && p.M >= bm && p.N >= bn && (p.lda & 3) == 0 && (p.ldb & 3) == 0 &&
+           ((uintptr_t)p.A & 15) == 0 && ((uintptr_t)p.B & 15) == 0 && (long)8 * p.lda * 4 < 0x7fffffffL &&
+           (long)8 * p.ldb * 4 < 0x7fffffffL;
+}
+
+// NT dispatch: the pipelined kernel when its tiles fill the chip, else the general kernel
+int dispatch_nt(SgArgs p, int batch, hipStream_t s, const char* name)
+{
+    const long cus = knx::num_cus();
+    const long t256 = (long)((p.M + 255) / 256) * ((p.N + 255) / 256) * batch;
+    const long t128 = (long)((p.M + 127) / 128) * ((p.N + 127) / 128) * batch;
+    // KNX_SGEMM_KERNEL=general forces the general kernel (tests)
+    const char* force = getenv("KNX_SGEMM_KERNEL");
+    const bool general = force != nullptr && strcmp(force, "general") == 0;
+    if (!general && t256 >= cus && k32_ok(p, 256, 256)) return launch_k32<256, 256, 4, 2>(p, batch, s, name);
+    if (!general && t128 >= cus && k32_ok(p, 128, 128)) return launch_k32<128, 128, 2, 2>(p, batch, s, name);
+    return dispatch<true>(p, batch, s, name);
+}
+
 }  // namespace
 
 extern "C" int knx_hip_sgemm_ep(int M, int N, int K, const float* A, int lda, const float* W, int ldw, const float* bias,
@@ -214,6 +445,21 @@ extern "C" int knx_hip_sgemm_ep(int M, int N, int K, const float* A, int lda, co
     p.M = M; p.N = N; p.K = K; p.A = A; p.lda = lda; p.B = W; p.ldb = ldw; p.C = C; p.ldc = ldc;
     p.bias = bias; p.act = act; p.act_alpha = alpha; p.alpha = 1.0f; p.causal = 0; p.zh = 1;
     return dispatch<false>(p, 1, knx::as_stream(stream), name);
+}
+
+extern "C" int knx_hip_sgemm_nt_ep(int M, int N, int K, const float* A, int lda, const float* Wt, int ldwt,
+                                   const float* bias, int act, float alpha, float* C, int ldc, void* stream)
+{
+    const char* name = "knx_hip_sgemm_nt_ep";
+    KNX_ENTRY(name);
+    KNX_REQUIRE(M >= 0 && N >= 0 && K >= 0 && act >= -1 && act <= 15, name);
+    if (M == 0 || N == 0) return KNX_OK;
+    KNX_REQUIRE(C != nullptr && ldc >= N, name);
+    KNX_REQUIRE(K == 0 || (A != nullptr && Wt != nullptr && lda >= K && ldwt >= K), name);
+    SgArgs p{};
+    p.M = M; p.N = N; p.K = K; p.A = A; p.lda = lda; p.B = Wt; p.ldb = ldwt; p.C = C; p.ldc = ldc;
+    p.bias = bias; p.act = act; p.act_alpha = alpha; p.alpha = 1.0f; p.causal = 0; p.zh = 1;
+    return dispatch_nt(p, 1, knx::as_stream(stream), name);
 }
 
 // Batched GEMM used by the attention core (internal to this library, declared in knx_attn.hip).

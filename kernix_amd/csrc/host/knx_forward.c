@@ -40,6 +40,21 @@ static int up_t(float** dst, const float_tensor* t, void* stream)
 {
     return t == NULL ? (*dst = NULL, 0) : up_f(dst, t->tensor, (size_t)t->row * (size_t)t->col, stream);
 }
+/* K×N host weight → N×K device copy (both GEMM operands K-contiguous, see knx_hip_sgemm_nt_ep) */
+static int up_tT(float** dst, const float_tensor* t, void* stream)
+{
+    *dst = NULL;
+    if (t == NULL) return 0;
+    const size_t k = (size_t)t->row, n = (size_t)t->col;
+    float* h = malloc(sizeof(float) * k * n);
+    if (h == NULL) return -1;
+    for (size_t i = 0; i < k; i++)
+        for (size_t j = 0; j < n; j++) h[j * k + i] = t->tensor[i * n + j];
+    int rc = up_f(dst, h, k * n, stream);
+    if (rc == 0) rc = knx_hip_stream_sync(stream) != KNX_OK; /* the copy reads h: wait before freeing it */
+    free(h);
+    return rc;
+}
 static int up_q(int8_t** dq, float** ds, const kernix_qweight* q, void* stream)
 {
     *dq = NULL;
@@ -60,7 +75,7 @@ static int upload_step(kernix_step* s, void* stream)
     const size_t nb = s->kind == KERNIX_OP_GRU ? 2 * gu : gu;
     switch (s->kind) {
     case KERNIX_OP_LINEAR:
-        if (up_t(&d->w, s->w, stream) || up_q(&d->q, &d->qscale, s->q, stream) || up_f(&d->bias, s->bias, (size_t)s->out, stream)) return -1;
+        if (up_tT(&d->w, s->w, stream) || up_q(&d->q, &d->qscale, s->q, stream) || up_f(&d->bias, s->bias, (size_t)s->out, stream)) return -1;
         break;
     case KERNIX_OP_LAYERNORM:
         if (up_f(&d->gamma, s->gamma, (size_t)s->in, stream) || up_f(&d->beta, s->beta, (size_t)s->in, stream)) return -1;
@@ -99,9 +114,9 @@ static int upload_step(kernix_step* s, void* stream)
         break;
     case KERNIX_OP_ATTENTION: {
         const size_t hk = (size_t)s->heads * s->dk, hv = (size_t)s->heads * s->dv;
-        if (up_t(&d->w, s->w, stream) || up_f(&d->bias, s->bias, hk, stream) || up_t(&d->wk, s->wk, stream) ||
-            up_f(&d->bk, s->bk, hk, stream) || up_t(&d->wv, s->wv, stream) || up_f(&d->bv, s->bv, hv, stream) ||
-            up_t(&d->wo, s->wo, stream) || up_f(&d->bo, s->bo, (size_t)s->out, stream))
+        if (up_tT(&d->w, s->w, stream) || up_f(&d->bias, s->bias, hk, stream) || up_tT(&d->wk, s->wk, stream) ||
+            up_f(&d->bk, s->bk, hk, stream) || up_tT(&d->wv, s->wv, stream) || up_f(&d->bv, s->bv, hv, stream) ||
+            up_tT(&d->wo, s->wo, stream) || up_f(&d->bo, s->bo, (size_t)s->out, stream))
             return -1;
         break;
     }
@@ -231,10 +246,10 @@ static int ws_walk(kernix_model* m, size_t B, ws_ctx* c)
                 float* pb = s->q_b ? ws_take(c, (size_t)s->q_b->k * (size_t)s->q_b->n * sizeof(float)) : NULL;
                 if (c->mode == WS_ALLOC) {
                     if ((s->deq = malloc(sizeof(float_tensor))) == NULL) return -1;
-                    *s->deq = (float_tensor){ s->q->k, s->q->n, p };
+                    *s->deq = (float_tensor){ s->q->n, s->q->k, p }; /* N×K: the transposed weight */
                     if (s->q_b) {
                         if ((s->deq_b = malloc(sizeof(float_tensor))) == NULL) return -1;
-                        *s->deq_b = (float_tensor){ s->q_b->k, s->q_b->n, pb };
+                        *s->deq_b = (float_tensor){ s->q_b->n, s->q_b->k, pb };
                     }
                 }
             }
@@ -346,11 +361,11 @@ static int alloc_ws(kernix_model* m, int rows)
     /* the fp32 copies of the int8 weights, computed on the device from the uploaded int8 weights */
     for (int i = 0; i < m->n_steps; i++) {
         kernix_step* s = &m->steps[i];
-        if (s->deq && hip_ok(knx_hip_dequant(s->dev->q, s->q->kp, s->dev->qscale, s->q->k, s->q->n, s->deq->tensor, m->dev->stream), "dequantization") != 0) {
+        if (s->deq && hip_ok(knx_hip_dequant_t(s->dev->q, s->q->kp, s->dev->qscale, s->q->k, s->q->n, s->deq->tensor, m->dev->stream), "dequantization") != 0) {
             knx_model_release_device_ws(m);
             return -1;
         }
-        if (s->deq_b && hip_ok(knx_hip_dequant(s->dev->q_b, s->q_b->kp, s->dev->qscale_b, s->q_b->k, s->q_b->n, s->deq_b->tensor, m->dev->stream), "dequantization") != 0) {
+        if (s->deq_b && hip_ok(knx_hip_dequant_t(s->dev->q_b, s->q_b->kp, s->dev->qscale_b, s->q_b->k, s->q_b->n, s->deq_b->tensor, m->dev->stream), "dequantization") != 0) {
             knx_model_release_device_ws(m);
             return -1;
         }
@@ -387,7 +402,7 @@ static int run_qlinear(const kernix_model* m, const kernix_qweight* q, const int
     }
     if (deq == NULL) { KNX_LOG("KERNIX: missing fp32 copy of an int8 weight\n"); return -1; }
     if (accumulate) return -1; /* the recurrence adds through a separate buffer on this path */
-    return hip_ok(knx_hip_sgemm_ep(rows, q->n, q->k, x, q->k, deq->tensor, q->n, bias, act, alpha, y, q->n, st), "fp32 GEMM");
+    return hip_ok(knx_hip_sgemm_nt_ep(rows, q->n, q->k, x, q->k, deq->tensor, q->k, bias, act, alpha, y, q->n, st), "fp32 GEMM");
 }
 
 /* One direction of an RNN, reference include/kernix_model.h:563-632: the input projection of all timesteps is one
@@ -431,7 +446,10 @@ static int run_rnn_dir(const kernix_model* m, kernix_step* s, int dir, const flo
             rec_term = kind == KERNIX_OP_GRU ? hu : NULL;
         } else {
             if (U == NULL) return -1;
-            if (hip_ok(knx_hip_sgemm_ep(B, gu, u, h, u, U, gu, brec, -1, 0.0f, hu, gu, st), "RNN recurrence")) return -1;
+            /* the fp32 copy of an int8 U is stored transposed (gu × u); a float U is u × gu as in the file */
+            const int rc = q != NULL ? knx_hip_sgemm_nt_ep(B, gu, u, h, u, U, u, brec, -1, 0.0f, hu, gu, st)
+                                     : knx_hip_sgemm_ep(B, gu, u, h, u, U, gu, brec, -1, 0.0f, hu, gu, st);
+            if (hip_ok(rc, "RNN recurrence")) return -1;
             rec_term = hu;
         }
         float* out_t = s->ret_seq ? dst + (size_t)t * stride : NULL;
@@ -471,8 +489,8 @@ static int run_step(kernix_model* m, int i, int B, void* st)
         if (s->q != NULL)
             return run_qlinear(m, s->q, d->q, d->qscale, s->deq, d->xq, d->sx, d->xq_rows, a->tensor, a->row, d->bias,
                                s->act, s->alpha, 0, y->tensor, st);
-        return hip_ok(knx_hip_sgemm_ep(a->row, s->out, s->in, a->tensor, s->in, d->w, s->out, d->bias, s->act, s->alpha,
-                                       y->tensor, s->out, st), "Linear");
+        return hip_ok(knx_hip_sgemm_nt_ep(a->row, s->out, s->in, a->tensor, s->in, d->w, s->in, d->bias, s->act, s->alpha,
+                                          y->tensor, s->out, st), "Linear");
     case KERNIX_OP_ACT:
         return hip_ok(knx_hip_bias_act(a->tensor, y->tensor, rows, cols, NULL, s->act, s->alpha, st), "activation");
     case KERNIX_OP_LAYERNORM:
@@ -551,14 +569,14 @@ static int run_step(kernix_model* m, int i, int B, void* st)
         float* K = s->tmp[1]->tensor;
         float* V = s->tmp[2]->tensor;
         float* ctx = s->tmp[4]->tensor;
-        if (hip_ok(knx_hip_sgemm_ep(vq->row, hk, vq->col, vq->tensor, vq->col, d->w, hk, d->bias, -1, 0.0f, Q, hk, st), "attention Q") ||
-            hip_ok(knx_hip_sgemm_ep(vk->row, hk, vk->col, vk->tensor, vk->col, d->wk, hk, d->bk, -1, 0.0f, K, hk, st), "attention K") ||
-            hip_ok(knx_hip_sgemm_ep(vv->row, hv, vv->col, vv->tensor, vv->col, d->wv, hv, d->bv, -1, 0.0f, V, hv, st), "attention V"))
+        if (hip_ok(knx_hip_sgemm_nt_ep(vq->row, hk, vq->col, vq->tensor, vq->col, d->w, vq->col, d->bias, -1, 0.0f, Q, hk, st), "attention Q") ||
+            hip_ok(knx_hip_sgemm_nt_ep(vk->row, hk, vk->col, vk->tensor, vk->col, d->wk, vk->col, d->bk, -1, 0.0f, K, hk, st), "attention K") ||
+            hip_ok(knx_hip_sgemm_nt_ep(vv->row, hv, vv->col, vv->tensor, vv->col, d->wv, vv->col, d->bv, -1, 0.0f, V, hv, st), "attention V"))
             return -1;
         if (hip_ok(knx_hip_attention_core(Q, K, V, ctx, s->tmp[3]->tensor, B, H, Rq, S, s->dk, s->dv, 1.0f / sqrtf((float)s->dk),
                                           s->causal, st), "attention"))
             return -1;
-        return hip_ok(knx_hip_sgemm_ep(vq->row, s->out, hv, ctx, hv, d->wo, s->out, d->bo, -1, 0.0f, y->tensor, s->out, st),
+        return hip_ok(knx_hip_sgemm_nt_ep(vq->row, s->out, hv, ctx, hv, d->wo, hv, d->bo, -1, 0.0f, y->tensor, s->out, st),
                       "attention output");
     }
     case KERNIX_OP_SELECT: {

@@ -9,7 +9,7 @@
 
 /* Device copies of one step's parameters, uploaded on the first forward and kept until kernix_model_free. */
 struct knx_dstep {
-    float* w;         /* LINEAR/CONV/EMBEDDING fp32 weight, RNN input weight, ATTENTION Wq */
+    float* w;         /* LINEAR fp32 weight (stored N×K), CONV/EMBEDDING weight, RNN input weight, ATTENTION Wq (N×K) */
     float* bias;
     float* gamma;
     float* beta;

@@ -24,7 +24,9 @@ SIGS = {
     "knx_hip_quantize_rows": ([P, I, I, I, I, P, I, P, P], I),
     "knx_hip_i8gemm": ([I, I, I, P, I, P, P, I, P, P, I, F, I, P, I, P, I, P], I),
     "knx_hip_dequant": ([P, I, P, I, I, P, P], I),
+    "knx_hip_dequant_t": ([P, I, P, I, I, P, P], I),
     "knx_hip_sgemm_ep": ([I, I, I, P, I, P, I, P, I, F, P, I, P], I),
+    "knx_hip_sgemm_nt_ep": ([I, I, I, P, I, P, I, P, I, F, P, I, P], I),
     "knx_hip_conv": ([ctypes.POINTER(ConvGeom), P, P, P, I, F, P, P], I),
     "knx_hip_layernorm": ([P, P, I, I, P, P, F, P], I),
     "knx_hip_softmax": ([P, P, I, I, P], I),

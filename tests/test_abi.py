@@ -84,7 +84,7 @@ from kernix_amd.kernix import Model
 x = configs.fp32_mlp({str(tmp_path / 'f.knx')!r}, batch=3, dims=(16, 32, 8))
 m = Model({str(tmp_path / 'f.knx')!r})
 good = m(x)
-os.environ["KNX_HIP_FAIL"] = "knx_hip_sgemm_ep"
+os.environ["KNX_HIP_FAIL"] = "knx_hip_sgemm_nt_ep"
 try:
     m(x)
     print("no error")

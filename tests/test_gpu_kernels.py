@@ -161,6 +161,26 @@ def test_sgemm_ep(L, M, N, K, act):
     assert rel_err(host(C), want) <= 1e-4
 
 
+# the weight-transposed entry point: pipelined kernel (K % 32 == 0, tiles inside M and N, moved back at the edges)
+# and the general kernel otherwise
+SGNT_SHAPES = [(256, 256, 64), (300, 200, 96), (1024, 1000, 512), (4096, 1024, 256), (128, 128, 32), (100, 77, 50),
+               (512, 512, 30), (2048, 640, 2048)]
+
+
+@pytest.mark.parametrize("M,N,K", SGNT_SHAPES)
+@pytest.mark.parametrize("act", [-1, 0, 1])
+def test_sgemm_nt_ep(L, M, N, K, act):
+    rng = np.random.default_rng(M + 5 * N + 11 * K)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    W = (rng.standard_normal((K, N)) / np.sqrt(K)).astype(np.float32)
+    b = rng.normal(0, 0.1, N).astype(np.float32)
+    want = knx_ref.act(knx_ref.dense64(A, W, b), act)
+    C = torch.full((M, N), 7.0, dtype=torch.float32, device="cuda")
+    dA, dWt, db = dev(A), dev(np.ascontiguousarray(W.T)), dev(b)
+    hipabi.check(L.knx_hip_sgemm_nt_ep(M, N, K, ptr(dA), K, ptr(dWt), K, ptr(db), act, 0.0, ptr(C), N, hipabi.stream()))
+    assert rel_err(host(C), want) <= 1e-4
+
+
 # ---------------------------------------------------------------- rows / elementwise
 # scalar kernels (cols % 4 != 0 or > 2048) and every register-resident shape (16/32/64 lanes per row, 1–8 float4)
 @pytest.mark.parametrize("rows,cols", [(1, 1), (7, 10), (64, 512), (300, 2048), (5, 9000), (9, 12), (17, 60),
