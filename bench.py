@@ -148,7 +148,7 @@ def rows_bench(steps, warmup):
 
 def conv_bench(steps, warmup):
     """The four convolutions of the CNN configuration (batch 256, NHWC, 3×3, pad 1, bias + ReLU fused) through
-    knx_hip_conv: algorithmic flops 2·B·Ho·Wo·Co·9·Cin per launch against the fp32 MFMA peak, and the minimum HBM
+    knx_hip_conv_t: algorithmic flops 2·B·Ho·Wo·Co·9·Cin per launch against the fp32 MFMA peak, and the minimum HBM
     bytes (input + weights + output once)."""
     import torch
 
@@ -163,13 +163,13 @@ def conv_bench(steps, warmup):
         ho = (h + 2 - 3) // st + 1
         g = hipabi.ConvGeom(256, h, h, cin, ho, ho, cout, 3, 3, st, st, 1, 1, 1, 1, 1)
         x = torch.randn(256, h, h, cin, device="cuda")
-        w = torch.randn(9 * cin, cout, device="cuda") * (2.0 / (9 * cin)) ** 0.5
+        wt = torch.randn(cout, 9 * cin, device="cuda") * (2.0 / (9 * cin)) ** 0.5  # Co × K, the model's device layout
         b = torch.randn(cout, device="cuda") * 0.01
         y = torch.empty(256, ho, ho, cout, device="cuda")
-        ms, _ = time_launches(lambda: hipabi.check(L.knx_hip_conv(ctypes.byref(g), P(x), P(w), P(b), 0, 0.0, P(y), S)),
+        ms, _ = time_launches(lambda: hipabi.check(L.knx_hip_conv_t(ctypes.byref(g), P(x), P(wt), P(b), 0, 0.0, P(y), S)),
                               steps, warmup)
         flops = 2.0 * 256 * ho * ho * cout * 9 * cin
-        nbytes = 4 * (x.numel() + w.numel() + cout + y.numel())
+        nbytes = 4 * (x.numel() + wt.numel() + cout + y.numel())
         tf = flops / (ms * 1e-3) / 1e12
         out[name] = dict(us=round(ms * 1e3, 2), tflops=round(tf, 2), mfma_frac=round(tf / PEAK_F32_TFLOPS, 4),
                          gbs=round(nbytes / (ms * 1e-3) / 1e9, 1))

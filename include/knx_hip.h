@@ -17,7 +17,7 @@
  *   knx_hip_sgemm_nt_ep
  *                           + kernix_bias_act epilogue                          include/kernix.h:951-977,
  *                                                                               include/kernix_model.h:528-550
- *   knx_hip_conv            kernix_conv_run (im2col → sgemm → bias_act)         include/kernix_model.h:711-771
+ *   knx_hip_conv(_t)        kernix_conv_run (im2col → sgemm → bias_act)         include/kernix_model.h:711-771
  *   knx_hip_layernorm       kernix_layer_norm_rows_into                         include/kernix.h:667-677
  *   knx_hip_softmax         floats_softmax_into                                 include/kernix.h:652-657
  *   knx_hip_bias_act        kernix_bias_act / ACT step                          include/kernix_model.h:528-541, :1866-1869
@@ -109,6 +109,10 @@ typedef struct {
 /* y = act(conv(x, w) + bias); w is (kh·kw·C/groups) × Co with rows ordered (ky, kx, ci). */
 KNX_API int knx_hip_conv(const knx_conv_geom* g, const float* x, const float* w, const float* bias, int act,
                          float alpha, float* y, void* stream);
+/* Same with the weight transposed: Wt Co × (kh·kw·C/groups), the device layout of the model's convolution weights.
+ * Channel counts per group that are multiples of 32 run on the pipelined implicit GEMM (LDS-DMA gathers). */
+KNX_API int knx_hip_conv_t(const knx_conv_geom* g, const float* x, const float* wt, const float* bias, int act,
+                           float alpha, float* y, void* stream);
 
 /* ---- row and elementwise ops (y may equal x unless noted) ---- */
 KNX_API int knx_hip_layernorm(const float* x, float* y, int rows, int cols, const float* gamma, const float* beta,

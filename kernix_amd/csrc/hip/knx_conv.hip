@@ -9,6 +9,10 @@
 
 typedef float v16f __attribute__((ext_vector_type(16)));
 
+// the pipelined implicit-GEMM kernel (knx_sgemm.hip): returns 1 without launching when the shape does not qualify
+int knx_conv_k32(const knx_conv_geom* g, const float* x, const float* wt, const float* bias, int act, float alpha,
+                 float* y, hipStream_t s, const char* name);
+
 namespace {
 
 struct ConvArgs {
@@ -25,7 +29,8 @@ struct ConvArgs {
 
 constexpr int BK = 16;
 
-template <int BM, int BN, int WM, int WN, bool VEC>
+// TB: the weight is given transposed (Wt, Co × K, the device layout of the model's convolution weights)
+template <int BM, int BN, int WM, int WN, bool VEC, bool TB = false>
 __global__ void __launch_bounds__(WM * WN * 64) conv_tile(ConvArgs p)
 {
     constexpr int NT = WM * WN * 64;
@@ -46,8 +51,9 @@ __global__ void __launch_bounds__(WM * WN * 64) conv_tile(ConvArgs p)
     const int grp = blockIdx.y;
     const int M = p.M, N = p.N, K = p.K, cg = p.cg;
     const int cbase = grp * cg;                 // first input channel of the group
-    const float* W = p.w + (size_t)grp * N;     // column offset of the group in the (K × Co) weight
-    const bool b_vec = (g.Co & 3) == 0 && (N & 3) == 0;
+    // the group's weight columns in W (K × Co), or its rows in Wt (Co × K)
+    const float* W = TB ? p.w + (size_t)grp * N * K : p.w + (size_t)grp * N;
+    const bool b_vec = TB ? (K & 3) == 0 && ((uintptr_t)p.w & 15) == 0 : (g.Co & 3) == 0 && (N & 3) == 0;
 
     // per load slot: the output pixel this thread gathers for (fixed over the whole K loop)
     int sb[LA], siy[LA], six[LA];
@@ -117,6 +123,23 @@ __global__ void __launch_bounds__(WM * WN * 64) conv_tile(ConvArgs p)
         advance(tci, tkx, tky, BK);
 #pragma unroll
         for (int i = 0; i < LB; ++i) {
+            if (TB) {  // row r of Wt (output channel n0 + r), k-chunk kc
+                const int idx = i * NT + t, r = idx >> 2, kc = (idx & 3) * 4;
+                const int gn = n0 + r, gkb = k0 + kc;
+                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (gn < N) {
+                    const float* src = W + (size_t)gn * K + gkb;
+                    if (b_vec && gkb + 3 < K) v = *reinterpret_cast<const float4*>(src);
+                    else {
+                        if (gkb + 0 < K) v.x = src[0];
+                        if (gkb + 1 < K) v.y = src[1];
+                        if (gkb + 2 < K) v.z = src[2];
+                        if (gkb + 3 < K) v.w = src[3];
+                    }
+                }
+                rb[i] = v;
+                continue;
+            }
             const int idx = i * NT + t, k = idx / (BN / 4), nc = (idx % (BN / 4)) * 4;
             const int gkb = k0 + k, gn = n0 + nc;
             float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -142,8 +165,14 @@ __global__ void __launch_bounds__(WM * WN * 64) conv_tile(ConvArgs p)
         }
 #pragma unroll
         for (int i = 0; i < LB; ++i) {
-            const int idx = i * NT + t, k = idx / (BN / 4), nc = (idx % (BN / 4)) * 4;
-            *reinterpret_cast<float4*>(&Bs[buf][k * SB + nc]) = rb[i];
+            if (TB) {
+                const int idx = i * NT + t, r = idx >> 2, kc = (idx & 3) * 4;
+                float* d = &Bs[buf][kc * SB + r];
+                d[0] = rb[i].x; d[SB] = rb[i].y; d[2 * SB] = rb[i].z; d[3 * SB] = rb[i].w;
+            } else {
+                const int idx = i * NT + t, k = idx / (BN / 4), nc = (idx % (BN / 4)) * 4;
+                *reinterpret_cast<float4*>(&Bs[buf][k * SB + nc]) = rb[i];
+            }
         }
     };
 
@@ -201,22 +230,20 @@ __global__ void __launch_bounds__(WM * WN * 64) conv_tile(ConvArgs p)
     }
 }
 
-template <int BM, int BN, int WM, int WN>
+template <int BM, int BN, int WM, int WN, bool TB>
 int launch(ConvArgs p, bool vec, hipStream_t s, const char* name)
 {
     p.tiles_n = (p.N + BN - 1) / BN;
     const unsigned tiles = (unsigned)((p.M + BM - 1) / BM) * (unsigned)p.tiles_n;
-    if (vec) hipLaunchKernelGGL((conv_tile<BM, BN, WM, WN, true>), dim3(tiles, p.g.groups), dim3(WM * WN * 64), 0, s, p);
-    else hipLaunchKernelGGL((conv_tile<BM, BN, WM, WN, false>), dim3(tiles, p.g.groups), dim3(WM * WN * 64), 0, s, p);
+    if (vec) hipLaunchKernelGGL((conv_tile<BM, BN, WM, WN, true, TB>), dim3(tiles, p.g.groups), dim3(WM * WN * 64), 0, s, p);
+    else hipLaunchKernelGGL((conv_tile<BM, BN, WM, WN, false, TB>), dim3(tiles, p.g.groups), dim3(WM * WN * 64), 0, s, p);
     return knx::check_launch(name);
 }
 
-}  // namespace
-
-extern "C" int knx_hip_conv(const knx_conv_geom* g, const float* x, const float* w, const float* bias, int act,
-                            float alpha, float* y, void* stream)
+template <bool TB>
+int conv_entry(const knx_conv_geom* g, const float* x, const float* w, const float* bias, int act, float alpha, float* y,
+               void* stream, const char* name)
 {
-    const char* name = "knx_hip_conv";
     KNX_ENTRY(name);
     KNX_REQUIRE(g != nullptr, name);
     KNX_REQUIRE(g->B >= 0 && g->H >= 1 && g->W >= 1 && g->C >= 1 && g->Ho >= 1 && g->Wo >= 1 && g->Co >= 1, name);
@@ -227,6 +254,11 @@ extern "C" int knx_hip_conv(const knx_conv_geom* g, const float* x, const float*
     KNX_REQUIRE((long long)g->B * g->Ho * g->Wo <= 0x7fffffffLL && (long long)g->B * g->H * g->W * g->C <= (1LL << 40), name);
     if (g->B == 0) return KNX_OK;
     KNX_REQUIRE(x && w && y && x != y, name);
+    hipStream_t s = knx::as_stream(stream);
+    if (TB) {
+        const int rc = knx_conv_k32(g, x, w, bias, act, alpha, y, s, name);
+        if (rc != 1) return rc;
+    }
     ConvArgs p{};
     p.g = *g; p.x = x; p.w = w; p.bias = bias; p.act = act; p.alpha = alpha; p.y = y;
     p.cg = g->C / g->groups;
@@ -234,13 +266,26 @@ extern "C" int knx_hip_conv(const knx_conv_geom* g, const float* x, const float*
     p.N = g->Co / g->groups;
     p.K = g->kh * g->kw * p.cg;
     const bool vec = (p.cg & 3) == 0 && (((uintptr_t)x) & 15) == 0;
-    hipStream_t s = knx::as_stream(stream);
     const long tiles = (long)((p.M + 127) / 128) * g->groups;
     if (tiles >= knx::num_cus()) {
         // narrow outputs: 256 pixels × 64 channels, each wave 64 × 64 (four MFMAs per four fragment reads)
-        if (vec && p.N <= 64 && tiles >= 2L * knx::num_cus()) return launch<256, 64, 4, 1>(p, vec, s, name);
-        if (p.N <= 64) return launch<128, 64, 2, 2>(p, vec, s, name);
-        return launch<128, 128, 2, 2>(p, vec, s, name);
+        if (vec && p.N <= 64 && tiles >= 2L * knx::num_cus()) return launch<256, 64, 4, 1, TB>(p, vec, s, name);
+        if (p.N <= 64) return launch<128, 64, 2, 2, TB>(p, vec, s, name);
+        return launch<128, 128, 2, 2, TB>(p, vec, s, name);
     }
-    return launch<64, 64, 2, 2>(p, vec, s, name);
+    return launch<64, 64, 2, 2, TB>(p, vec, s, name);
+}
+
+}  // namespace
+
+extern "C" int knx_hip_conv(const knx_conv_geom* g, const float* x, const float* w, const float* bias, int act,
+                            float alpha, float* y, void* stream)
+{
+    return conv_entry<false>(g, x, w, bias, act, alpha, y, stream, "knx_hip_conv");
+}
+
+extern "C" int knx_hip_conv_t(const knx_conv_geom* g, const float* x, const float* wt, const float* bias, int act,
+                              float alpha, float* y, void* stream)
+{
+    return conv_entry<true>(g, x, wt, bias, act, alpha, y, stream, "knx_hip_conv_t");
 }

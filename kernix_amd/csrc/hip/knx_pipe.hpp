@@ -53,3 +53,10 @@ static __device__ __forceinline__ void dma16(const void* base, unsigned voff, vo
     const unsigned l = (unsigned)(uintptr_t)(lds_ptr_t)dst;
     asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(l), "v"(voff), "s"(base) : "memory");
 }
+
+// The same load with a per-lane 64-bit source address (gathers: every lane's row may live anywhere).
+static __device__ __forceinline__ void dma16_at(const void* src, void* dst)
+{
+    const unsigned l = (unsigned)(uintptr_t)(lds_ptr_t)dst;
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(l), "v"(src) : "memory");
+}

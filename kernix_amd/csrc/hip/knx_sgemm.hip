@@ -38,6 +38,8 @@ struct SgArgs {
     int causal;    // C[i][j] = −inf for j > i (attention scores)
     int tiles_n;
     int tiles_m;
+    knx_conv_geom cv;  // implicit-GEMM convolution (sgemm_k32<…, true>): A rows are output pixels gathered from x
+    int cgc;           // input channels per group
     int zh;        // batch index z = zb·zh + zi
     long long sAb, sAh, sBb, sBh, sCb, sCh;
 };
@@ -216,7 +218,10 @@ int dispatch(SgArgs p, int batch, hipStream_t s, const char* name)
 // lanes 0-31 take floats 0-15 and lanes 32-63 floats 16-31, one per v_mfma_f32_32x32x2_f32 k-step, so a lane reads
 // its 16 operand values of a k-tile as four 16-byte chunks ("quads" of four k-steps).  Tiles that would cross M or N
 // are moved back inside and store only what they own.
-template <int BM, int BN, int WM, int WN>
+// 128 zero bytes: the source of the gathered rows that fall in a convolution's zero padding
+__device__ __attribute__((aligned(128))) int8_t knx_zero_line[128];
+
+template <int BM, int BN, int WM, int WN, bool CONV = false>
 __global__ void __launch_bounds__(WM * WN * 64) sgemm_k32(SgArgs p)
 {
     constexpr int NW = WM * WN;
@@ -238,23 +243,64 @@ __global__ void __launch_bounds__(WM * WN * 64) sgemm_k32(SgArgs p)
     tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
     const int mlo = tm * BM, nlo = tn * BN;
     const int m0 = min(mlo, p.M - BM), n0 = min(nlo, p.N - BN);
-    const int z = blockIdx.y, zb = z / p.zh, zi = z % p.zh;
-    const float* A = p.A + zb * p.sAb + zi * p.sAh;
-    const float* B = p.B + zb * p.sBb + zi * p.sBh;
-    float* C = p.C + zb * p.sCb + zi * p.sCh;
+    const float* A;
+    const float* B;
+    float* C;
+    const float* bias = p.bias;
+    int cbase = 0;
+    if (CONV) {  // grid.y = group: its channel slice of x, its rows of Wt, its columns of y and of the bias
+        const int grp = blockIdx.y;
+        cbase = grp * p.cgc;
+        A = p.A;
+        B = p.B + (size_t)grp * p.N * p.ldb;
+        C = p.C + (size_t)grp * p.N;
+        if (bias) bias += (size_t)grp * p.N;
+    } else {
+        const int z = blockIdx.y, zb = z / p.zh, zi = z % p.zh;
+        A = p.A + zb * p.sAb + zi * p.sAh;
+        B = p.B + zb * p.sBb + zi * p.sBh;
+        C = p.C + zb * p.sCb + zi * p.sCh;
+    }
 
     const int8_t* tile_a = reinterpret_cast<const int8_t*>(A + (size_t)m0 * p.lda);
     const int8_t* tile_b = reinterpret_cast<const int8_t*>(B + (size_t)n0 * p.ldb);
     const int lda4 = p.lda * 4, ldb4 = p.ldb * 4;  // row strides in bytes
     const int cl = (lane & 7) ^ (lane >> 3), rs = lane >> 3;
     const int nk = p.K / 32;
+    // convolution: the output pixel of this lane's row in every A slot (fixed over K) as (b, oy·sh − pt, ox·sw − pl)
+    constexpr int SAC = CONV ? SA : 1;
+    int pb[SAC], piy[SAC], pix[SAC];
+    if (CONV) {
+        const knx_conv_geom& g = p.cv;
+#pragma unroll
+        for (int i = 0; i < SAC; ++i) {
+            const int m = m0 + (i * NW + wave) * 8 + rs;
+            const int ox = m % g.Wo, oy = (m / g.Wo) % g.Ho;
+            pb[i] = m / (g.Wo * g.Ho);
+            piy[i] = oy * g.sh - g.pt;
+            pix[i] = ox * g.sw - g.pl;
+        }
+    }
     auto issue1 = [&](int kt, int i) {
         const int slot = i * NW + wave;
         const bool a = i < SA;
-        const int ld = a ? lda4 : ldb4;
         const int chunk = cl ^ (slot & 7);
+        int8_t* dst = lds + (kt & 1) * STAGE + slot * 1024;
+        if (CONV && a) {
+            // k-tile kt is 32 consecutive channels of one tap (the group's channel count is a multiple of 32)
+            const knx_conv_geom& g = p.cv;
+            const int k0 = kt * 32, seg = k0 / p.cgc, ci0 = k0 - seg * p.cgc;
+            const int ky = seg / g.kw, kx = seg - ky * g.kw;
+            const int iy = piy[i] + ky * g.dh, ix = pix[i] + kx * g.dw;
+            const bool in = iy >= 0 && iy < g.H && ix >= 0 && ix < g.W;
+            const int8_t* src = in ? reinterpret_cast<const int8_t*>(A + (((size_t)pb[i] * g.H + iy) * g.W + ix) * g.C + cbase + ci0) + chunk * 16
+                                   : knx_zero_line + chunk * 16;
+            dma16_at(src, dst);
+            return;
+        }
+        const int ld = a ? lda4 : ldb4;
         const int8_t* base = (a ? tile_a + (size_t)(slot * 8) * ld : tile_b + (size_t)(slot * 8 - BM) * ld) + kt * 128;
-        dma16(base, (unsigned)(rs * ld + chunk * 16), lds + (kt & 1) * STAGE + slot * 1024);
+        dma16(base, (unsigned)(rs * ld + chunk * 16), dst);
     };
 
     // fragment offsets: row r + 32·f has swizzle swz8(r) ^ 4·(f & 1), i.e. the chunk of half-wave g ^ (f & 1)
@@ -356,7 +402,7 @@ __global__ void __launch_bounds__(WM * WN * 64) sgemm_k32(SgArgs p)
     const int nb = n0 + wn * TN + cq;
     float bv[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) bv[q] = p.bias ? p.bias[nb + q] : 0.0f;
+    for (int q = 0; q < 4; ++q) bv[q] = bias ? bias[nb + q] : 0.0f;
     const bool vec = nb >= nlo && (p.ldc & 3) == 0 && ((uintptr_t)C & 15) == 0;
     KNX_WAIT_LDS();
     knx_barrier_nofence();  // nobody reads the operand stages any more
@@ -380,7 +426,7 @@ __global__ void __launch_bounds__(WM * WN * 64) sgemm_k32(SgArgs p)
                 for (int q = 0; q < 4; ++q) {
                     float v = (&a.x)[q];
                     if (p.alpha != 1.0f) v = p.alpha * v;
-                    if (p.bias) v = v + bv[q];
+                    if (bias) v = v + bv[q];
                     if (p.causal && nb + q > m) v = -INFINITY;
                     r[q] = knx_act(v, p.act, p.act_alpha);
                 }
@@ -430,7 +476,42 @@ int dispatch_nt(SgArgs p, int batch, hipStream_t s, const char* name)
     return dispatch<true>(p, batch, s, name);
 }
 
+template <int BM, int BN, int WM, int WN>
+int launch_conv_k32(SgArgs p, hipStream_t s, const char* name)
+{
+    p.tiles_m = (p.M + BM - 1) / BM;
+    p.tiles_n = (p.N + BN - 1) / BN;
+    const unsigned tiles = (unsigned)p.tiles_m * (unsigned)p.tiles_n;
+    hipLaunchKernelGGL((sgemm_k32<BM, BN, WM, WN, true>), dim3(tiles, p.cv.groups), dim3(WM * WN * 64), 0, s, p);
+    return knx::check_launch(name);
+}
+
 }  // namespace
+
+// Convolution on the pipelined kernel (internal to this library, declared in knx_conv.hip): A rows are the output
+// pixels (M = B·Ho·Wo), K = kh·kw·cg with cg % 32 == 0 so a k-tile is 32 channels of one tap, Wt is Co × K.
+// Returns 1 without launching when the shape does not qualify (the caller then runs the general kernel).
+int knx_conv_k32(const knx_conv_geom* g, const float* x, const float* wt, const float* bias, int act, float alpha,
+                 float* y, hipStream_t s, const char* name)
+{
+    const int cg = g->C / g->groups, N = g->Co / g->groups;
+    const long M = (long)g->B * g->Ho * g->Wo;
+    if (cg % 32 != 0 || ((uintptr_t)x & 15) != 0 || ((uintptr_t)wt & 15) != 0 || M > 0x7fffffffL) return 1;
+    const char* force = getenv("KNX_SGEMM_KERNEL");
+    if (force != nullptr && strcmp(force, "general") == 0) return 1;
+    SgArgs p{};
+    p.M = (int)M; p.N = N; p.K = g->kh * g->kw * cg;
+    p.A = x; p.lda = 0; p.B = wt; p.ldb = p.K; p.C = y; p.ldc = g->Co;
+    p.bias = bias; p.act = act; p.act_alpha = alpha; p.alpha = 1.0f; p.causal = 0; p.zh = 1;
+    p.cv = *g; p.cgc = cg;
+    const long cus = knx::num_cus(), groups = g->groups;
+    auto tiles = [&](int bm, int bn) { return (long)((M + bm - 1) / bm) * ((N + bn - 1) / bn) * groups; };
+    if (N >= 256 && M >= 256 && tiles(256, 256) >= cus) return launch_conv_k32<256, 256, 4, 2>(p, s, name);
+    if (N >= 128 && M >= 256 && tiles(256, 128) >= cus) return launch_conv_k32<256, 128, 4, 2>(p, s, name);
+    if (N >= 128 && M >= 128 && tiles(128, 128) >= cus) return launch_conv_k32<128, 128, 2, 2>(p, s, name);
+    if (N >= 64 && M >= 256 && tiles(256, 64) >= cus) return launch_conv_k32<256, 64, 4, 1>(p, s, name);
+    return 1;
+}
 
 extern "C" int knx_hip_sgemm_ep(int M, int N, int K, const float* A, int lda, const float* W, int ldw, const float* bias,
                                 int act, float alpha, float* C, int ldc, void* stream)

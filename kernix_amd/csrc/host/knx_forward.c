@@ -87,6 +87,8 @@ static int upload_step(kernix_step* s, void* stream)
         if (up_f(&d->cst, s->cst, (size_t)s->in, stream)) return -1;
         break;
     case KERNIX_OP_CONV:
+        if (up_tT(&d->w, s->w, stream) || up_f(&d->bias, s->bias, (size_t)s->out, stream)) return -1;
+        break;
     case KERNIX_OP_EMBEDDING:
         if (up_t(&d->w, s->w, stream) || up_f(&d->bias, s->bias, (size_t)s->out, stream)) return -1;
         break;
@@ -503,8 +505,8 @@ static int run_step(kernix_model* m, int i, int B, void* st)
         return run_rnn(m, s, a, y, st);
     case KERNIX_OP_CONV: {
         if (knx_conv_is_gemm(s) == 0) /* 1×1 stride 1: a GEMM on the NHWC rows */
-            return hip_ok(knx_hip_sgemm_ep(a->row, s->out, s->in, a->tensor, s->in, d->w, s->out, d->bias, s->act, s->alpha,
-                                           y->tensor, s->out, st), "convolution");
+            return hip_ok(knx_hip_sgemm_nt_ep(a->row, s->out, s->in, a->tensor, s->in, d->w, s->in, d->bias, s->act, s->alpha,
+                                              y->tensor, s->out, st), "convolution");
         knx_conv_geom g;
         hw(vi, &g.H, &g.W);
         hw(vo, &g.Ho, &g.Wo);
@@ -512,7 +514,7 @@ static int run_step(kernix_model* m, int i, int B, void* st)
         g.C = vi->c; g.Co = vo->c;
         g.kh = s->kh; g.kw = s->kw; g.sh = s->sh; g.sw = s->sw; g.dh = s->dh; g.dw = s->dw; g.pt = s->pt; g.pl = s->pl;
         g.groups = s->groups;
-        return hip_ok(knx_hip_conv(&g, a->tensor, d->w, d->bias, s->act, s->alpha, y->tensor, st), "convolution");
+        return hip_ok(knx_hip_conv_t(&g, a->tensor, d->w, d->bias, s->act, s->alpha, y->tensor, st), "convolution");
     }
     case KERNIX_OP_POOL: {
         knx_conv_geom g;

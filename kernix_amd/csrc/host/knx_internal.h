@@ -9,7 +9,8 @@
 
 /* Device copies of one step's parameters, uploaded on the first forward and kept until kernix_model_free. */
 struct knx_dstep {
-    float* w;         /* LINEAR fp32 weight (stored N×K), CONV/EMBEDDING weight, RNN input weight, ATTENTION Wq (N×K) */
+    float* w;         /* LINEAR / CONV fp32 weight and ATTENTION Wq stored transposed (out × in); EMBEDDING table;
+                         RNN input weight (in × gates, as in the file) */
     float* bias;
     float* gamma;
     float* beta;

@@ -28,6 +28,7 @@ SIGS = {
     "knx_hip_sgemm_ep": ([I, I, I, P, I, P, I, P, I, F, P, I, P], I),
     "knx_hip_sgemm_nt_ep": ([I, I, I, P, I, P, I, P, I, F, P, I, P], I),
     "knx_hip_conv": ([ctypes.POINTER(ConvGeom), P, P, P, I, F, P, P], I),
+    "knx_hip_conv_t": ([ctypes.POINTER(ConvGeom), P, P, P, I, F, P, P], I),
     "knx_hip_layernorm": ([P, P, I, I, P, P, F, P], I),
     "knx_hip_softmax": ([P, P, I, I, P], I),
     "knx_hip_bias_act": ([P, P, I, I, P, I, F, P], I),

@@ -255,11 +255,18 @@ CONV_CASES = [
     # enough output pixels for the 256 × 64 tile (≥ 512 tiles of 128 on 256 CUs), channel-vector and scalar gathers
     (64, 32, 32, 64, 64, 3, 1, 1, 1, 1),
     (65, 32, 32, 3, 64, 3, 1, 1, 1, 1),
+    # shapes for the pipelined implicit GEMM (channels per group % 32 == 0, enough tiles): 256×64 tiles with groups,
+    # dilation 2, 128×128 tiles, stride 2
+    (128, 16, 16, 128, 128, 3, 1, 1, 2, 1),
+    (64, 32, 32, 64, 64, 3, 1, 2, 1, 2),
+    (128, 16, 16, 64, 128, 3, 1, 1, 1, 1),
+    (256, 16, 16, 128, 256, 3, 2, 1, 1, 1),
 ]
 
 
 @pytest.mark.parametrize("case", CONV_CASES)
-def test_conv(L, case):
+@pytest.mark.parametrize("wt", [False, True])  # weight as in the file (K × Co) or transposed (Co × K)
+def test_conv(L, case, wt):
     B, H, W, C, Co, k, s, p, g, dil = case
     rng = np.random.default_rng(sum(case))
     Ho = (H + 2 * p - dil * (k - 1) - 1) // s + 1
@@ -272,7 +279,11 @@ def test_conv(L, case):
     geom = hipabi.ConvGeom(B, H, W, C, Ho, Wo, Co, k, k, s, s, dil, dil, p, p, g)
     y = torch.empty((B * Ho * Wo, Co), dtype=torch.float32, device="cuda")
     dx, dw, db = dev(x), dev(w), dev(b)
-    hipabi.check(L.knx_hip_conv(ctypes.byref(geom), ptr(dx), ptr(dw), ptr(db), 0, 0.0, ptr(y), hipabi.stream()))
+    if wt:
+        dwt = dev(np.ascontiguousarray(w.T))
+        hipabi.check(L.knx_hip_conv_t(ctypes.byref(geom), ptr(dx), ptr(dwt), ptr(db), 0, 0.0, ptr(y), hipabi.stream()))
+    else:
+        hipabi.check(L.knx_hip_conv(ctypes.byref(geom), ptr(dx), ptr(dw), ptr(db), 0, 0.0, ptr(y), hipabi.stream()))
     assert rel_err(host(y), want) <= 1e-4
 
 
