@@ -177,6 +177,40 @@ def conv_bench(steps, warmup):
     return out
 
 
+def attention_bench(steps, warmup):
+    """The attention core of the Transformer configuration (batch 64, 8 heads, 128 queries and keys, dk = dv = 64):
+    algorithmic flops 2·B·H·Rq·S·(dk + dv) per launch against the fp32 MFMA peak, and the minimum HBM bytes (Q, K,
+    V read once, the context written once), for the fused kernel and for the three-launch path it replaces."""
+    import torch
+
+    from kernix_amd import hipabi
+
+    L = hipabi.lib()
+    hipabi.check(L.knx_hip_init())
+    P, S = hipabi.ptr, hipabi.stream()
+    B, H, T, d = 64, 8, 128, 64
+    q, k, v = (torch.randn(B * T, H * d, device="cuda") for _ in range(3))
+    ctx = torch.empty(B * T, H * d, device="cuda")
+    sc = torch.empty(B * H * T, T, device="cuda")
+    vt = torch.empty(H * d, B * T, device="cuda")
+    flops = 2.0 * B * H * T * T * (2 * d)
+    nbytes = 4 * 4 * B * T * H * d
+    out = {}
+    for name, env in (("fused", None), ("unfused", "unfused")):
+        if env:
+            os.environ["KNX_ATTN_KERNEL"] = env
+        try:
+            ms, _ = time_launches(lambda: hipabi.check(L.knx_hip_attention_core_vt(
+                P(q), P(k), P(v), P(vt), P(ctx), P(sc), B, H, T, T, d, d, 0.125, 0, S)), steps, warmup)
+        finally:
+            os.environ.pop("KNX_ATTN_KERNEL", None)
+        tf = flops / (ms * 1e-3) / 1e12
+        out[name] = dict(us=round(ms * 1e3, 2), tflops=round(tf, 2), mfma_frac=round(tf / PEAK_F32_TFLOPS, 4),
+                         gbs=round(nbytes / (ms * 1e-3) / 1e9, 1))
+        log(f"attention b64 h8 s128 d64 {name}: {ms * 1e3:.1f} us  {tf:.1f} TFLOP/s")
+    return out
+
+
 def measured_traffic():
     """HBM bytes per launch of the M=N=K=4096 GEMM from the committed rocprofv3 counter summary (FETCH_SIZE and
     WRITE_SIZE per dispatch, each scaled by the same counter on a kernel of known traffic), or None without it."""
@@ -307,6 +341,7 @@ def main():
     if not args.no_small:
         out["row_kernels"] = rows_bench(max(args.steps, 20), args.warmup)
         out["conv_layers"] = conv_bench(max(args.steps // 4, 10), max(args.warmup // 10, 3))
+        out["attention_core"] = attention_bench(max(args.steps // 4, 10), max(args.warmup // 10, 3))
     if not args.no_forward:
         fw = {}
         st = max(5, args.steps // 5)

@@ -4,31 +4,235 @@
 // the loop body of kernix_attention_run (reference include/kernix_model.h:1021-1046).  The Q/K/V/O projections
 // are ordinary Linear GEMMs run by the host (knx_hip_sgemm_ep).
 //
-// Path: one batched NT MFMA GEMM writes all B·H score matrices (alpha = scale and the causal mask fused in its
-// epilogue), the wavefront softmax normalizes each row in place, one batched NN MFMA GEMM multiplies by V and writes
-// the context directly in the (B·Rq) × (H·dv) layout the output projection reads.
+// Paths: for dk = dv ∈ {32, 64, 128} and S ≤ 256 (S ≤ 128 at 128) one fused kernel keeps each head's K and Vᵀ in
+// LDS and the scores in registers, so nothing but Q, K, V and the context touches HBM.  Otherwise one batched NT
+// MFMA GEMM writes all B·H score matrices (alpha = scale and the causal mask fused in its epilogue), the wavefront
+// softmax normalizes each row in place, and one batched GEMM multiplies by V and writes the context directly in the
+// (B·Rq) × (H·dv) layout the output projection reads; given scratch for Vᵀ, V is transposed once so that both
+// products have K-contiguous operands and run on the pipelined kernel.
+#include <stdlib.h>
+#include <string.h>
+
 #include "knx_common.hpp"
 
 int knx_sgemm_batched(int M, int N, int K, const float* A, int lda, long long sAb, long long sAh, const float* B, int ldb,
                       long long sBb, long long sBh, bool transB, float* C, int ldc, long long sCb, long long sCh, int nb,
                       int nh, float alpha, int causal, hipStream_t s);
 
-extern "C" int knx_hip_attention_core(const float* Q, const float* K, const float* V, float* ctx, float* scores, int B,
-                                      int H, int Rq, int S, int dk, int dv, float scale, int causal, void* stream)
+namespace {
+
+// Vt (C × R) = Vᵀ for V (R × C), 32 × 32 tiles through LDS
+__global__ void __launch_bounds__(256) transpose_kernel(const float* __restrict__ v, int R, int C, float* __restrict__ vt)
+{
+    __shared__ float tile[32][33];
+    const int r0 = blockIdx.x * 32, c0 = blockIdx.y * 32;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 × 8
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int r = r0 + ty + 8 * i, c = c0 + tx;
+        tile[ty + 8 * i][tx] = (r < R && c < C) ? v[(size_t)r * C + c] : 0.0f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int c = c0 + ty + 8 * i, r = r0 + tx;
+        if (c < C && r < R) vt[(size_t)c * R + r] = tile[tx][ty + 8 * i];
+    }
+}
+
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+// Fused attention for sequences of at most 32·NS keys, dk = DK, dv = DV.  One block per (b·h, 128 queries): K_h
+// (row pitch DK + 4) and V_hᵀ (row pitch 32·NS + 4) of the whole sequence are staged in LDS, zero beyond S; each
+// wave owns 32 queries.  It computes Sᵀ = K_h·Q_hᵀ on 32×32×2 fp32 MFMA, so its accumulators hold, per lane, one
+// query (lane & 31) and 16 keys of each 32-key tile: the row max and sum of the softmax need one exchange between
+// the two half-waves, and the normalized probabilities are already the B operand of ctxᵀ = V_hᵀ·Pᵀ.  Keys beyond S
+// count as −inf, which leaves max, sum and probabilities as they are over the S keys alone.
+template <int NS, int DK, int DV>
+__global__ void __launch_bounds__(256) attention_fused(const float* __restrict__ Q, const float* __restrict__ K,
+                                                       const float* __restrict__ V, float* __restrict__ ctx, int H,
+                                                       int Rq, int S, float scale, int causal)
+{
+    constexpr int SK = 32 * NS, KP = DK + 4, VP = SK + 4;  // pitches put rows 4 banks apart
+    __shared__ __attribute__((aligned(16))) float ks[SK * KP];
+    __shared__ __attribute__((aligned(16))) float vts[DV * VP];
+    const int z = blockIdx.y, b = z / H, h = z % H;
+    const int tid = threadIdx.x, lane = tid & 63, col = lane & 31, hf = lane >> 5;
+    const size_t ldk = (size_t)H * DK, ldv = (size_t)H * DV;
+    const float* Kh = K + (size_t)b * S * ldk + (size_t)h * DK;
+    const float* Vh = V + (size_t)b * S * ldv + (size_t)h * DV;
+    for (int i = tid; i < SK * (DK / 4); i += 256) {
+        const int r = i / (DK / 4), c = i % (DK / 4);
+        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (r < S) v = *reinterpret_cast<const float4*>(Kh + (size_t)r * ldk + 4 * c);
+        *reinterpret_cast<float4*>(&ks[r * KP + 4 * c]) = v;
+    }
+    for (int i = tid; i < SK * (DV / 4); i += 256) {
+        const int r = i / (DV / 4), c = i % (DV / 4);
+        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (r < S) v = *reinterpret_cast<const float4*>(Vh + (size_t)r * ldv + 4 * c);
+        vts[(4 * c + 0) * VP + r] = v.x;
+        vts[(4 * c + 1) * VP + r] = v.y;
+        vts[(4 * c + 2) * VP + r] = v.z;
+        vts[(4 * c + 3) * VP + r] = v.w;
+    }
+    // Q fragments: at step c of group g, half-wave hf contracts over d = 8g + 4hf + c (K fragments likewise)
+    const int qi = blockIdx.x * 128 + (tid >> 6) * 32 + col;
+    const float* Qr = Q + ((size_t)b * Rq + (qi < Rq ? qi : Rq - 1)) * ((size_t)H * DK) + (size_t)h * DK;
+    float4 qf[DK / 8];
+#pragma unroll
+    for (int g = 0; g < DK / 8; ++g) qf[g] = *reinterpret_cast<const float4*>(Qr + 8 * g + 4 * hf);
+    __syncthreads();
+
+    v16f sc[NS];
+#pragma unroll
+    for (int t = 0; t < NS; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sc[t][e] = 0.0f;
+#pragma unroll
+    for (int g = 0; g < DK / 8; ++g)
+#pragma unroll
+        for (int t = 0; t < NS; ++t) {
+            const float4 kf = *reinterpret_cast<const float4*>(&ks[(32 * t + col) * KP + 8 * g + 4 * hf]);
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                sc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32((&kf.x)[c], (&qf[g].x)[c], sc[t], 0, 0, 0);
+        }
+
+    // element e of tile t is key 32t + 8(e/4) + 4hf + e%4 of query qi
+    float m = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < NS; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int j = 32 * t + 8 * (e >> 2) + 4 * hf + (e & 3);
+            float v = scale * sc[t][e];
+            if (j >= S || (causal && j > qi)) v = -INFINITY;
+            sc[t][e] = v;
+            m = v > m ? v : m;
+        }
+    {
+        const float w = __shfl_xor(m, 32, 64);
+        m = w > m ? w : m;
+    }
+    float sum = 0.0f;
+#pragma unroll
+    for (int t = 0; t < NS; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            sc[t][e] = expf(sc[t][e] - m);
+            sum += sc[t][e];
+        }
+    sum += __shfl_xor(sum, 32, 64);
+    const float inv = 1.0f / sum;
+#pragma unroll
+    for (int t = 0; t < NS; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sc[t][e] = sc[t][e] * inv;
+
+    v16f o[DV / 32];
+#pragma unroll
+    for (int u = 0; u < DV / 32; ++u)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[u][e] = 0.0f;
+#pragma unroll
+    for (int t = 0; t < NS; ++t)
+#pragma unroll
+        for (int e4 = 0; e4 < 4; ++e4)
+#pragma unroll
+            for (int u = 0; u < DV / 32; ++u) {
+                const float4 vf = *reinterpret_cast<const float4*>(&vts[(32 * u + col) * VP + 32 * t + 8 * e4 + 4 * hf]);
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    o[u] = __builtin_amdgcn_mfma_f32_32x32x2f32((&vf.x)[c], sc[t][4 * e4 + c], o[u], 0, 0, 0);
+            }
+    if (qi >= Rq) return;
+    // element e of o[u] is ctx column 32u + 8(e/4) + 4hf + e%4 of query qi
+    float* y = ctx + ((size_t)b * Rq + qi) * ldv + (size_t)h * DV + 4 * hf;
+#pragma unroll
+    for (int u = 0; u < DV / 32; ++u)
+#pragma unroll
+        for (int e4 = 0; e4 < 4; ++e4)
+            *reinterpret_cast<float4*>(y + 32 * u + 8 * e4) =
+                make_float4(o[u][4 * e4], o[u][4 * e4 + 1], o[u][4 * e4 + 2], o[u][4 * e4 + 3]);
+}
+
+template <int NS, int D>
+int launch_fused(const float* Q, const float* K, const float* V, float* ctx, int B, int H, int Rq, int S, float scale,
+                 int causal, hipStream_t s, const char* name)
+{
+    hipLaunchKernelGGL((attention_fused<NS, D, D>), dim3((Rq + 127) / 128, B * H), dim3(256), 0, s, Q, K, V, ctx, H, Rq,
+                       S, scale, causal);
+    return knx::check_launch(name);
+}
+
+// the fused kernel when dk = dv ∈ {32, 64, 128}, S fits its LDS tiles and every row is 16-byte aligned; 1 = not eligible
+int try_fused(const float* Q, const float* K, const float* V, float* ctx, int B, int H, int Rq, int S, int dk, int dv,
+              float scale, int causal, hipStream_t s, const char* name)
+{
+    const char* force = getenv("KNX_ATTN_KERNEL");
+    if (force != nullptr && strcmp(force, "unfused") == 0) return 1;
+    if (dk != dv || (((uintptr_t)Q | (uintptr_t)K | (uintptr_t)V | (uintptr_t)ctx) & 15) != 0) return 1;
+    if ((long long)B * H > 65535) return 1;  // grid.y
+    const int ns = S <= 32 ? 1 : S <= 64 ? 2 : S <= 128 ? 4 : S <= 256 ? 8 : 0;
+    if (ns == 0 || (dk == 128 && ns == 8)) return 1;
+#define KNX_FUSED_NS(D)                                                                                   \
+    switch (ns) {                                                                                        \
+    case 1: return launch_fused<1, D>(Q, K, V, ctx, B, H, Rq, S, scale, causal, s, name);                \
+    case 2: return launch_fused<2, D>(Q, K, V, ctx, B, H, Rq, S, scale, causal, s, name);                \
+    case 4: return launch_fused<4, D>(Q, K, V, ctx, B, H, Rq, S, scale, causal, s, name);                \
+    default: return launch_fused<8, D>(Q, K, V, ctx, B, H, Rq, S, scale, causal, s, name);               \
+    }
+    switch (dk) {
+    case 32: KNX_FUSED_NS(32)
+    case 64: KNX_FUSED_NS(64)
+    case 128:
+        switch (ns) {
+        case 1: return launch_fused<1, 128>(Q, K, V, ctx, B, H, Rq, S, scale, causal, s, name);
+        case 2: return launch_fused<2, 128>(Q, K, V, ctx, B, H, Rq, S, scale, causal, s, name);
+        default: return launch_fused<4, 128>(Q, K, V, ctx, B, H, Rq, S, scale, causal, s, name);
+        }
+    default: return 1;
+    }
+#undef KNX_FUSED_NS
+}
+
+}  // namespace
+
+extern "C" int knx_hip_attention_core_vt(const float* Q, const float* K, const float* V, float* vt, float* ctx,
+                                         float* scores, int B, int H, int Rq, int S, int dk, int dv, float scale,
+                                         int causal, void* stream)
 {
     const char* name = "knx_hip_attention_core";
     KNX_ENTRY(name);
     KNX_REQUIRE(B >= 0 && H >= 1 && Rq >= 1 && S >= 1 && dk >= 1 && dv >= 1, name);
     if (B == 0) return KNX_OK;
     KNX_REQUIRE(Q && K && V && ctx && scores, name);
-    KNX_REQUIRE((long long)B * H * Rq * S <= (1LL << 40), name);
+    KNX_REQUIRE((long long)B * H * Rq * S <= (1LL << 40) && (long long)B * S * H * dv <= 0x7fffffffLL, name);
     hipStream_t s = knx::as_stream(stream);
+    int rc = try_fused(Q, K, V, ctx, B, H, Rq, S, dk, dv, scale, causal, s, name);
+    if (rc != 1) return rc;
     const long long hdk = (long long)H * dk, hdv = (long long)H * dv, RS = (long long)Rq * S;
-    int rc = knx_sgemm_batched(Rq, S, dk, Q, (int)hdk, Rq * hdk, dk, K, (int)hdk, S * hdk, dk, true, scores, S, H * RS, RS,
+    rc = knx_sgemm_batched(Rq, S, dk, Q, (int)hdk, Rq * hdk, dk, K, (int)hdk, S * hdk, dk, true, scores, S, H * RS, RS,
                                B, H, scale, causal, s);
     if (rc != KNX_OK) return rc;
     rc = knx_hip_softmax(scores, scores, B * H * Rq, S, stream);
     if (rc != KNX_OK) return rc;
-    return knx_sgemm_batched(Rq, dv, S, scores, S, H * RS, RS, V, (int)hdv, S * hdv, dv, false, ctx, (int)hdv, Rq * hdv, dv,
-                             B, H, 1.0f, 0, s);
+    if (vt == nullptr)
+        return knx_sgemm_batched(Rq, dv, S, scores, S, H * RS, RS, V, (int)hdv, S * hdv, dv, false, ctx, (int)hdv, Rq * hdv,
+                                 dv, B, H, 1.0f, 0, s);
+    // P·V as an NT product against Vᵀ: head h of batch b is rows h·dv.. of Vt, columns b·S.. (row stride B·S)
+    const int R = B * S, C = (int)hdv;
+    KNX_REQUIRE((C + 31) / 32 <= 65535, name);
+    hipLaunchKernelGGL(transpose_kernel, dim3((R + 31) / 32, (C + 31) / 32), dim3(256), 0, s, V, R, C, vt);
+    rc = knx::check_launch(name);
+    if (rc != KNX_OK) return rc;
+    return knx_sgemm_batched(Rq, dv, S, scores, S, H * RS, RS, vt, R, S, (long long)dv * R, true, ctx, (int)hdv, Rq * hdv,
+                             dv, B, H, 1.0f, 0, s);
+}
+
+extern "C" int knx_hip_attention_core(const float* Q, const float* K, const float* V, float* ctx, float* scores, int B,
+                                      int H, int Rq, int S, int dk, int dv, float scale, int causal, void* stream)
+{
+    return knx_hip_attention_core_vt(Q, K, V, nullptr, ctx, scores, B, H, Rq, S, dk, dv, scale, causal, stream);
 }

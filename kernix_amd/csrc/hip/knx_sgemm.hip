@@ -457,7 +457,9 @@ int launch_k32(SgArgs p, int batch, hipStream_t s, const char* name)
 // the pipelined kernel needs K % 32 == 0, 16-byte aligned rows and whole tiles inside M and N
 bool k32_ok(const SgArgs& p, int bm, int bn)
 {
-    return p.K > 0 && p.K % 32 == 0 && p.M >= bm && p.N >= bn && (p.lda & 3) == 0 && (p.ldb & 3) == 0 &&
+    // batch offsets keep every operand base 16-byte aligned
+    const bool strides = ((p.sAb | p.sAh | p.sBb | p.sBh) & 3) == 0;
+    return p.K > 0 && p.K % 32 == 0 && p.M >= bm && p.N >= bn && (p.lda & 3) == 0 && (p.ldb & 3) == 0 && strides &&
            ((uintptr_t)p.A & 15) == 0 && ((uintptr_t)p.B & 15) == 0 && (long)8 * p.lda * 4 < 0x7fffffffL &&
            (long)8 * p.ldb * 4 < 0x7fffffffL;
 }
@@ -473,6 +475,8 @@ int dispatch_nt(SgArgs p, int batch, hipStream_t s, const char* name)
     const bool general = force != nullptr && strcmp(force, "general") == 0;
     if (!general && t256 >= cus && k32_ok(p, 256, 256)) return launch_k32<256, 256, 4, 2>(p, batch, s, name);
     if (!general && t128 >= cus && k32_ok(p, 128, 128)) return launch_k32<128, 128, 2, 2>(p, batch, s, name);
+    const long t64 = (long)((p.M + 127) / 128) * ((p.N + 63) / 64) * batch;
+    if (!general && t64 >= cus && k32_ok(p, 128, 64)) return launch_k32<128, 64, 4, 1>(p, batch, s, name);
     return dispatch<true>(p, batch, s, name);
 }
 
@@ -553,5 +557,5 @@ int knx_sgemm_batched(int M, int N, int K, const float* A, int lda, long long sA
     p.M = M; p.N = N; p.K = K; p.A = A; p.lda = lda; p.B = B; p.ldb = ldb; p.C = C; p.ldc = ldc;
     p.bias = nullptr; p.act = -1; p.act_alpha = 0.0f; p.alpha = alpha; p.causal = causal; p.zh = nh;
     p.sAb = sAb; p.sAh = sAh; p.sBb = sBb; p.sBh = sBh; p.sCb = sCb; p.sCh = sCh;
-    return transB ? dispatch<true>(p, nb * nh, s, name) : dispatch<false>(p, nb * nh, s, name);
+    return transB ? dispatch_nt(p, nb * nh, s, name) : dispatch<false>(p, nb * nh, s, name);
 }

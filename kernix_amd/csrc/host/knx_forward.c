@@ -262,7 +262,7 @@ static int ws_walk(kernix_model* m, size_t B, ws_ctx* c)
             const size_t S = (size_t)vv->r, SR = B * S, H = (size_t)s->heads;
             if (ws_tensor(c, &s->tmp[0], rin, H * s->dk) || ws_tensor(c, &s->tmp[1], SR, H * s->dk) ||
                 ws_tensor(c, &s->tmp[2], SR, H * s->dv) || ws_tensor(c, &s->tmp[3], rin * H, S) ||
-                ws_tensor(c, &s->tmp[4], rin, H * s->dv))
+                ws_tensor(c, &s->tmp[4], rin, H * s->dv) || ws_tensor(c, &s->tmp[5], H * s->dv, SR))
                 return -1;
             break;
         }
@@ -575,7 +575,7 @@ static int run_step(kernix_model* m, int i, int B, void* st)
             hip_ok(knx_hip_sgemm_nt_ep(vk->row, hk, vk->col, vk->tensor, vk->col, d->wk, vk->col, d->bk, -1, 0.0f, K, hk, st), "attention K") ||
             hip_ok(knx_hip_sgemm_nt_ep(vv->row, hv, vv->col, vv->tensor, vv->col, d->wv, vv->col, d->bv, -1, 0.0f, V, hv, st), "attention V"))
             return -1;
-        if (hip_ok(knx_hip_attention_core(Q, K, V, ctx, s->tmp[3]->tensor, B, H, Rq, S, s->dk, s->dv, 1.0f / sqrtf((float)s->dk),
+        if (hip_ok(knx_hip_attention_core_vt(Q, K, V, s->tmp[5]->tensor, ctx, s->tmp[3]->tensor, B, H, Rq, S, s->dk, s->dv, 1.0f / sqrtf((float)s->dk),
                                           s->causal, st), "attention"))
             return -1;
         return hip_ok(knx_hip_sgemm_nt_ep(vq->row, s->out, hv, ctx, hv, d->wo, hv, d->bo, -1, 0.0f, y->tensor, s->out, st),

@@ -288,9 +288,21 @@ def test_conv(L, case, wt):
 
 
 # ---------------------------------------------------------------- attention core
-@pytest.mark.parametrize("B,H,Rq,S,dk,dv,causal", [(2, 2, 5, 5, 4, 4, 1), (2, 8, 128, 128, 64, 64, 0),
-                                                   (1, 3, 7, 9, 16, 8, 0), (3, 4, 33, 33, 32, 32, 1)])
-def test_attention_core(L, B, H, Rq, S, dk, dv, causal):
+# fused: one kernel with K, Vᵀ in LDS (dk = dv ∈ {32, 64, 128}, S ≤ 256); unfused: scores GEMM, softmax, P·V GEMM
+# (the last two shapes of the list reach the pipelined GEMM there, with ragged tiles in the first); unfused_vt: P·V
+# against a transposed copy of V
+ATTN_SHAPES = [(2, 2, 5, 5, 4, 4, 1), (2, 8, 128, 128, 64, 64, 0), (1, 3, 7, 9, 16, 8, 0), (3, 4, 33, 33, 32, 32, 1),
+               (2, 2, 5, 5, 64, 64, 1), (2, 4, 200, 200, 32, 32, 1), (3, 2, 50, 70, 128, 128, 1),
+               (2, 2, 130, 300, 64, 64, 1), (2, 3, 140, 256, 64, 64, 1), (1, 2, 64, 128, 128, 128, 0),
+               (16, 8, 160, 224, 32, 64, 1), (64, 8, 128, 128, 64, 64, 0)]
+
+
+@pytest.mark.parametrize("B,H,Rq,S,dk,dv,causal", ATTN_SHAPES)
+@pytest.mark.parametrize("mode", ["fused", "unfused", "unfused_vt"])
+def test_attention_core(L, B, H, Rq, S, dk, dv, causal, mode, monkeypatch):
+    if mode != "fused":
+        monkeypatch.setenv("KNX_ATTN_KERNEL", "unfused")
+    vt = mode == "unfused_vt"
     rng = np.random.default_rng(B + H + Rq + S)
     Q = rng.standard_normal((B * Rq, H * dk)).astype(np.float32)
     K = rng.standard_normal((B * S, H * dk)).astype(np.float32)
@@ -302,6 +314,12 @@ def test_attention_core(L, B, H, Rq, S, dk, dv, causal):
     ctx = torch.empty((B * Rq, H * dv), dtype=torch.float32, device="cuda")
     sc = torch.empty((B * H * Rq, S), dtype=torch.float32, device="cuda")
     dQ, dK, dV = dev(Q), dev(K), dev(V)
-    hipabi.check(L.knx_hip_attention_core(ptr(dQ), ptr(dK), ptr(dV), ptr(ctx), ptr(sc), B, H, Rq, S, dk, dv,
-                                          float(scale), causal, hipabi.stream()))
+    if vt:
+        dvt = torch.full((H * dv, B * S), float("nan"), dtype=torch.float32, device="cuda")
+        hipabi.check(L.knx_hip_attention_core_vt(ptr(dQ), ptr(dK), ptr(dV), ptr(dvt), ptr(ctx), ptr(sc), B, H, Rq, S,
+                                                 dk, dv, float(scale), causal, hipabi.stream()))
+        assert np.array_equal(host(dvt), V.T)
+    else:
+        hipabi.check(L.knx_hip_attention_core(ptr(dQ), ptr(dK), ptr(dV), ptr(ctx), ptr(sc), B, H, Rq, S, dk, dv,
+                                              float(scale), causal, hipabi.stream()))
     assert rel_err(host(ctx), want) <= 1e-4
