@@ -444,6 +444,83 @@ __global__ void __launch_bounds__(WM * WN * 64) sgemm_k32(SgArgs p)
     }
 }
 
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// Small NT GEMMs (a few dozen 64×64 tiles at most, e.g. a batch of 64 rows through a Linear layer): a 16×16 output
+// tile per block so that the grid still spreads over the chip, K split over the 4 waves (wave w takes the 16-wide
+// k-chunks w, w + 4, …), the partial sums added in wave order through LDS.  Both operands are K-contiguous and read
+// straight from global memory as 16-byte vectors; 16×16×4 fp32 MFMA.  Needs lda, ldb % 4 == 0 and 16-byte aligned
+// A and B (the tail K % 16 is read element by element).
+__global__ void __launch_bounds__(256) sgemm_skinny(SgArgs p)
+{
+    __shared__ float part[4][64 * 4];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane & 15, kq = lane >> 4;
+    const int m0 = blockIdx.y * 16, n0 = blockIdx.x * 16;
+    const float* a = p.A + (size_t)min(m0 + r, p.M - 1) * p.lda + 4 * kq;
+    const float* b = p.B + (size_t)min(n0 + r, p.N - 1) * p.ldb + 4 * kq;
+    // step c of a chunk: half-row kq of the lanes contracts over k = 16·chunk + 4·kq + c, for A and B alike
+    v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    const int nk = p.K / 16;
+    int kc = wave;
+    for (; kc + 12 < nk; kc += 16) {  // four chunks in flight
+        float4 x[4], y[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            x[u] = *reinterpret_cast<const float4*>(a + 16 * (kc + 4 * u));
+            y[u] = *reinterpret_cast<const float4*>(b + 16 * (kc + 4 * u));
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc = __builtin_amdgcn_mfma_f32_16x16x4f32((&x[u].x)[c], (&y[u].x)[c], acc, 0, 0, 0);
+    }
+    for (; kc < nk; kc += 4) {
+        const float4 x = *reinterpret_cast<const float4*>(a + 16 * kc);
+        const float4 y = *reinterpret_cast<const float4*>(b + 16 * kc);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc = __builtin_amdgcn_mfma_f32_16x16x4f32((&x.x)[c], (&y.x)[c], acc, 0, 0, 0);
+    }
+    if (p.K % 16 != 0 && wave == nk % 4) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int k = 16 * nk + 4 * kq + c;  // relative to the row starts below
+            const bool in = k < p.K;
+            const float xa = in ? a[16 * nk + c] : 0.0f, yb = in ? b[16 * nk + c] : 0.0f;
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xa, yb, acc, 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) part[wave][lane * 4 + e] = acc[e];
+    __syncthreads();
+    if (wave != 0) return;
+    // element e of a lane is row 4·kq + e, column r of the tile
+    const int n = n0 + r;
+    if (n >= p.N) return;
+    const float bv = p.bias ? p.bias[n] : 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int m = m0 + 4 * kq + e;
+        if (m >= p.M) break;
+        float v = ((part[0][lane * 4 + e] + part[1][lane * 4 + e]) + part[2][lane * 4 + e]) + part[3][lane * 4 + e];
+        if (p.alpha != 1.0f) v = p.alpha * v;
+        if (p.bias) v = v + bv;
+        if (p.causal && n > m) v = -INFINITY;
+        p.C[(size_t)m * p.ldc + n] = knx_act(v, p.act, p.act_alpha);
+    }
+}
+
+bool skinny_ok(const SgArgs& p, int batch)
+{
+    return batch == 1 && p.K >= 16 && (p.lda & 3) == 0 && (p.ldb & 3) == 0 && ((uintptr_t)p.A & 15) == 0 &&
+           ((uintptr_t)p.B & 15) == 0 && (p.N + 15) / 16 <= 0x7fffffff && (p.M + 15) / 16 <= 65535;
+}
+
+int launch_skinny(SgArgs p, hipStream_t s, const char* name)
+{
+    hipLaunchKernelGGL(sgemm_skinny, dim3((p.N + 15) / 16, (p.M + 15) / 16), dim3(256), 0, s, p);
+    return knx::check_launch(name);
+}
+
 template <int BM, int BN, int WM, int WN>
 int launch_k32(SgArgs p, int batch, hipStream_t s, const char* name)
 {
@@ -470,13 +547,23 @@ int dispatch_nt(SgArgs p, int batch, hipStream_t s, const char* name)
     const long cus = knx::num_cus();
     const long t256 = (long)((p.M + 255) / 256) * ((p.N + 255) / 256) * batch;
     const long t128 = (long)((p.M + 127) / 128) * ((p.N + 127) / 128) * batch;
-    // KNX_SGEMM_KERNEL=general forces the general kernel (tests)
+    // KNX_SGEMM_KERNEL forces the general kernel ("general"), one pipelined tile ("t256", "t128", "t64") or the
+    // small-GEMM kernel ("skinny") where the shape allows it, else the general kernel (tests, tuning)
     const char* force = getenv("KNX_SGEMM_KERNEL");
-    const bool general = force != nullptr && strcmp(force, "general") == 0;
-    if (!general && t256 >= cus && k32_ok(p, 256, 256)) return launch_k32<256, 256, 4, 2>(p, batch, s, name);
-    if (!general && t128 >= cus && k32_ok(p, 128, 128)) return launch_k32<128, 128, 2, 2>(p, batch, s, name);
+    if (force != nullptr && *force) {
+        if (strcmp(force, "t256") == 0 && k32_ok(p, 256, 256)) return launch_k32<256, 256, 4, 2>(p, batch, s, name);
+        if (strcmp(force, "t128") == 0 && k32_ok(p, 128, 128)) return launch_k32<128, 128, 2, 2>(p, batch, s, name);
+        if (strcmp(force, "t64") == 0 && k32_ok(p, 128, 64)) return launch_k32<128, 64, 4, 1>(p, batch, s, name);
+        if (strcmp(force, "skinny") == 0 && skinny_ok(p, batch)) return launch_skinny(p, s, name);
+        return dispatch<true>(p, batch, s, name);
+    }
+    // fewer 64×64 tiles than a quarter of the CUs: 16×16 tiles with split K
+    const long t64x64 = (long)((p.M + 63) / 64) * ((p.N + 63) / 64) * batch;
+    if (t64x64 * 4 < cus && skinny_ok(p, batch)) return launch_skinny(p, s, name);
+    if (t256 >= cus && k32_ok(p, 256, 256)) return launch_k32<256, 256, 4, 2>(p, batch, s, name);
+    if (t128 >= cus && k32_ok(p, 128, 128)) return launch_k32<128, 128, 2, 2>(p, batch, s, name);
     const long t64 = (long)((p.M + 127) / 128) * ((p.N + 63) / 64) * batch;
-    if (!general && t64 >= cus && k32_ok(p, 128, 64)) return launch_k32<128, 64, 4, 1>(p, batch, s, name);
+    if (t64 >= cus && k32_ok(p, 128, 64)) return launch_k32<128, 64, 4, 1>(p, batch, s, name);
     return dispatch<true>(p, batch, s, name);
 }
 

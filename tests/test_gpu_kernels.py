@@ -165,11 +165,25 @@ def test_sgemm_ep(L, M, N, K, act):
 # and the general kernel otherwise
 SGNT_SHAPES = [(256, 256, 64), (300, 200, 96), (1024, 1000, 512), (4096, 1024, 256), (128, 128, 32), (100, 77, 50),
                (512, 512, 30), (2048, 640, 2048)]
+# small GEMMs (split-K 16×16 kernel by default): the int8 MLP's layers at batch 64, ragged M/N, K % 16 ≠ 0
+SGNT_SMALL = [(64, 512, 784), (64, 256, 512), (64, 10, 256), (1, 1, 16), (5, 33, 100), (17, 70, 20), (256, 10, 256),
+              (3, 4000, 4096), (2, 48, 4100)]
 
 
 @pytest.mark.parametrize("M,N,K", SGNT_SHAPES)
 @pytest.mark.parametrize("act", [-1, 0, 1])
 def test_sgemm_nt_ep(L, M, N, K, act):
+    _sgemm_nt_case(L, M, N, K, act)
+
+
+@pytest.mark.parametrize("M,N,K", SGNT_SMALL)
+@pytest.mark.parametrize("kernel", ["", "skinny", "general"])
+def test_sgemm_nt_small(L, M, N, K, kernel, monkeypatch):
+    monkeypatch.setenv("KNX_SGEMM_KERNEL", kernel)
+    _sgemm_nt_case(L, M, N, K, 0)
+
+
+def _sgemm_nt_case(L, M, N, K, act):
     rng = np.random.default_rng(M + 5 * N + 11 * K)
     A = rng.standard_normal((M, K)).astype(np.float32)
     W = (rng.standard_normal((K, N)) / np.sqrt(K)).astype(np.float32)
