@@ -200,8 +200,9 @@ def attention_bench(steps, warmup):
         if env:
             os.environ["KNX_ATTN_KERNEL"] = env
         try:
-            ms, _ = time_launches(lambda: hipabi.check(L.knx_hip_attention_core_vt(
-                P(q), P(k), P(v), P(vt), P(ctx), P(sc), B, H, T, T, d, d, 0.125, 0, S)), steps, warmup)
+            ms, _ = time_launches(lambda: hipabi.check(L.knx_hip_attention_core_ex(
+                P(q), H * d, P(k), H * d, P(v), H * d, P(vt), P(ctx), P(sc), B, H, T, T, d, d, 0.125, 0, S)), steps,
+                warmup)
         finally:
             os.environ.pop("KNX_ATTN_KERNEL", None)
         tf = flops / (ms * 1e-3) / 1e12

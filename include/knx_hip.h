@@ -137,10 +137,12 @@ KNX_API int knx_hip_add_const(const float* x, float* y, int B, int per, const fl
  * scores: scratch of B·H·Rq·S floats used when the fused kernel does not apply (may be NULL otherwise). */
 KNX_API int knx_hip_attention_core(const float* Q, const float* K, const float* V, float* ctx, float* scores, int B,
                                    int H, int Rq, int S, int dk, int dv, float scale, int causal, void* stream);
-/* Same; vt (H·dv × B·S floats, or NULL) is scratch for Vᵀ, which lets P·V run on the pipelined GEMM. */
-KNX_API int knx_hip_attention_core_vt(const float* Q, const float* K, const float* V, float* vt, float* ctx,
-                                      float* scores, int B, int H, int Rq, int S, int dk, int dv, float scale,
-                                      int causal, void* stream);
+/* Same with row strides ldq, ldk, ldv (≥ H·dk, H·dk, H·dv) for Q, K and V — e.g. column slices of one Q|K|V
+ * projection output — and vt (H·dv × B·S floats, or NULL): scratch for Vᵀ, which lets P·V run on the pipelined
+ * GEMM when the fused kernel does not apply.  Same reference loop (include/kernix_model.h:1021-1046). */
+KNX_API int knx_hip_attention_core_ex(const float* Q, int ldq, const float* K, int ldk, const float* V, int ldv,
+                                      float* vt, float* ctx, float* scores, int B, int H, int Rq, int S, int dk,
+                                      int dv, float scale, int causal, void* stream);
 
 /* ---- shape/copy ops for the remaining graph kinds ---- */
 /* Windowed pooling over NHWC (type max/avg, count_pad as PyTorch count_include_pad). */

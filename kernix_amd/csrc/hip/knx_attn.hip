@@ -21,8 +21,9 @@ int knx_sgemm_batched(int M, int N, int K, const float* A, int lda, long long sA
 
 namespace {
 
-// Vt (C × R) = Vᵀ for V (R × C), 32 × 32 tiles through LDS
-__global__ void __launch_bounds__(256) transpose_kernel(const float* __restrict__ v, int R, int C, float* __restrict__ vt)
+// Vt (C × R) = Vᵀ for V (R × C, row stride ldv), 32 × 32 tiles through LDS
+__global__ void __launch_bounds__(256) transpose_kernel(const float* __restrict__ v, int R, int C, int ldv,
+                                                        float* __restrict__ vt)
 {
     __shared__ float tile[32][33];
     const int r0 = blockIdx.x * 32, c0 = blockIdx.y * 32;
@@ -30,7 +31,7 @@ __global__ void __launch_bounds__(256) transpose_kernel(const float* __restrict_
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int r = r0 + ty + 8 * i, c = c0 + tx;
-        tile[ty + 8 * i][tx] = (r < R && c < C) ? v[(size_t)r * C + c] : 0.0f;
+        tile[ty + 8 * i][tx] = (r < R && c < C) ? v[(size_t)r * ldv + c] : 0.0f;
     }
     __syncthreads();
 #pragma unroll
@@ -49,16 +50,16 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 // the two half-waves, and the normalized probabilities are already the B operand of ctxᵀ = V_hᵀ·Pᵀ.  Keys beyond S
 // count as −inf, which leaves max, sum and probabilities as they are over the S keys alone.
 template <int NS, int DK, int DV>
-__global__ void __launch_bounds__(256) attention_fused(const float* __restrict__ Q, const float* __restrict__ K,
-                                                       const float* __restrict__ V, float* __restrict__ ctx, int H,
-                                                       int Rq, int S, float scale, int causal)
+__global__ void __launch_bounds__(256) attention_fused(const float* __restrict__ Q, int ldq, const float* __restrict__ K,
+                                                       int ldk, const float* __restrict__ V, int ldv,
+                                                       float* __restrict__ ctx, int H, int Rq, int S, float scale,
+                                                       int causal)
 {
     constexpr int SK = 32 * NS, KP = DK + 4, VP = SK + 4;  // pitches put rows 4 banks apart
     __shared__ __attribute__((aligned(16))) float ks[SK * KP];
     __shared__ __attribute__((aligned(16))) float vts[DV * VP];
     const int z = blockIdx.y, b = z / H, h = z % H;
     const int tid = threadIdx.x, lane = tid & 63, col = lane & 31, hf = lane >> 5;
-    const size_t ldk = (size_t)H * DK, ldv = (size_t)H * DV;
     const float* Kh = K + (size_t)b * S * ldk + (size_t)h * DK;
     const float* Vh = V + (size_t)b * S * ldv + (size_t)h * DV;
     for (int i = tid; i < SK * (DK / 4); i += 256) {
@@ -78,7 +79,7 @@ __global__ void __launch_bounds__(256) attention_fused(const float* __restrict__
     }
     // Q fragments: at step c of group g, half-wave hf contracts over d = 8g + 4hf + c (K fragments likewise)
     const int qi = blockIdx.x * 128 + (tid >> 6) * 32 + col;
-    const float* Qr = Q + ((size_t)b * Rq + (qi < Rq ? qi : Rq - 1)) * ((size_t)H * DK) + (size_t)h * DK;
+    const float* Qr = Q + ((size_t)b * Rq + (qi < Rq ? qi : Rq - 1)) * ldq + (size_t)h * DK;
     float4 qf[DK / 8];
 #pragma unroll
     for (int g = 0; g < DK / 8; ++g) qf[g] = *reinterpret_cast<const float4*>(Qr + 8 * g + 4 * hf);
@@ -148,7 +149,7 @@ __global__ void __launch_bounds__(256) attention_fused(const float* __restrict__
             }
     if (qi >= Rq) return;
     // element e of o[u] is ctx column 32u + 8(e/4) + 4hf + e%4 of query qi
-    float* y = ctx + ((size_t)b * Rq + qi) * ldv + (size_t)h * DV + 4 * hf;
+    float* y = ctx + ((size_t)b * Rq + qi) * ((size_t)H * DV) + (size_t)h * DV + 4 * hf;
 #pragma unroll
     for (int u = 0; u < DV / 32; ++u)
 #pragma unroll
@@ -157,40 +158,53 @@ __global__ void __launch_bounds__(256) attention_fused(const float* __restrict__
                 make_float4(o[u][4 * e4], o[u][4 * e4 + 1], o[u][4 * e4 + 2], o[u][4 * e4 + 3]);
 }
 
+struct AttnArgs {
+    const float* Q;
+    int ldq;
+    const float* K;
+    int ldk;
+    const float* V;
+    int ldv;
+    float* ctx;
+    int B, H, Rq, S, dk, dv;
+    float scale;
+    int causal;
+};
+
 template <int NS, int D>
-int launch_fused(const float* Q, const float* K, const float* V, float* ctx, int B, int H, int Rq, int S, float scale,
-                 int causal, hipStream_t s, const char* name)
+int launch_fused(const AttnArgs& a, hipStream_t s, const char* name)
 {
-    hipLaunchKernelGGL((attention_fused<NS, D, D>), dim3((Rq + 127) / 128, B * H), dim3(256), 0, s, Q, K, V, ctx, H, Rq,
-                       S, scale, causal);
+    hipLaunchKernelGGL((attention_fused<NS, D, D>), dim3((a.Rq + 127) / 128, a.B * a.H), dim3(256), 0, s, a.Q, a.ldq, a.K,
+                       a.ldk, a.V, a.ldv, a.ctx, a.H, a.Rq, a.S, a.scale, a.causal);
     return knx::check_launch(name);
 }
 
 // the fused kernel when dk = dv ∈ {32, 64, 128}, S fits its LDS tiles and every row is 16-byte aligned; 1 = not eligible
-int try_fused(const float* Q, const float* K, const float* V, float* ctx, int B, int H, int Rq, int S, int dk, int dv,
-              float scale, int causal, hipStream_t s, const char* name)
+int try_fused(const AttnArgs& a, hipStream_t s, const char* name)
 {
     const char* force = getenv("KNX_ATTN_KERNEL");
     if (force != nullptr && strcmp(force, "unfused") == 0) return 1;
-    if (dk != dv || (((uintptr_t)Q | (uintptr_t)K | (uintptr_t)V | (uintptr_t)ctx) & 15) != 0) return 1;
-    if ((long long)B * H > 65535) return 1;  // grid.y
-    const int ns = S <= 32 ? 1 : S <= 64 ? 2 : S <= 128 ? 4 : S <= 256 ? 8 : 0;
-    if (ns == 0 || (dk == 128 && ns == 8)) return 1;
-#define KNX_FUSED_NS(D)                                                                                   \
-    switch (ns) {                                                                                        \
-    case 1: return launch_fused<1, D>(Q, K, V, ctx, B, H, Rq, S, scale, causal, s, name);                \
-    case 2: return launch_fused<2, D>(Q, K, V, ctx, B, H, Rq, S, scale, causal, s, name);                \
-    case 4: return launch_fused<4, D>(Q, K, V, ctx, B, H, Rq, S, scale, causal, s, name);                \
-    default: return launch_fused<8, D>(Q, K, V, ctx, B, H, Rq, S, scale, causal, s, name);               \
+    if (a.dk != a.dv || (((uintptr_t)a.Q | (uintptr_t)a.K | (uintptr_t)a.V | (uintptr_t)a.ctx) & 15) != 0 ||
+        ((a.ldq | a.ldk | a.ldv) & 3) != 0)
+        return 1;
+    if ((long long)a.B * a.H > 65535) return 1;  // grid.y
+    const int ns = a.S <= 32 ? 1 : a.S <= 64 ? 2 : a.S <= 128 ? 4 : a.S <= 256 ? 8 : 0;
+    if (ns == 0 || (a.dk == 128 && ns == 8)) return 1;
+#define KNX_FUSED_NS(D)                                         \
+    switch (ns) {                                              \
+    case 1: return launch_fused<1, D>(a, s, name);             \
+    case 2: return launch_fused<2, D>(a, s, name);             \
+    case 4: return launch_fused<4, D>(a, s, name);             \
+    default: return launch_fused<8, D>(a, s, name);            \
     }
-    switch (dk) {
+    switch (a.dk) {
     case 32: KNX_FUSED_NS(32)
     case 64: KNX_FUSED_NS(64)
     case 128:
         switch (ns) {
-        case 1: return launch_fused<1, 128>(Q, K, V, ctx, B, H, Rq, S, scale, causal, s, name);
-        case 2: return launch_fused<2, 128>(Q, K, V, ctx, B, H, Rq, S, scale, causal, s, name);
-        default: return launch_fused<4, 128>(Q, K, V, ctx, B, H, Rq, S, scale, causal, s, name);
+        case 1: return launch_fused<1, 128>(a, s, name);
+        case 2: return launch_fused<2, 128>(a, s, name);
+        default: return launch_fused<4, 128>(a, s, name);
         }
     default: return 1;
     }
@@ -199,32 +213,36 @@ int try_fused(const float* Q, const float* K, const float* V, float* ctx, int B,
 
 }  // namespace
 
-extern "C" int knx_hip_attention_core_vt(const float* Q, const float* K, const float* V, float* vt, float* ctx,
-                                         float* scores, int B, int H, int Rq, int S, int dk, int dv, float scale,
-                                         int causal, void* stream)
+extern "C" int knx_hip_attention_core_ex(const float* Q, int ldq, const float* K, int ldk, const float* V, int ldv,
+                                         float* vt, float* ctx, float* scores, int B, int H, int Rq, int S, int dk,
+                                         int dv, float scale, int causal, void* stream)
 {
     const char* name = "knx_hip_attention_core";
     KNX_ENTRY(name);
     KNX_REQUIRE(B >= 0 && H >= 1 && Rq >= 1 && S >= 1 && dk >= 1 && dv >= 1, name);
     if (B == 0) return KNX_OK;
-    KNX_REQUIRE(Q && K && V && ctx && scores, name);
+    KNX_REQUIRE(Q && K && V && ctx, name);
+    KNX_REQUIRE((long long)ldq >= (long long)H * dk && (long long)ldk >= (long long)H * dk &&
+                    (long long)ldv >= (long long)H * dv, name);
     KNX_REQUIRE((long long)B * H * Rq * S <= (1LL << 40) && (long long)B * S * H * dv <= 0x7fffffffLL, name);
     hipStream_t s = knx::as_stream(stream);
-    int rc = try_fused(Q, K, V, ctx, B, H, Rq, S, dk, dv, scale, causal, s, name);
+    const AttnArgs a{Q, ldq, K, ldk, V, ldv, ctx, B, H, Rq, S, dk, dv, scale, causal};
+    int rc = try_fused(a, s, name);
     if (rc != 1) return rc;
-    const long long hdk = (long long)H * dk, hdv = (long long)H * dv, RS = (long long)Rq * S;
-    rc = knx_sgemm_batched(Rq, S, dk, Q, (int)hdk, Rq * hdk, dk, K, (int)hdk, S * hdk, dk, true, scores, S, H * RS, RS,
-                               B, H, scale, causal, s);
+    KNX_REQUIRE(scores != nullptr, name);
+    const long long hdv = (long long)H * dv, RS = (long long)Rq * S;
+    rc = knx_sgemm_batched(Rq, S, dk, Q, ldq, Rq * (long long)ldq, dk, K, ldk, S * (long long)ldk, dk, true, scores, S,
+                           H * RS, RS, B, H, scale, causal, s);
     if (rc != KNX_OK) return rc;
     rc = knx_hip_softmax(scores, scores, B * H * Rq, S, stream);
     if (rc != KNX_OK) return rc;
     if (vt == nullptr)
-        return knx_sgemm_batched(Rq, dv, S, scores, S, H * RS, RS, V, (int)hdv, S * hdv, dv, false, ctx, (int)hdv, Rq * hdv,
-                                 dv, B, H, 1.0f, 0, s);
+        return knx_sgemm_batched(Rq, dv, S, scores, S, H * RS, RS, V, ldv, S * (long long)ldv, dv, false, ctx, (int)hdv,
+                                 Rq * hdv, dv, B, H, 1.0f, 0, s);
     // P·V as an NT product against Vᵀ: head h of batch b is rows h·dv.. of Vt, columns b·S.. (row stride B·S)
     const int R = B * S, C = (int)hdv;
     KNX_REQUIRE((C + 31) / 32 <= 65535, name);
-    hipLaunchKernelGGL(transpose_kernel, dim3((R + 31) / 32, (C + 31) / 32), dim3(256), 0, s, V, R, C, vt);
+    hipLaunchKernelGGL(transpose_kernel, dim3((R + 31) / 32, (C + 31) / 32), dim3(256), 0, s, V, R, C, ldv, vt);
     rc = knx::check_launch(name);
     if (rc != KNX_OK) return rc;
     return knx_sgemm_batched(Rq, dv, S, scores, S, H * RS, RS, vt, R, S, (long long)dv * R, true, ctx, (int)hdv, Rq * hdv,
@@ -234,5 +252,6 @@ extern "C" int knx_hip_attention_core_vt(const float* Q, const float* K, const f
 extern "C" int knx_hip_attention_core(const float* Q, const float* K, const float* V, float* ctx, float* scores, int B,
                                       int H, int Rq, int S, int dk, int dv, float scale, int causal, void* stream)
 {
-    return knx_hip_attention_core_vt(Q, K, V, nullptr, ctx, scores, B, H, Rq, S, dk, dv, scale, causal, stream);
+    return knx_hip_attention_core_ex(Q, H * dk, K, H * dk, V, H * dv, nullptr, ctx, scores, B, H, Rq, S, dk, dv, scale,
+                                     causal, stream);
 }

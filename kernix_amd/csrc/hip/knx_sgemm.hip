@@ -221,9 +221,10 @@ int dispatch(SgArgs p, int batch, hipStream_t s, const char* name)
 // 128 zero bytes: the source of the gathered rows that fall in a convolution's zero padding
 __device__ __attribute__((aligned(128))) int8_t knx_zero_line[128];
 
-template <int BM, int BN, int WM, int WN, bool CONV = false>
+template <int BM, int BN, int WM, int WN, bool CONV = false, int STG = 2>
 __global__ void __launch_bounds__(WM * WN * 64) sgemm_k32(SgArgs p)
 {
+    static_assert(STG == 2 || STG == 3, "stages");
     constexpr int NW = WM * WN;
     constexpr int TM = BM / WM, TN = BN / WN;
     constexpr int FM = TM / 32, FN = TN / 32;
@@ -234,7 +235,7 @@ __global__ void __launch_bounds__(WM * WN * 64) sgemm_k32(SgArgs p)
     static_assert(BM % (8 * NW) == 0 && BN % (8 * NW) == 0, "load split");
     static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile");
     static_assert(NW * 16 * (TN + 4) * 4 <= 2 * STAGE, "staging fits in the stages");
-    __shared__ __attribute__((aligned(16))) int8_t lds[2 * STAGE];
+    __shared__ __attribute__((aligned(16))) int8_t lds[STG * STAGE];
 
     const int t = threadIdx.x, lane = t & 63;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -285,7 +286,7 @@ __global__ void __launch_bounds__(WM * WN * 64) sgemm_k32(SgArgs p)
         const int slot = i * NW + wave;
         const bool a = i < SA;
         const int chunk = cl ^ (slot & 7);
-        int8_t* dst = lds + (kt & 1) * STAGE + slot * 1024;
+        int8_t* dst = lds + (kt % STG) * STAGE + slot * 1024;
         if (CONV && a) {
             // k-tile kt is 32 consecutive channels of one tap (the group's channel count is a multiple of 32)
             const knx_conv_geom& g = p.cv;
@@ -319,7 +320,7 @@ __global__ void __launch_bounds__(WM * WN * 64) sgemm_k32(SgArgs p)
     }
     float4 fa[2][FM], fb[2][FN];
     auto read1 = [&](int kt, int q, int j) {  // fragment j (A if j < FM) of quad q
-        const int8_t* cur = lds + (kt & 1) * STAGE;
+        const int8_t* cur = lds + (kt % STG) * STAGE;
         if (j < FM) fa[q & 1][j] = *(const float4*)(cur + aoff[j & 1][q] + j * 4096);
         else fb[q & 1][j - FM] = *(const float4*)(cur + boff[(j - FM) & 1][q] + (j - FM) * 4096);
     };
@@ -337,11 +338,12 @@ __global__ void __launch_bounds__(WM * WN * 64) sgemm_k32(SgArgs p)
 
     // One k-tile, as in the int8 kernel with quads in place of k-steps: quads 0..2 multiply set q & 1 while the
     // fragments of quad q+1 are read; before quad 3's remaining multiplies the wave waits for its loads of tile kt+1
-    // and its own LDS reads, then the barrier hands stage kt & 1 over to the loads of tile kt+2.
+    // (with three stages the loads of tile kt+2 stay in flight: MORE) and its own LDS reads, then the barrier hands
+    // stage kt % STG over to the loads of tile kt+STG.
     constexpr int NM = 4 * FM * FN, NR = FM + FN, PRE = NM / 4;
     constexpr int GAPS = NM - PRE;
-    auto ktile = [&](int kt, auto ARRIVE, auto ISSUE) {
-        constexpr bool arrive = decltype(ARRIVE)::value, iss = decltype(ISSUE)::value;
+    auto ktile = [&](int kt, auto ARRIVE, auto ISSUE, auto MORE) {
+        constexpr bool arrive = decltype(ARRIVE)::value, iss = decltype(ISSUE)::value, more = decltype(MORE)::value;
 #pragma unroll
         for (int q = 0; q < 3; ++q) {
 #pragma unroll
@@ -363,7 +365,10 @@ __global__ void __launch_bounds__(WM * WN * 64) sgemm_k32(SgArgs p)
 #pragma unroll
         for (int j = 0; j < PRE; ++j) mfma1(3, j);
         __builtin_amdgcn_sched_barrier(0);
-        KNX_WAIT_VM_LDS(0);
+        if (more)
+            KNX_WAIT_VM_LDS(SLOTS);
+        else
+            KNX_WAIT_VM_LDS(0);
         knx_barrier_nofence();
         int r = 0, l = 0;
 #pragma unroll
@@ -373,7 +378,7 @@ __global__ void __launch_bounds__(WM * WN * 64) sgemm_k32(SgArgs p)
             while (r < rupto) read1(kt + 1, 0, r++);
             if (iss) {
                 const int upto = (SLOTS * (j - PRE + 1) + GAPS - 1) / GAPS;
-                while (l < upto) issue1(kt + 2, l++);
+                while (l < upto) issue1(kt + STG, l++);
             }
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -382,17 +387,37 @@ __global__ void __launch_bounds__(WM * WN * 64) sgemm_k32(SgArgs p)
     using no = std::integral_constant<bool, false>;
 #pragma unroll
     for (int i = 0; i < SLOTS; ++i) issue1(0, i);
-    KNX_WAIT_VM_LDS(0);
-    knx_barrier_nofence();
-    if (nk > 1)
-#pragma unroll
-        for (int i = 0; i < SLOTS; ++i) issue1(1, i);
-#pragma unroll
-    for (int j = 0; j < NR; ++j) read1(0, 0, j);
     int kt = 0;
-    for (; kt < nk - 2; ++kt) ktile(kt, yes{}, yes{});
-    if (nk >= 2) ktile(kt++, yes{}, no{});
-    ktile(kt, no{}, no{});
+    if (STG == 2) {
+        KNX_WAIT_VM_LDS(0);
+        knx_barrier_nofence();
+        if (nk > 1)
+#pragma unroll
+            for (int i = 0; i < SLOTS; ++i) issue1(1, i);
+#pragma unroll
+        for (int j = 0; j < NR; ++j) read1(0, 0, j);
+        for (; kt < nk - 2; ++kt) ktile(kt, yes{}, yes{}, no{});
+        if (nk >= 2) ktile(kt++, yes{}, no{}, no{});
+    } else {
+        // tiles 0 and 1 in flight, wait for tile 0; tile 2 goes out once every wave is past the barrier
+        if (nk > 1) {
+#pragma unroll
+            for (int i = 0; i < SLOTS; ++i) issue1(1, i);
+            KNX_WAIT_VM_LDS(SLOTS);
+        } else {
+            KNX_WAIT_VM_LDS(0);
+        }
+        knx_barrier_nofence();
+        if (nk > 2)
+#pragma unroll
+            for (int i = 0; i < SLOTS; ++i) issue1(2, i);
+#pragma unroll
+        for (int j = 0; j < NR; ++j) read1(0, 0, j);
+        for (; kt < nk - 3; ++kt) ktile(kt, yes{}, yes{}, yes{});
+        if (kt < nk - 2) ktile(kt++, yes{}, no{}, yes{});
+        if (kt < nk - 1) ktile(kt++, yes{}, no{}, no{});
+    }
+    ktile(kt, no{}, no{}, no{});
 
     // Epilogue: each wave stages 16 rows × TN of its accumulators at a time in its own LDS region (row stride TN+4),
     // then every lane writes 4 consecutive columns of a row with one 16-byte store.
@@ -521,13 +546,13 @@ int launch_skinny(SgArgs p, hipStream_t s, const char* name)
     return knx::check_launch(name);
 }
 
-template <int BM, int BN, int WM, int WN>
+template <int BM, int BN, int WM, int WN, int STG = 2>
 int launch_k32(SgArgs p, int batch, hipStream_t s, const char* name)
 {
     p.tiles_m = (p.M + BM - 1) / BM;
     p.tiles_n = (p.N + BN - 1) / BN;
     const unsigned tiles = (unsigned)p.tiles_m * (unsigned)p.tiles_n;
-    hipLaunchKernelGGL((sgemm_k32<BM, BN, WM, WN>), dim3(tiles, batch), dim3(WM * WN * 64), 0, s, p);
+    hipLaunchKernelGGL((sgemm_k32<BM, BN, WM, WN, false, STG>), dim3(tiles, batch), dim3(WM * WN * 64), 0, s, p);
     return knx::check_launch(name);
 }
 
@@ -554,6 +579,9 @@ int dispatch_nt(SgArgs p, int batch, hipStream_t s, const char* name)
         if (strcmp(force, "t256") == 0 && k32_ok(p, 256, 256)) return launch_k32<256, 256, 4, 2>(p, batch, s, name);
         if (strcmp(force, "t128") == 0 && k32_ok(p, 128, 128)) return launch_k32<128, 128, 2, 2>(p, batch, s, name);
         if (strcmp(force, "t64") == 0 && k32_ok(p, 128, 64)) return launch_k32<128, 64, 4, 1>(p, batch, s, name);
+        if (strcmp(force, "t128s3") == 0 && k32_ok(p, 128, 128)) return launch_k32<128, 128, 2, 2, 3>(p, batch, s, name);
+        if (strcmp(force, "t64s3") == 0 && k32_ok(p, 128, 64)) return launch_k32<128, 64, 4, 1, 3>(p, batch, s, name);
+        if (strcmp(force, "t64w2") == 0 && k32_ok(p, 128, 64)) return launch_k32<128, 64, 2, 2>(p, batch, s, name);
         if (strcmp(force, "skinny") == 0 && skinny_ok(p, batch)) return launch_skinny(p, s, name);
         return dispatch<true>(p, batch, s, name);
     }

@@ -66,6 +66,37 @@ static int up_q(int8_t** dq, float** ds, const kernix_qweight* q, void* stream)
 
 static size_t gates(int kind) { return kind == KERNIX_OP_LSTM ? 4 : kind == KERNIX_OP_GRU ? 3 : 1; }
 
+/* ATTENTION whose queries, keys and values all come from one input: Q|K|V are one GEMM against the stacked weights */
+static int attn_self(const kernix_step* s)
+{
+    const int iv = s->inp[s->n_in > 1 ? 1 : 0], ik = s->inp[s->n_in > 2 ? 2 : s->n_in > 1 ? 1 : 0];
+    return iv == s->inp[0] && ik == s->inp[0];
+}
+
+/* [Wqᵀ; Wkᵀ; Wvᵀ] ((2·H·dk + H·dv) × in) and [bq | bk | bv] (zeros for absent biases, NULL if all are absent) */
+static int up_qkv(struct knx_dstep* d, const kernix_step* s, void* stream)
+{
+    const float_tensor* w[3] = { s->w, s->wk, s->wv };
+    const float* b[3] = { s->bias, s->bk, s->bv };
+    const size_t in = (size_t)s->w->row;
+    size_t n = 0;
+    for (int t = 0; t < 3; t++) n += (size_t)w[t]->col;
+    float* h = malloc(sizeof(float) * n * in);
+    float* hb = (b[0] || b[1] || b[2]) ? calloc(n, sizeof(float)) : NULL;
+    int rc = h == NULL || ((b[0] || b[1] || b[2]) && hb == NULL);
+    for (size_t t = 0, off = 0; !rc && t < 3; off += (size_t)w[t]->col, t++) {
+        const size_t c = (size_t)w[t]->col;
+        for (size_t i = 0; i < in; i++)
+            for (size_t j = 0; j < c; j++) h[(off + j) * in + i] = w[t]->tensor[i * c + j];
+        if (b[t]) memcpy(hb + off, b[t], sizeof(float) * c);
+    }
+    if (!rc) rc = up_f(&d->wqkv, h, n * in, stream) || (hb && up_f(&d->bqkv, hb, n, stream));
+    if (!rc) rc = knx_hip_stream_sync(stream) != KNX_OK; /* the copies read h and hb: wait before freeing them */
+    free(h);
+    free(hb);
+    return rc;
+}
+
 static int upload_step(kernix_step* s, void* stream)
 {
     struct knx_dstep* d = calloc(1, sizeof *d);
@@ -116,10 +147,11 @@ static int upload_step(kernix_step* s, void* stream)
         break;
     case KERNIX_OP_ATTENTION: {
         const size_t hk = (size_t)s->heads * s->dk, hv = (size_t)s->heads * s->dv;
-        if (up_tT(&d->w, s->w, stream) || up_f(&d->bias, s->bias, hk, stream) || up_tT(&d->wk, s->wk, stream) ||
-            up_f(&d->bk, s->bk, hk, stream) || up_tT(&d->wv, s->wv, stream) || up_f(&d->bv, s->bv, hv, stream) ||
-            up_tT(&d->wo, s->wo, stream) || up_f(&d->bo, s->bo, (size_t)s->out, stream))
+        if (attn_self(s) ? up_qkv(d, s, stream) != 0
+                         : (up_tT(&d->w, s->w, stream) || up_f(&d->bias, s->bias, hk, stream) || up_tT(&d->wk, s->wk, stream) ||
+                            up_f(&d->bk, s->bk, hk, stream) || up_tT(&d->wv, s->wv, stream) || up_f(&d->bv, s->bv, hv, stream)))
             return -1;
+        if (up_tT(&d->wo, s->wo, stream) || up_f(&d->bo, s->bo, (size_t)s->out, stream)) return -1;
         break;
     }
     default:
@@ -133,7 +165,7 @@ static void free_dstep(kernix_step* s)
     struct knx_dstep* d = s->dev;
     if (d == NULL) return;
     void* p[] = { d->w, d->bias, d->gamma, d->beta, d->cst, d->q, d->qscale, d->rec, d->w_b, d->bias_b, d->q_b,
-                  d->qscale_b, d->rec_b, d->wk, d->wv, d->wo, d->bk, d->bv, d->bo, d->half, d->zero };
+                  d->qscale_b, d->rec_b, d->wk, d->wv, d->wo, d->bk, d->bv, d->bo, d->half, d->zero, d->wqkv, d->bqkv };
     for (size_t i = 0; i < sizeof p / sizeof p[0]; i++) knx_hip_free(p[i]);
     free(d);
     s->dev = NULL;
@@ -260,9 +292,13 @@ static int ws_walk(kernix_model* m, size_t B, ws_ctx* c)
         case KERNIX_OP_ATTENTION: {
             const kernix_val* vv = &m->vals[s->inp[s->n_in > 1 ? 1 : 0]];
             const size_t S = (size_t)vv->r, SR = B * S, H = (size_t)s->heads;
-            if (ws_tensor(c, &s->tmp[0], rin, H * s->dk) || ws_tensor(c, &s->tmp[1], SR, H * s->dk) ||
-                ws_tensor(c, &s->tmp[2], SR, H * s->dv) || ws_tensor(c, &s->tmp[3], rin * H, S) ||
-                ws_tensor(c, &s->tmp[4], rin, H * s->dv) || ws_tensor(c, &s->tmp[5], H * s->dv, SR))
+            /* Q, K, V (one rin × (2·H·dk + H·dv) block for self-attention), scores, context, Vᵀ */
+            if (attn_self(s) ? ws_tensor(c, &s->tmp[0], rin, 2 * H * s->dk + H * s->dv)
+                             : (ws_tensor(c, &s->tmp[0], rin, H * s->dk) || ws_tensor(c, &s->tmp[1], SR, H * s->dk) ||
+                                ws_tensor(c, &s->tmp[2], SR, H * s->dv)))
+                return -1;
+            if (ws_tensor(c, &s->tmp[3], rin * H, S) || ws_tensor(c, &s->tmp[4], rin, H * s->dv) ||
+                ws_tensor(c, &s->tmp[5], H * s->dv, SR))
                 return -1;
             break;
         }
@@ -567,16 +603,28 @@ static int run_step(kernix_model* m, int i, int B, void* st)
         const float_tensor* vk = &m->views[ik];
         const int Rq = vi->r, S = m->vals[iv].r, H = s->heads, hk = H * s->dk, hv = H * s->dv;
         if (B == 0) return 0;
-        float* Q = s->tmp[0]->tensor;
-        float* K = s->tmp[1]->tensor;
-        float* V = s->tmp[2]->tensor;
         float* ctx = s->tmp[4]->tensor;
-        if (hip_ok(knx_hip_sgemm_nt_ep(vq->row, hk, vq->col, vq->tensor, vq->col, d->w, vq->col, d->bias, -1, 0.0f, Q, hk, st), "attention Q") ||
-            hip_ok(knx_hip_sgemm_nt_ep(vk->row, hk, vk->col, vk->tensor, vk->col, d->wk, vk->col, d->bk, -1, 0.0f, K, hk, st), "attention K") ||
-            hip_ok(knx_hip_sgemm_nt_ep(vv->row, hv, vv->col, vv->tensor, vv->col, d->wv, vv->col, d->bv, -1, 0.0f, V, hv, st), "attention V"))
-            return -1;
-        if (hip_ok(knx_hip_attention_core_vt(Q, K, V, s->tmp[5]->tensor, ctx, s->tmp[3]->tensor, B, H, Rq, S, s->dk, s->dv, 1.0f / sqrtf((float)s->dk),
-                                          s->causal, st), "attention"))
+        float *Q, *K, *V;
+        int ldq = hk, ldk = hk, ldv = hv;
+        if (d->wqkv) {
+            const int n = 2 * hk + hv;
+            Q = s->tmp[0]->tensor;
+            K = Q + hk;
+            V = Q + 2 * hk;
+            ldq = ldk = ldv = n;
+            if (hip_ok(knx_hip_sgemm_nt_ep(vq->row, n, vq->col, vq->tensor, vq->col, d->wqkv, vq->col, d->bqkv, -1, 0.0f, Q, n, st), "attention QKV"))
+                return -1;
+        } else {
+            Q = s->tmp[0]->tensor;
+            K = s->tmp[1]->tensor;
+            V = s->tmp[2]->tensor;
+            if (hip_ok(knx_hip_sgemm_nt_ep(vq->row, hk, vq->col, vq->tensor, vq->col, d->w, vq->col, d->bias, -1, 0.0f, Q, hk, st), "attention Q") ||
+                hip_ok(knx_hip_sgemm_nt_ep(vk->row, hk, vk->col, vk->tensor, vk->col, d->wk, vk->col, d->bk, -1, 0.0f, K, hk, st), "attention K") ||
+                hip_ok(knx_hip_sgemm_nt_ep(vv->row, hv, vv->col, vv->tensor, vv->col, d->wv, vv->col, d->bv, -1, 0.0f, V, hv, st), "attention V"))
+                return -1;
+        }
+        if (hip_ok(knx_hip_attention_core_ex(Q, ldq, K, ldk, V, ldv, s->tmp[5]->tensor, ctx, s->tmp[3]->tensor, B, H, Rq, S,
+                                             s->dk, s->dv, 1.0f / sqrtf((float)s->dk), s->causal, st), "attention"))
             return -1;
         return hip_ok(knx_hip_sgemm_nt_ep(vq->row, s->out, hv, ctx, hv, d->wo, hv, d->bo, -1, 0.0f, y->tensor, s->out, st),
                       "attention output");

@@ -29,6 +29,8 @@ struct knx_dstep {
     float* bk;
     float* bv;
     float* bo;
+    float* wqkv;      /* self-attention: [Wqᵀ; Wkᵀ; Wvᵀ], (2·H·dk + H·dv) × in (replaces w, wk, wv) */
+    float* bqkv;      /* [bq | bk | bv] or NULL */
     float* half;      /* RNN AVE merge: u × 0.5 */
     float* zero;      /* u × 0 */
     /* per-chunk scratch inside the workspace arena */

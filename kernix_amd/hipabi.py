@@ -37,7 +37,7 @@ SIGS = {
     "knx_hip_affine": ([P, P, I, I, P, P, P], I),
     "knx_hip_add_const": ([P, P, I, I, P, P], I),
     "knx_hip_attention_core": ([P, P, P, P, P, I, I, I, I, I, I, F, I, P], I),
-    "knx_hip_attention_core_vt": ([P, P, P, P, P, P, I, I, I, I, I, I, F, I, P], I),
+    "knx_hip_attention_core_ex": ([P, I, P, I, P, I, P, P, P, I, I, I, I, I, I, F, I, P], I),
 }
 
 _lib = None

@@ -330,10 +330,35 @@ def test_attention_core(L, B, H, Rq, S, dk, dv, causal, mode, monkeypatch):
     dQ, dK, dV = dev(Q), dev(K), dev(V)
     if vt:
         dvt = torch.full((H * dv, B * S), float("nan"), dtype=torch.float32, device="cuda")
-        hipabi.check(L.knx_hip_attention_core_vt(ptr(dQ), ptr(dK), ptr(dV), ptr(dvt), ptr(ctx), ptr(sc), B, H, Rq, S,
-                                                 dk, dv, float(scale), causal, hipabi.stream()))
+        hipabi.check(L.knx_hip_attention_core_ex(ptr(dQ), H * dk, ptr(dK), H * dk, ptr(dV), H * dv, ptr(dvt), ptr(ctx),
+                                                 ptr(sc), B, H, Rq, S, dk, dv, float(scale), causal, hipabi.stream()))
         assert np.array_equal(host(dvt), V.T)
     else:
         hipabi.check(L.knx_hip_attention_core(ptr(dQ), ptr(dK), ptr(dV), ptr(ctx), ptr(sc), B, H, Rq, S, dk, dv,
                                               float(scale), causal, hipabi.stream()))
+    assert rel_err(host(ctx), want) <= 1e-4
+
+
+@pytest.mark.parametrize("B,H,Rq,dk,dv,causal", [(4, 8, 128, 64, 64, 1), (2, 3, 40, 32, 32, 0), (2, 2, 20, 16, 8, 1),
+                                                 (3, 2, 300, 64, 64, 0)])
+@pytest.mark.parametrize("mode", ["fused", "unfused", "unfused_vt"])
+def test_attention_core_strided(L, B, H, Rq, dk, dv, causal, mode, monkeypatch):
+    """Q, K, V as column slices of one (B·S) × (2·H·dk + H·dv) matrix (the output of a stacked Q|K|V projection)"""
+    if mode != "fused":
+        monkeypatch.setenv("KNX_ATTN_KERNEL", "unfused")
+    S, n = Rq, 2 * H * dk + H * dv
+    rng = np.random.default_rng(7 * B + H + Rq)
+    qkv = rng.standard_normal((B * S, n)).astype(np.float32)
+    Q, K, V = (np.ascontiguousarray(qkv[:, a:b]) for a, b in ((0, H * dk), (H * dk, 2 * H * dk), (2 * H * dk, n)))
+    scale = np.float32(1.0) / np.sqrt(np.float32(dk))
+    want = np.zeros((B * Rq, H * dv), np.float32)
+    knx_ref.lib().ko_attention_core(knx_ref._p(Q), knx_ref._p(K), knx_ref._p(V), knx_ref._p(want), B, H, Rq, S, dk, dv,
+                                    float(scale), causal)
+    d = dev(qkv)
+    at = lambda off: ctypes.c_void_p(d.data_ptr() + 4 * off)  # noqa: E731
+    ctx = torch.empty((B * Rq, H * dv), dtype=torch.float32, device="cuda")
+    sc = torch.empty((B * H * Rq, S), dtype=torch.float32, device="cuda")
+    dvt = torch.empty((H * dv, B * S), dtype=torch.float32, device="cuda") if mode == "unfused_vt" else None
+    hipabi.check(L.knx_hip_attention_core_ex(at(0), n, at(H * dk), n, at(2 * H * dk), n, ptr(dvt), ptr(ctx), ptr(sc),
+                                             B, H, Rq, S, dk, dv, float(scale), causal, hipabi.stream()))
     assert rel_err(host(ctx), want) <= 1e-4
