@@ -42,10 +42,12 @@ __device__ __forceinline__ float knx_act(float x, int act, float alpha)
 {
     switch (act) {
     case 0: return x >= 0.0f ? x : 0.0f;  // threshold at 0 (NaN → 0, as vDSP_vthr and Metal max)
-    case 1: {                              // GELU with Abramowitz–Stegun 7.1.26 erf
-        const float zz = x * 0.70710678f, t = expf(-zz * zz);
+    case 1: {  // GELU with Abramowitz–Stegun 7.1.26 erf; exp and 1/(1 + p·z) on the hardware exp2 / reciprocal
+               // (≤ 1-2 ulp each; the formula's own error is 1.5e-7), as the epilogue of large GEMMs evaluates it
+               // once per output element
         const float z = fabsf(x) * 0.70710678f;
-        const float k = 1.0f / (1.0f + 0.3275911f * z);
+        const float t = __builtin_amdgcn_exp2f(-(z * z) * 1.44269504f);
+        const float k = __builtin_amdgcn_rcpf(1.0f + 0.3275911f * z);
         const float p = k * (0.254829592f + k * (-0.284496736f + k * (1.421413741f + k * (-1.453152027f + k * 1.061405429f))));
         const float e = 1.0f - p * t;
         return 0.5f * x * (1.0f + (x < 0.0f ? -e : e));
