@@ -474,8 +474,16 @@ int launch_pipe(I8Args p, hipStream_t s, const char* name)
 
 // ---------------------------------------------------------------- 128-byte k-tile kernel
 // Each operand row contributes one whole 128-byte cache line per k-tile (a 64-byte k-tile fetches half lines, which
-// wastes half of every L2 → CU transfer).  Two LDS stages of (BM+BN)·128 bytes: the loads of tile kt+1 run under the
-// four 32-byte k-steps of tile kt, with one workgroup barrier per 128 bytes of K.
+// wastes half of every L2 → CU transfer).  The A rows of the tile go through a ring of ASTG LDS stages, the W rows
+// through a ring of two; one workgroup barrier per 128 bytes of K.
+//
+// Why three A stages: the L2 → LDS path of a CU moves a 64-KB k-tile (256 A + 256 W rows) in about the time the
+// MFMAs need for it, so with two stages of both operands the loads of k-tile kt+2, which can only start once every
+// wave is done with stage kt, arrive just when they are needed and the barrier waits for them.  160 KB of LDS holds
+// three 32-KB A stages and two 32-KB W stages: the loads of A k-tile kt+3 are issued together with those of W k-tile
+// kt+2 and have two k-tiles to arrive, and the W loads, issued first, only half the bytes within one k-tile.
+// Vector-memory loads retire in issue order, so the wait for k-tile kt+1 leaves exactly this wave's A loads of
+// k-tile kt+2 outstanding (SA of them).
 //
 // LDS layout: a row holds 8 chunks of 16 bytes, global chunk c of row r at position c ^ swz8(r).  The 16 rows that
 // one quarter-wave of a ds_read_b128 touches (same chunk, consecutive rows) then fall on 16 distinct 16-byte bank
@@ -487,22 +495,25 @@ int launch_pipe(I8Args p, hipStream_t s, const char* name)
 // (row-in-slot · ld + chunk).  A tile that would run past M (or N) is moved back to end at row M (column N): it
 // recomputes a few rows of its neighbour and stores only the rows (columns) it owns, so every operand row it reads
 // exists.  A half k-tile at the end (K % 128 == 64) loads its lower 64 bytes twice and multiplies two k-steps only.
-template <int BM, int BN, int WM, int WN>
+template <int BM, int BN, int WM, int WN, int ASTG, bool EARLY = false>
 __global__ void __launch_bounds__(WM * WN * 64) i8gemm_k128(I8Args p)
 {
     constexpr int NW = WM * WN;
     constexpr int TM = BM / WM, TN = BN / WN;
     constexpr int FM = TM / 32, FN = TN / 32;
-    constexpr int ROWS = BM + BN;
-    constexpr int STAGE = ROWS * 128;      // bytes per k-tile
-    constexpr int SLOTS = ROWS / 8 / NW;   // 1-KB loads (8 rows × 128 bytes) per wave per k-tile
-    constexpr int SA = BM / 8 / NW;        // slots 0..SA-1 load A rows, the rest W rows
+    constexpr int ABYTES = BM * 128, WBYTES = BN * 128;  // one k-tile of A rows / of W rows
+    constexpr int WRING = ASTG * ABYTES;                 // the W ring follows the A ring
+    constexpr int SLOTS = (BM + BN) / 8 / NW;            // 1-KB loads (8 rows × 128 bytes) per wave per k-tile
+    constexpr int SA = BM / 8 / NW;                      // slots 0..SA-1 load A rows, the rest W rows
+    constexpr int SW = SLOTS - SA;
+    constexpr int STG = NW * 16 * (TN + 4) * 4;          // epilogue staging bytes (from offset 0)
+    static_assert(ASTG == 2 || ASTG == 3, "A ring depth");
     static_assert(BM % (8 * NW) == 0 && BN % (8 * NW) == 0 && SLOTS <= 63, "load split");
-    static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile");
-    static_assert(NW * 16 * (TN + 4) * 4 <= 2 * STAGE, "staging fits in the stages");
+    static_assert(TM % 32 == 0 && TN % 32 == 0 && BM % 64 == 0, "wave tile");
+    static_assert(STG <= WRING + WBYTES - BM * 4, "staging below the row scales");
+    static_assert(WRING + 2 * WBYTES <= 160 * 1024, "LDS");
     static_assert(BM <= NW * 64, "one row scale per thread");
-    __shared__ __attribute__((aligned(16))) int8_t lds[2 * STAGE];
-    __shared__ float row_scale[BM];
+    __shared__ __attribute__((aligned(16))) int8_t lds[WRING + 2 * WBYTES];
 
     const int t = threadIdx.x, lane = t & 63;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -530,6 +541,8 @@ __global__ void __launch_bounds__(WM * WN * 64) i8gemm_k128(I8Args p)
     const int cl = (lane & 7) ^ (lane >> 3), rs = lane >> 3;
     const int nk = (p.K + 127) / 128;
     const bool half = (p.K & 127) != 0;
+    auto abuf = [&](int kt) { return lds + (ASTG == 2 ? (kt & 1) : kt % 3) * ABYTES; };
+    auto wbuf = [&](int kt) { return lds + WRING + (kt & 1) * WBYTES; };
     // load slot i of k-tile kt into its stage
     auto issue1 = [&](int kt, int i) {
         const int slot = i * NW + wave;
@@ -538,13 +551,14 @@ __global__ void __launch_bounds__(WM * WN * 64) i8gemm_k128(I8Args p)
         int chunk = cl ^ (slot & 7);
         if (half && kt == nk - 1) chunk &= 3;  // the upper 64 bytes are past K: load the lower ones again (never multiplied)
         const int8_t* base = (a ? tile_a + (size_t)(slot * 8) * ld : tile_w + (size_t)(slot * 8 - BM) * ld) + kt * 128;
-        dma16(base, (unsigned)(rs * ld + chunk * 16), lds + (kt & 1) * STAGE + slot * 1024);
+        int8_t* dst = a ? abuf(kt) + slot * 1024 : wbuf(kt) + (slot - BM / 8) * 1024;
+        dma16(base, (unsigned)(rs * ld + chunk * 16), dst);
     };
 
     const int rl = lane & 31, g = lane >> 5;
     int aoff[4], boff[4];
     {
-        const int ra_ = wm * TM + rl, rb_ = BM + wn * TN + rl;
+        const int ra_ = wm * TM + rl, rb_ = wn * TN + rl;
         const int sa_ = swz8(ra_), sb_ = swz8(rb_);
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
@@ -555,9 +569,8 @@ __global__ void __launch_bounds__(WM * WN * 64) i8gemm_k128(I8Args p)
     // fragment j of k-step s of k-tile kt: j < FM an A fragment, else a W fragment
     v4i fa[2][FM], fb[2][FN];
     auto read1 = [&](int kt, int s, int j) {
-        const int8_t* cur = lds + (kt & 1) * STAGE;
-        if (j < FM) fa[s & 1][j] = *(const v4i*)(cur + aoff[s ^ (2 * (j & 1))] + j * 4096);
-        else fb[s & 1][j - FM] = *(const v4i*)(cur + boff[s ^ (2 * ((j - FM) & 1))] + (j - FM) * 4096);
+        if (j < FM) fa[s & 1][j] = *(const v4i*)(abuf(kt) + aoff[s ^ (2 * (j & 1))] + j * 4096);
+        else fb[s & 1][j - FM] = *(const v4i*)(wbuf(kt) + boff[s ^ (2 * ((j - FM) & 1))] + (j - FM) * 4096);
     };
 
     v16i acc[FM][FN];
@@ -575,16 +588,25 @@ __global__ void __launch_bounds__(WM * WN * 64) i8gemm_k128(I8Args p)
 
     // One k-tile.  K-steps 0..2: multiply fragment set s & 1 while the FM+FN fragments of k-step s+1 are read, one
     // read after each of the first FM+FN multiplies (the reads hide under the MFMA pipeline).  K-step 3: after the
-    // first PRE multiplies the wave waits for its loads of tile kt+1 and for its own LDS reads (which include the last
-    // ones of stage kt & 1), then the workgroup barrier: tile kt+1 is complete in LDS and nobody reads stage kt & 1
-    // any more, so the remaining multiplies are interleaved with the first fragment reads of tile kt+1 and the loads
-    // of tile kt+2 into stage kt & 1.  ARRIVE / ISSUE are compile-time so the steady-state loop has no branches (a
-    // branch merge makes the compiler wait for every outstanding LDS read at the merge); the sched_barrier(0) calls
-    // pin the interleaving.
+    // first PRE multiplies the wave waits for its loads of tile kt+1 (WAITC younger loads may stay outstanding) and for
+    // its own LDS reads (which include the last ones of tile kt), then the workgroup barrier: tile kt+1 is complete in
+    // LDS and nobody reads the stages of tile kt any more, so the remaining multiplies are interleaved with the first
+    // fragment reads of tile kt+1 and the loads into those stages: W rows of tile kt+2 (ISSW), then A rows of tile
+    // kt+ASTG (ISSA).  The flags are compile-time so the steady-state loop has no branches (a branch merge makes the
+    // compiler wait for every outstanding LDS read at the merge); the sched_barrier(0) calls pin the interleaving.
     constexpr int NM = FM * FN, NR = FM + FN, PRE = NM / 4;
     constexpr int GAPS = NM - PRE;
-    auto ktile = [&](int kt, auto ARRIVE, auto ISSUE, bool upper) {
-        constexpr bool arrive = decltype(ARRIVE)::value, iss = decltype(ISSUE)::value;
+    auto ktile = [&](int kt, auto ARRIVE, auto ISSW, auto ISSA, auto WAITC, bool upper) {
+        constexpr bool arrive = decltype(ARRIVE)::value;
+        constexpr bool isw = decltype(ISSW)::value, isa = decltype(ISSA)::value;
+        // EARLY: the A loads (tile kt+2, into the stage tile kt-1 left) go out during k-steps 0..2, one group per
+        // k-step, instead of in the burst after the barrier
+        constexpr bool early = EARLY && ASTG == 3;
+        constexpr int NL = (isw ? SW : 0) + (isa && !early ? SA : 0);
+        auto issue_nth = [&](int l) {  // the l-th load after the barrier: W slots first, then A slots
+            if (isw && l < SW) issue1(kt + 2, SA + l);
+            else issue1(kt + ASTG, l - (isw ? SW : 0));
+        };
 #pragma unroll
         for (int s = 0; s < 3; ++s) {
 #pragma unroll
@@ -598,6 +620,12 @@ __global__ void __launch_bounds__(WM * WN * 64) i8gemm_k128(I8Args p)
                 __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
             }
             __builtin_amdgcn_sched_group_barrier(0x008, NM - NR, 0);
+            if (early && isa) {
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int i = SA * s / 3; i < SA * (s + 1) / 3; ++i) issue1(kt + 2, i);
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
         if (!upper) return;  // a half k-tile: k-steps 2 and 3 are past K
         if (!arrive) {
@@ -608,7 +636,7 @@ __global__ void __launch_bounds__(WM * WN * 64) i8gemm_k128(I8Args p)
 #pragma unroll
         for (int j = 0; j < PRE; ++j) mfma1(3, j);
         __builtin_amdgcn_sched_barrier(0);
-        KNX_WAIT_VM_LDS(0);
+        KNX_WAIT_VM_LDS(decltype(WAITC)::value);
         knx_barrier_nofence();
         int r = 0, l = 0;
 #pragma unroll
@@ -616,15 +644,15 @@ __global__ void __launch_bounds__(WM * WN * 64) i8gemm_k128(I8Args p)
             mfma1(3, j);
             const int rupto = (NR * (j - PRE + 1) + GAPS - 1) / GAPS;  // reads first: they are needed sooner
             while (r < rupto) read1(kt + 1, 0, r++);
-            if (iss) {
-                const int upto = (SLOTS * (j - PRE + 1) + GAPS - 1) / GAPS;  // spread the loads over the gaps
-                while (l < upto) issue1(kt + 2, l++);
-            }
+            const int upto = (NL * (j - PRE + 1) + GAPS - 1) / GAPS;  // spread the loads over the gaps
+            while (l < upto) issue_nth(l++);
             __builtin_amdgcn_sched_barrier(0);
         }
     };
     using yes = std::integral_constant<bool, true>;
     using no = std::integral_constant<bool, false>;
+    using w0 = std::integral_constant<int, 0>;
+    using wa = std::integral_constant<int, ASTG == 3 ? SA : 0>;
 #pragma unroll
     for (int i = 0; i < SLOTS; ++i) issue1(0, i);
     KNX_WAIT_VM_LDS(0);
@@ -635,20 +663,33 @@ __global__ void __launch_bounds__(WM * WN * 64) i8gemm_k128(I8Args p)
 #pragma unroll
     for (int j = 0; j < NR; ++j) read1(0, 0, j);
     int kt = 0;
-    for (; kt < nk - 2; ++kt) ktile(kt, yes{}, yes{}, true);
-    if (nk >= 2) ktile(kt++, yes{}, no{}, true);
-    ktile(kt, no{}, no{}, !half);
+    if (ASTG == 3 && EARLY) {
+        // tile kt issues A(kt+2) during its k-steps 0..2 and W(kt+2) after its barrier
+        for (; kt < nk - 2; ++kt) ktile(kt, yes{}, yes{}, yes{}, wa{}, true);
+    } else if (ASTG == 3) {
+        if (nk > 2)
+#pragma unroll
+            for (int i = 0; i < SA; ++i) issue1(2, i);
+        for (; kt < nk - 3; ++kt) ktile(kt, yes{}, yes{}, yes{}, wa{}, true);
+        if (nk >= 3) ktile(kt++, yes{}, yes{}, no{}, wa{}, true);
+    } else {
+        for (; kt < nk - 2; ++kt) ktile(kt, yes{}, yes{}, yes{}, w0{}, true);
+    }
+    if (nk >= 2) ktile(kt++, yes{}, no{}, no{}, w0{}, true);
+    ktile(kt, no{}, no{}, no{}, w0{}, !half);
 
+    // the row scales go to the W stage that the last k-tile does not use (free since the barrier of k-tile nk-2)
+    float* row_scale = reinterpret_cast<float*>(wbuf(nk) + WBYTES - BM * 4);
     tile_epilogue<BM, BN, WM, WN>(p, acc, lds, row_scale, my_sa, m0, nb, swv, bv, mlo, nlo);
 }
 
-template <int BM, int BN, int WM, int WN>
+template <int BM, int BN, int WM, int WN, int ASTG, bool EARLY = false>
 int launch_k128(I8Args p, hipStream_t s, const char* name)
 {
     p.tiles_m = (p.M + BM - 1) / BM;
     p.tiles_n = (p.N + BN - 1) / BN;
     const unsigned grid = (unsigned)p.tiles_m * (unsigned)p.tiles_n;
-    hipLaunchKernelGGL((i8gemm_k128<BM, BN, WM, WN>), dim3(grid), dim3(WM * WN * 64), 0, s, p);
+    hipLaunchKernelGGL((i8gemm_k128<BM, BN, WM, WN, ASTG, EARLY>), dim3(grid), dim3(WM * WN * 64), 0, s, p);
     return knx::check_launch(name);
 }
 
@@ -1092,10 +1133,14 @@ extern "C" int knx_hip_i8gemm(int M, int N, int K, const int8_t* A, int lda, con
         if (f == "pipe256s3") return launch_pipe<256, 256, 2, 2, 3>(p, s, name);
         if (f == "pipe128") return launch_pipe<128, 128, 2, 2, 4>(p, s, name);
         if (f == "pipe64") return launch_pipe<64, 64, 2, 2, 4>(p, s, name);
-        if (f == "k128" && k128_fits<256, 256>(p)) return launch_k128<256, 256, 2, 2>(p, s, name);
-        if (f == "k128w8" && k128_fits<256, 256>(p)) return launch_k128<256, 256, 2, 4>(p, s, name);
-        if (f == "k128w8t" && k128_fits<256, 256>(p)) return launch_k128<256, 256, 4, 2>(p, s, name);
-        if (f == "k128m" && k128_fits<128, 128>(p)) return launch_k128<128, 128, 2, 2>(p, s, name);
+        if (f == "k128" && k128_fits<256, 256>(p)) return launch_k128<256, 256, 2, 2, 2>(p, s, name);
+        if (f == "k128w8" && k128_fits<256, 256>(p)) return launch_k128<256, 256, 2, 4, 2>(p, s, name);
+        if (f == "k128w8t" && k128_fits<256, 256>(p)) return launch_k128<256, 256, 4, 2, 2>(p, s, name);
+        if (f == "k128w8ta3" && k128_fits<256, 256>(p)) return launch_k128<256, 256, 4, 2, 3>(p, s, name);
+        if (f == "k128w8ta3e" && k128_fits<256, 256>(p)) return launch_k128<256, 256, 4, 2, 3, true>(p, s, name);
+        if (f == "k128w16" && k128_fits<256, 256>(p)) return launch_k128<256, 256, 4, 4, 2>(p, s, name);
+        if (f == "k128m" && k128_fits<128, 128>(p)) return launch_k128<128, 128, 2, 2, 2>(p, s, name);
+        if (f == "k128ma3" && k128_fits<128, 128>(p)) return launch_k128<128, 128, 2, 2, 3>(p, s, name);
         if (f == "pp" && k128_fits<256, 256>(p)) return launch_pp<256, 256>(p, s, name);
         if (f == "skinny" && M <= 64) return M <= 16 ? launch_skinny<1>(p, s, name) : M <= 32 ? launch_skinny<2>(p, s, name) : launch_skinny<4>(p, s, name);
     }
@@ -1104,9 +1149,14 @@ extern "C" int knx_hip_i8gemm(int M, int N, int K, const int8_t* A, int lda, con
     if (M <= 64) return launch_skinny<4>(p, s, name);
     // the largest tile that still gives every CU a workgroup
     const long tiles256 = (long)((M + 255) / 256) * ((N + 255) / 256);
-    if (tiles256 >= knx::num_cus() && k128_fits<256, 256>(p)) return launch_k128<256, 256, 4, 2>(p, s, name);
+    // three A stages with the A loads spread over the k-tile pay off once the K loop is long (4096³: 67.9 against
+    // 69.8-70.5 µs); for short K the deeper prologue costs more than it saves (8192×2048×512: 23.9 against 23.1 µs)
+    if (tiles256 >= knx::num_cus() && k128_fits<256, 256>(p)) {
+        if (K >= 2048) return launch_k128<256, 256, 4, 2, 3, true>(p, s, name);
+        return launch_k128<256, 256, 4, 2, 2>(p, s, name);
+    }
     const long tiles128 = (long)((M + 127) / 128) * ((N + 127) / 128);
-    if (tiles128 >= knx::num_cus() && k128_fits<128, 128>(p)) return launch_k128<128, 128, 2, 2>(p, s, name);
+    if (tiles128 >= knx::num_cus() && k128_fits<128, 128>(p)) return launch_k128<128, 128, 2, 2, 2>(p, s, name);
     return launch_pipe<64, 64, 2, 2, 4>(p, s, name);
 }
 

@@ -64,9 +64,12 @@ def test_i8gemm_bit_exact(L, M, N, K):
     assert np.array_equal(host(Y), want_y)
 
 
-I8_VARIANTS = ["default", "pp", "k128", "k128w8", "k128w8t", "k128m", "pipe256", "pipe256w8", "pipe128", "pipe64", "tile64"]
-# tiles moved back at the M/N edges, half k-tiles (K % 128 == 64), N % 4 != 0, one whole 256x256 tile
-I8_EDGE_SHAPES = [(300, 300, 1024), (520, 700, 320), (257, 259, 192), (256, 256, 64), (640, 384, 4096)]
+I8_VARIANTS = ["default", "pp", "k128", "k128w8", "k128w8t", "k128m", "k128w8ta3", "k128ma3", "k128w8ta3e", "k128w16",
+               "pipe256", "pipe256w8", "pipe128", "pipe64", "tile64"]
+# tiles moved back at the M/N edges, half k-tiles (K % 128 == 64), N % 4 != 0, one whole 256x256 tile, 2..4 k-tiles
+# (every branch of the three-stage A ring's prologue and tail), and an 8 x 8 tile grid split into XCD blocks
+I8_EDGE_SHAPES = [(300, 300, 1024), (520, 700, 320), (257, 259, 192), (256, 256, 64), (640, 384, 4096),
+                  (512, 256, 256), (256, 512, 384), (384, 384, 448), (2048, 2048, 512)]
 
 
 @pytest.mark.parametrize("variant", I8_VARIANTS)
