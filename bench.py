@@ -223,7 +223,9 @@ def measured_traffic():
         return None
 
 
-def forward_bench(name, make, flops, steps, warmup, mode="ref", roof="f32"):
+def forward_bench(name, make, flops, steps, warmup, mode="ref", i8_ops=0.0):
+    """`flops` of one forward, `i8_ops` of them on the int8 MFMA (`i8` mode): the roofline time is the fp32 part at
+    the fp32 MFMA peak plus the int8 part at the int8 peak, and roofline_frac that time over the measured one."""
     import numpy as np
     import torch
 
@@ -260,10 +262,10 @@ def forward_bench(name, make, flops, steps, warmup, mode="ref", roof="f32"):
         e2e = (time.perf_counter() - t0) * 1e3 / n_e2e
         m.close()
     tf = flops / (ms * 1e-3) / 1e12
-    peak = PEAK_F32_TFLOPS if roof == "f32" else PEAK_I8_TOPS
+    ideal_ms = ((flops - i8_ops) / (PEAK_F32_TFLOPS * 1e12) + i8_ops / (PEAK_I8_TOPS * 1e12)) * 1e3
     return dict(batch=B, ms=round(ms, 4), samples_per_s=round(B / (ms * 1e-3), 1),
                 e2e_ms=round(e2e, 3), e2e_samples_per_s=round(B / (e2e * 1e-3), 1),
-                tflops=round(tf, 2), roofline_frac=round(tf / peak, 4), mode=mode)
+                tflops=round(tf, 2), roofline_frac=round(ideal_ms / ms, 4), mode=mode)
 
 
 def main():
@@ -351,14 +353,15 @@ def main():
             "mlp", lambda p: configs.int8_mlp(p, batch=64), configs.mlp_flops(64, (784, 512, 256, 10)), st, fwarm)
         fw["int8_mlp_784_512_256_10_b64_i8"] = forward_bench(
             "mlp", lambda p: configs.int8_mlp(p, batch=64), configs.mlp_flops(64, (784, 512, 256, 10)), st, fwarm,
-            mode="i8", roof="i8")
+            mode="i8", i8_ops=configs.mlp_flops(64, (784, 512, 256, 10)))
         fw["fp32_mlp_4096_4096_4096_1000_b8192"] = forward_bench(
             "f32", lambda p: configs.fp32_mlp(p), configs.mlp_flops(8192, (4096, 4096, 4096, 1000)), st, fwarm)
         fw["cnn_b256"] = forward_bench("cnn", lambda p: configs.cnn(p), configs.cnn_flops(), st, fwarm)
         fw["transformer_4l_d512_b64"] = forward_bench(
             "tr", lambda p: configs.transformer(p), configs.transformer_flops(), st, fwarm)
         fw["transformer_4l_d512_b64_i8"] = forward_bench(
-            "tr", lambda p: configs.transformer(p), configs.transformer_flops(), st, fwarm, mode="i8")
+            "tr", lambda p: configs.transformer(p), configs.transformer_flops(), st, fwarm, mode="i8",
+            i8_ops=configs.transformer_ffn_flops())
         for k, v in fw.items():
             log(f"forward {k}: {v['ms']:.3f} ms  {v['samples_per_s']:.0f} samples/s  {v['tflops']:.1f} TFLOP/s")
         out["forward"] = fw

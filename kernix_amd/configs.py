@@ -129,3 +129,9 @@ def transformer_flops(batch=64, seq=128, d=512, heads=8, ffn=2048, layers=4):
     attn = 2.0 * batch * heads * seq * seq * (d // heads) * 2
     ff = 2.0 * rows * d * ffn * 2
     return layers * (proj + attn + ff)
+
+
+def transformer_ffn_flops(batch=64, seq=128, d=512, ffn=2048, layers=4):
+    """The feed-forward LINEAR layers: the part of transformer_flops that runs on the int8 GEMM in `i8` mode (the
+    attention projections are dequantized to fp32 at load, as the reference does)."""
+    return layers * 2.0 * batch * seq * d * ffn * 2

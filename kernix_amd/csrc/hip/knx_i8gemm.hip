@@ -344,7 +344,7 @@ __global__ void __launch_bounds__(WM * WN * 64) i8gemm_pipe(I8Args p)
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int wm = wave / WN, wn = wave % WN;
     int tm, tn;
-    tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+    tile_of_best(blockIdx.x, p.tiles_m, p.tiles_n, BM, BN, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
 
     // per-lane epilogue constants (this lane's 4 output columns), loaded now so their latency hides under the K loop
@@ -519,7 +519,7 @@ __global__ void __launch_bounds__(WM * WN * 64) i8gemm_k128(I8Args p)
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int wm = wave / WN, wn = wave % WN;
     int tm, tn;
-    tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+    tile_of_best(blockIdx.x, p.tiles_m, p.tiles_n, BM, BN, tm, tn);
     const int mlo = tm * BM, nlo = tn * BN;                  // first row / column this tile owns
     const int m0 = min(mlo, p.M - BM), n0 = min(nlo, p.N - BN);  // first row / column it computes
 
@@ -726,7 +726,7 @@ __global__ void __launch_bounds__(512) i8gemm_pp(I8Args p)
     const int grp = wave >> 2;
     const int wm = wave / WN, wn = wave % WN;
     int tm, tn;
-    tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+    tile_of_best(blockIdx.x, p.tiles_m, p.tiles_n, BM, BN, tm, tn);
     const int mlo = tm * BM, nlo = tn * BN;
     const int m0 = min(mlo, p.M - BM), n0 = min(nlo, p.N - BN);
 
@@ -860,6 +860,172 @@ template <int BM, int BN>
 bool k128_fits(const I8Args& p)
 {
     return p.M >= BM && p.N >= BN && (long)8 * p.lda < 0x7fffffffL && (long)8 * p.ldw < 0x7fffffffL;
+}
+
+// ---------------------------------------------------------------- deep-ring kernel (mid-size M)
+// Shapes whose 256×256 and 128×128 tiles would leave CUs idle (e.g. M = 256, N = K = 4096: 64×64 tiles give every CU
+// one) move little MFMA work per k-tile (a 64×64×128 k-tile is 128 MFMA cycles per SIMD) against 16 KB of loads, so
+// latency decides: S LDS stages of 128-byte k-tiles (whole lines, the same swizzled layout and LDS-DMA loads as
+// i8gemm_k128) keep S−KPI k-tiles in flight per workgroup.  Per iteration of KPI k-tiles: wait until their loads have
+// landed (vmcnt counts the younger ones still in flight), one workgroup barrier (every wave is done with the previous
+// KPI k-tiles, whose stages are free), issue the loads of the k-tiles S−KPI ahead into those stages, read every
+// fragment of the KPI k-tiles at once (one LDS round trip instead of one per k-step), multiply.
+template <int BM, int BN, int WM, int WN, int S, int KPI>
+__global__ void __launch_bounds__(WM * WN * 64) i8gemm_ring(I8Args p)
+{
+    constexpr int NW = WM * WN;
+    constexpr int TM = BM / WM, TN = BN / WN;
+    constexpr int FM = TM / 32, FN = TN / 32;
+    constexpr int ROWS = BM + BN;
+    constexpr int STAGE = ROWS * 128;
+    constexpr int SLOTS = ROWS / 8 / NW;  // 1-KB loads per wave per k-tile
+    constexpr int SA = BM / 8 / NW;
+    static_assert(KPI == 1 || KPI == 2, "k-tiles per iteration");
+    static_assert(BM % (8 * NW) == 0 && BN % (8 * NW) == 0, "load split");
+    static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile");
+    static_assert(S >= 2 * KPI && SLOTS * 6 <= 63, "ring depth and vmcnt range");
+    static_assert(NW * 16 * (TN + 4) * 4 <= S * STAGE, "staging fits in the ring");
+    static_assert(BM <= NW * 64, "one row scale per thread");
+    __shared__ __attribute__((aligned(16))) int8_t lds[S * STAGE];
+    __shared__ float row_scale[BM];
+
+    const int t = threadIdx.x, lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int wm = wave / WN, wn = wave % WN;
+    int tm, tn;
+    tile_of_best(blockIdx.x, p.tiles_m, p.tiles_n, BM, BN, tm, tn);
+    const int mlo = tm * BM, nlo = tn * BN;
+    const int m0 = min(mlo, p.M - BM), n0 = min(nlo, p.N - BN);
+
+    const int nb = n0 + wn * TN + (lane % (TN / 4)) * 4;
+    float swv[4], bv[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        swv[q] = p.Y ? p.sw[nb + q] : 0.0f;
+        bv[q] = p.bias ? p.bias[nb + q] : 0.0f;
+    }
+    const float my_sa = (t < BM && p.Y) ? p.sa[m0 + t] : 0.0f;
+
+    const int8_t* tile_a = p.A + (size_t)m0 * p.lda;
+    const int8_t* tile_w = p.W + (size_t)n0 * p.ldw;
+    const int cl = (lane & 7) ^ (lane >> 3), rs = lane >> 3;
+    const int nk = (p.K + 127) / 128;
+    const bool half = (p.K & 127) != 0;
+    auto issue = [&](int kt) {  // this wave's loads of k-tile kt into stage kt % S
+        int8_t* stage = lds + (kt % S) * STAGE;
+#pragma unroll
+        for (int i = 0; i < SLOTS; ++i) {
+            const int slot = i * NW + wave;
+            const bool a = i < SA;
+            const int ld = a ? p.lda : p.ldw;
+            int chunk = cl ^ (slot & 7);
+            if (half && kt == nk - 1) chunk &= 3;  // past K: the lower 64 bytes again (never multiplied)
+            const int8_t* base = (a ? tile_a + (size_t)(slot * 8) * ld : tile_w + (size_t)(slot * 8 - BM) * ld) + kt * 128;
+            dma16(base, (unsigned)(rs * ld + chunk * 16), stage + slot * 1024);
+        }
+    };
+
+    const int rl = lane & 31, g = lane >> 5;
+    int aoff[4], boff[4];
+    {
+        const int ra_ = wm * TM + rl, rb_ = BM + wn * TN + rl;
+        const int sa_ = swz8(ra_), sb_ = swz8(rb_);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            aoff[s] = ra_ * 128 + (((2 * s + g) ^ sa_) << 4);
+            boff[s] = rb_ * 128 + (((2 * s + g) ^ sb_) << 4);
+        }
+    }
+    // NACC independent accumulator sets (k-step s adds into set s % NACC), so that a wave with few output blocks
+    // still has independent MFMAs to issue back to back; the sets are summed (exact int32 adds) before the epilogue
+    constexpr int NACC = FM * FN >= 4 ? 1 : 4 / (FM * FN);
+    v16i accs[NACC][FM][FN];
+#pragma unroll
+    for (int c = 0; c < NACC; ++c)
+#pragma unroll
+        for (int fi = 0; fi < FM; ++fi)
+#pragma unroll
+            for (int fj = 0; fj < FN; ++fj)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) accs[c][fi][fj][e] = 0;
+
+    // the fragments of NT k-tiles from kt on (4 k-steps each, the last one 2 k-steps when it is a half k-tile), then
+    // their multiplies
+    auto multiply = [&](int kt, auto NTC, bool last_half) {
+        constexpr int NT = decltype(NTC)::value;
+        v4i fa[NT][4][FM], fb[NT][4][FN];
+#pragma unroll
+        for (int u = 0; u < NT; ++u) {
+            const int8_t* stage = lds + ((kt + u) % S) * STAGE;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+#pragma unroll
+                for (int fi = 0; fi < FM; ++fi) fa[u][s][fi] = *(const v4i*)(stage + aoff[s ^ (2 * (fi & 1))] + fi * 4096);
+#pragma unroll
+                for (int fj = 0; fj < FN; ++fj) fb[u][s][fj] = *(const v4i*)(stage + boff[s ^ (2 * (fj & 1))] + fj * 4096);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < NT; ++u)
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                if (last_half && u == NT - 1 && s >= 2) break;
+#pragma unroll
+                for (int fi = 0; fi < FM; ++fi)
+#pragma unroll
+                    for (int fj = 0; fj < FN; ++fj)
+                        accs[s % NACC][fi][fj] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[u][s][fi], fb[u][s][fj],
+                                                                                      accs[s % NACC][fi][fj], 0, 0, 0);
+            }
+    };
+    using one = std::integral_constant<int, 1>;
+    using kpi = std::integral_constant<int, KPI>;
+
+    // k-tile kt lives in stage kt % S; `issued` is the next k-tile to load
+    int issued = 0;
+    for (; issued < min(S - KPI, nk); ++issued) issue(issued);
+    int kt = 0;
+    // steady state: k-tiles kt .. kt+KPI-1 are waited for while kt+KPI .. kt+S-KPI-1 stay in flight; after the
+    // barrier the stages of kt-KPI .. kt-1 are free and take k-tiles kt+S-KPI .. kt+S-1
+    for (; kt + S - 1 < nk; kt += KPI) {
+        KNX_WAIT_VM_LDS(SLOTS * (S - 2 * KPI));
+        knx_barrier_nofence();
+#pragma unroll
+        for (int u = 0; u < KPI; ++u) issue(kt + S - KPI + u);
+        issued = kt + S;
+        multiply(kt, kpi{}, false);
+    }
+    // tail, one k-tile at a time: issued-1-kt younger k-tiles in flight (a smaller count only waits for more)
+    for (; kt < nk; ++kt) {
+        const int young = min(issued - 1 - kt, 6);
+        if (young >= 6) KNX_WAIT_VM_LDS(SLOTS * 6);
+        else if (young == 5) KNX_WAIT_VM_LDS(SLOTS * 5);
+        else if (young == 4) KNX_WAIT_VM_LDS(SLOTS * 4);
+        else if (young == 3) KNX_WAIT_VM_LDS(SLOTS * 3);
+        else if (young == 2) KNX_WAIT_VM_LDS(SLOTS * 2);
+        else if (young == 1) KNX_WAIT_VM_LDS(SLOTS * 1);
+        else KNX_WAIT_VM_LDS(0);
+        knx_barrier_nofence();
+        while (issued < nk && issued <= kt + S - 1) issue(issued++);  // stages of k-tiles < kt are free
+        multiply(kt, one{}, half && kt == nk - 1);
+    }
+#pragma unroll
+    for (int c = 1; c < NACC; ++c)
+#pragma unroll
+        for (int fi = 0; fi < FM; ++fi)
+#pragma unroll
+            for (int fj = 0; fj < FN; ++fj) accs[0][fi][fj] += accs[c][fi][fj];
+    tile_epilogue<BM, BN, WM, WN>(p, accs[0], lds, row_scale, my_sa, m0, nb, swv, bv, mlo, nlo);
+}
+
+template <int BM, int BN, int WM, int WN, int S, int KPI>
+int launch_ring(I8Args p, hipStream_t s, const char* name)
+{
+    p.tiles_m = (p.M + BM - 1) / BM;
+    p.tiles_n = (p.N + BN - 1) / BN;
+    const unsigned grid = (unsigned)p.tiles_m * (unsigned)p.tiles_n;
+    hipLaunchKernelGGL((i8gemm_ring<BM, BN, WM, WN, S, KPI>), dim3(grid), dim3(WM * WN * 64), 0, s, p);
+    return knx::check_launch(name);
 }
 
 // ---------------------------------------------------------------- skinny kernel (M ≤ 64)
@@ -1142,6 +1308,8 @@ extern "C" int knx_hip_i8gemm(int M, int N, int K, const int8_t* A, int lda, con
         if (f == "k128m" && k128_fits<128, 128>(p)) return launch_k128<128, 128, 2, 2, 2>(p, s, name);
         if (f == "k128ma3" && k128_fits<128, 128>(p)) return launch_k128<128, 128, 2, 2, 3>(p, s, name);
         if (f == "pp" && k128_fits<256, 256>(p)) return launch_pp<256, 256>(p, s, name);
+        if (f == "ring64s4" && k128_fits<64, 64>(p)) return launch_ring<64, 64, 2, 2, 4, 1>(p, s, name);
+        if (f == "ring64s8k2" && k128_fits<64, 64>(p)) return launch_ring<64, 64, 2, 2, 8, 2>(p, s, name);
         if (f == "skinny" && M <= 64) return M <= 16 ? launch_skinny<1>(p, s, name) : M <= 32 ? launch_skinny<2>(p, s, name) : launch_skinny<4>(p, s, name);
     }
     if (M <= 16) return launch_skinny<1>(p, s, name);
@@ -1157,6 +1325,9 @@ extern "C" int knx_hip_i8gemm(int M, int N, int K, const int8_t* A, int lda, con
     }
     const long tiles128 = (long)((M + 127) / 128) * ((N + 127) / 128);
     if (tiles128 >= knx::num_cus() && k128_fits<128, 128>(p)) return launch_k128<128, 128, 2, 2, 2>(p, s, name);
+    // fewer tiles than CUs even at 128×128 (e.g. M = 256, N = 4096): one 64×64 tile per workgroup on the deep LDS
+    // ring (M = 256: 13.2 µs against 16.8 for the 64-byte k-tile pipeline)
+    if (k128_fits<64, 64>(p)) return launch_ring<64, 64, 2, 2, 4, 1>(p, s, name);
     return launch_pipe<64, 64, 2, 2, 4>(p, s, name);
 }
 

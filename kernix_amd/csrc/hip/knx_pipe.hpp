@@ -38,6 +38,34 @@ static __device__ __forceinline__ void tile_of(int t, int tiles_m, int tiles_n, 
     }
 }
 
+// Tile order with the XCD split chosen per shape: consecutive workgroups go to consecutive XCDs, and the tile grid is
+// cut into px × (8/px) equal blocks, one per XCD, with the px (of 2, 4, 1, 8 in that order of preference) that gives
+// each XCD the fewest operand rows to hold in its L2 (bm·BM A rows + bn·BN W rows).  M = 256, N = 4096 in 64×64
+// tiles: px = 1 (every XCD holds all 256 A rows and 512 W rows, 3 MB) instead of px = 2 (128 + 1024 rows, 4.5 MB).
+static __device__ __forceinline__ void tile_of_best(int t, int tiles_m, int tiles_n, int BM, int BN, int& tm, int& tn)
+{
+    int px = 0;
+    long best = 0;
+    if (tiles_m * tiles_n >= 64) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int x = c == 0 ? 2 : c == 1 ? 4 : c == 2 ? 1 : 8, y = 8 / x;
+            if (tiles_m % x != 0 || tiles_n % y != 0) continue;
+            const long rows = (long)(tiles_m / x) * BM + (long)(tiles_n / y) * BN;
+            if (px == 0 || rows < best) px = x, best = rows;
+        }
+    }
+    if (px > 0) {
+        const int py = 8 / px, x = t & 7, j = t >> 3;
+        const int bm = tiles_m / px, bn = tiles_n / py;
+        tm = (x / py) * bm + j / bn;
+        tn = (x % py) * bn + j % bn;
+    } else {
+        tm = t / tiles_n;
+        tn = t % tiles_n;
+    }
+}
+
 // 16-byte chunk swizzle of a 128-byte LDS row: chunk c of row r is stored at position c ^ swz8(r).  The 16 rows that
 // one quarter-wave of a ds_read_b128 touches (same chunk, consecutive rows) then fall on 16 distinct 16-byte bank
 // groups, and any 8 consecutive rows on 8; swz8(r + 32) = swz8(r) ^ 4.

@@ -64,7 +64,7 @@ def test_i8gemm_bit_exact(L, M, N, K):
     assert np.array_equal(host(Y), want_y)
 
 
-I8_VARIANTS = ["default", "pp", "k128", "k128w8", "k128w8t", "k128m", "k128w8ta3", "k128ma3", "k128w8ta3e", "k128w16",
+I8_VARIANTS = ["default", "pp", "k128", "k128w8", "k128w8t", "k128m", "k128w8ta3", "k128ma3", "k128w8ta3e", "k128w16", "ring64s4", "ring64s8k2",
                "pipe256", "pipe256w8", "pipe128", "pipe64", "tile64"]
 # tiles moved back at the M/N edges, half k-tiles (K % 128 == 64), N % 4 != 0, one whole 256x256 tile, 2..4 k-tiles
 # (every branch of the three-stage A ring's prologue and tail), and an 8 x 8 tile grid split into XCD blocks
@@ -96,6 +96,33 @@ def test_i8gemm_variants_y_only(L, monkeypatch, variant, M, N, K):
     hipabi.check(L.knx_hip_i8gemm(M, N, K, ptr(dA), K, ptr(dsa), ptr(dW), K, ptr(dsw), None, -1, 0.0, 1,
                                   ptr(Y2), N, None, 0, hipabi.stream()))
     assert np.array_equal(host(Y2), (y0 + plain).astype(np.float32))
+
+
+I8_SKINNY_VARIANTS = ["default", "skinny"]
+# every row-block count (1, 2, 4 blocks of 16), a lone half k-tile (K = 64), trailing half k-tiles (K % 128 == 64)
+I8_SKINNY_SHAPES = [(1, 16, 64), (3, 100, 192), (16, 4096, 4096), (17, 300, 320), (33, 64, 448), (64, 520, 1024),
+                    (1, 4096, 4096)]
+
+
+@pytest.mark.parametrize("variant", I8_SKINNY_VARIANTS)
+@pytest.mark.parametrize("M,N,K", I8_SKINNY_SHAPES)
+def test_i8gemm_skinny_variants(L, monkeypatch, variant, M, N, K):
+    """the M <= 64 kernels: int32 accumulators and the ReLU epilogue bit-exact against the oracle"""
+    monkeypatch.setenv("KNX_I8_KERNEL", variant)
+    rng = np.random.default_rng(11 * M + N + 7 * K)
+    A = rng.integers(-127, 128, (M, K), dtype=np.int8)
+    W = rng.integers(-128, 128, (N, K), dtype=np.int8)
+    sa = rng.uniform(0.001, 0.01, M).astype(np.float32)
+    sw = rng.uniform(0.001, 0.01, N).astype(np.float32)
+    bias = rng.normal(0, 0.1, N).astype(np.float32)
+    want_y, want_acc = knx_ref.i8gemm(A, W, sa, sw, bias, act_id=0)
+    dA, dW, dsa, dsw, db = dev(A), dev(W), dev(sa), dev(sw), dev(bias)
+    Y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    acc = torch.empty((M, N), dtype=torch.int32, device="cuda")
+    hipabi.check(L.knx_hip_i8gemm(M, N, K, ptr(dA), K, ptr(dsa), ptr(dW), K, ptr(dsw), ptr(db), 0, 0.0, 0,
+                                  ptr(Y), N, ptr(acc), N, hipabi.stream()))
+    assert np.array_equal(host(acc), want_acc)
+    assert np.array_equal(host(Y), want_y)
 
 
 def test_i8gemm_accumulate_and_no_bias(L):
