@@ -582,15 +582,22 @@ int dispatch_nt(SgArgs p, int batch, hipStream_t s, const char* name)
         if (strcmp(force, "t128s3") == 0 && k32_ok(p, 128, 128)) return launch_k32<128, 128, 2, 2, 3>(p, batch, s, name);
         if (strcmp(force, "t64s3") == 0 && k32_ok(p, 128, 64)) return launch_k32<128, 64, 4, 1, 3>(p, batch, s, name);
         if (strcmp(force, "t64w2") == 0 && k32_ok(p, 128, 64)) return launch_k32<128, 64, 2, 2>(p, batch, s, name);
+        if (strcmp(force, "t256x128") == 0 && k32_ok(p, 256, 128)) return launch_k32<256, 128, 4, 2>(p, batch, s, name);
+        if (strcmp(force, "t256x192") == 0 && k32_ok(p, 256, 192)) return launch_k32<256, 192, 4, 2>(p, batch, s, name);
+        if (strcmp(force, "t128x256") == 0 && k32_ok(p, 128, 256)) return launch_k32<128, 256, 2, 4>(p, batch, s, name);
         if (strcmp(force, "skinny") == 0 && skinny_ok(p, batch)) return launch_skinny(p, s, name);
         return dispatch<true>(p, batch, s, name);
     }
     // fewer 64×64 tiles than a quarter of the CUs: 16×16 tiles with split K
     const long t64x64 = (long)((p.M + 63) / 64) * ((p.N + 63) / 64) * batch;
     if (t64x64 * 4 < cus && skinny_ok(p, batch)) return launch_skinny(p, s, name);
+    const long t64 = (long)((p.M + 127) / 128) * ((p.N + 63) / 64) * batch;
+    // short K: 128×64 tiles, at least two per CU, so that several workgroups share a CU and one's prologue and
+    // epilogue overlap another's multiplies (Transformer layers at 8192 rows: 8192×512×512 41 µs against 48.5 for
+    // 128×128, 8192×2048×512 151 against 159 for 256×256, 8192×512×2048 134 against 143)
+    if (p.K <= 2048 && t64 >= 2 * cus && k32_ok(p, 128, 64)) return launch_k32<128, 64, 4, 1>(p, batch, s, name);
     if (t256 >= cus && k32_ok(p, 256, 256)) return launch_k32<256, 256, 4, 2>(p, batch, s, name);
     if (t128 >= cus && k32_ok(p, 128, 128)) return launch_k32<128, 128, 2, 2>(p, batch, s, name);
-    const long t64 = (long)((p.M + 127) / 128) * ((p.N + 63) / 64) * batch;
     if (t64 >= cus && k32_ok(p, 128, 64)) return launch_k32<128, 64, 4, 1>(p, batch, s, name);
     return dispatch<true>(p, batch, s, name);
 }
@@ -625,9 +632,22 @@ int knx_conv_k32(const knx_conv_geom* g, const float* x, const float* wt, const 
     p.cv = *g; p.cgc = cg;
     const long cus = knx::num_cus(), groups = g->groups;
     auto tiles = [&](int bm, int bn) { return (long)((M + bm - 1) / bm) * ((N + bn - 1) / bn) * groups; };
+    // KNX_CONV_TILE forces one tile of the pipelined convolution where the shape allows it (tests, tuning)
+    const char* tile = getenv("KNX_CONV_TILE");
+    if (tile != nullptr && *tile) {
+        if (strcmp(tile, "256x256") == 0 && N >= 256 && M >= 256) return launch_conv_k32<256, 256, 4, 2>(p, s, name);
+        if (strcmp(tile, "256x128") == 0 && N >= 128 && M >= 256) return launch_conv_k32<256, 128, 4, 2>(p, s, name);
+        if (strcmp(tile, "128x128") == 0 && N >= 128 && M >= 128) return launch_conv_k32<128, 128, 2, 2>(p, s, name);
+        if (strcmp(tile, "256x64") == 0 && N >= 64 && M >= 256) return launch_conv_k32<256, 64, 4, 1>(p, s, name);
+        if (strcmp(tile, "128x64") == 0 && N >= 64 && M >= 128) return launch_conv_k32<128, 64, 4, 1>(p, s, name);
+        if (strcmp(tile, "128x64w2") == 0 && N >= 64 && M >= 128) return launch_conv_k32<128, 64, 2, 2>(p, s, name);
+    }
     if (N >= 256 && M >= 256 && tiles(256, 256) >= cus) return launch_conv_k32<256, 256, 4, 2>(p, s, name);
     if (N >= 128 && M >= 256 && tiles(256, 128) >= cus) return launch_conv_k32<256, 128, 4, 2>(p, s, name);
     if (N >= 128 && M >= 128 && tiles(128, 128) >= cus) return launch_conv_k32<128, 128, 2, 2>(p, s, name);
+    // 64 output channels: 128×64 tiles on 2×2 waves (CNN conv2, 256×32×32×64 → 64: 189 µs against 209-225 for
+    // 256×64), several workgroups per CU
+    if (N >= 64 && M >= 128 && tiles(128, 64) >= 2 * cus) return launch_conv_k32<128, 64, 2, 2>(p, s, name);
     if (N >= 64 && M >= 256 && tiles(256, 64) >= cus) return launch_conv_k32<256, 64, 4, 1>(p, s, name);
     return 1;
 }

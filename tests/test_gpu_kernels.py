@@ -213,6 +213,17 @@ def test_sgemm_nt_small(L, M, N, K, kernel, monkeypatch):
     _sgemm_nt_case(L, M, N, K, 0)
 
 
+SGNT_VARIANTS = ["t256", "t128", "t64", "t128s3", "t64s3", "t64w2", "t256x128", "t256x192", "t128x256"]
+
+
+@pytest.mark.parametrize("kernel", SGNT_VARIANTS)
+@pytest.mark.parametrize("M,N,K", [(1024, 768, 512), (520, 700, 96), (256, 384, 64)])
+def test_sgemm_nt_variants(L, M, N, K, kernel, monkeypatch):
+    """every forced tile of the pipelined fp32 kernel, with tiles moved back at ragged M/N edges"""
+    monkeypatch.setenv("KNX_SGEMM_KERNEL", kernel)
+    _sgemm_nt_case(L, M, N, K, 1)
+
+
 def _sgemm_nt_case(L, M, N, K, act):
     rng = np.random.default_rng(M + 5 * N + 11 * K)
     A = rng.standard_normal((M, K)).astype(np.float32)
@@ -299,6 +310,9 @@ CONV_CASES = [
     # enough output pixels for the 256 × 64 tile (≥ 512 tiles of 128 on 256 CUs), channel-vector and scalar gathers
     (64, 32, 32, 64, 64, 3, 1, 1, 1, 1),
     (65, 32, 32, 3, 64, 3, 1, 1, 1, 1),
+    # few taps: stride 2 with dilation 2 and ragged edges, 1×1 taps
+    (4, 17, 15, 3, 32, 3, 2, 1, 1, 2),
+    (3, 9, 9, 16, 8, 1, 1, 0, 1, 1),
     # shapes for the pipelined implicit GEMM (channels per group % 32 == 0, enough tiles): 256×64 tiles with groups,
     # dilation 2, 128×128 tiles, stride 2
     (128, 16, 16, 128, 128, 3, 1, 1, 2, 1),
@@ -306,6 +320,19 @@ CONV_CASES = [
     (128, 16, 16, 64, 128, 3, 1, 1, 1, 1),
     (256, 16, 16, 128, 256, 3, 2, 1, 1, 1),
 ]
+
+
+CONV_TILES = ["256x256", "256x128", "128x128", "256x64", "128x64", "128x64w2"]
+CONV_TILE_CASES = [(64, 32, 32, 64, 64, 3, 1, 1, 1, 1), (128, 16, 16, 64, 128, 3, 1, 1, 1, 1),
+                   (256, 16, 16, 128, 256, 3, 2, 1, 1, 1), (128, 16, 16, 128, 128, 3, 1, 1, 2, 1)]
+
+
+@pytest.mark.parametrize("tile", CONV_TILES)
+@pytest.mark.parametrize("case", CONV_TILE_CASES)
+def test_conv_tiles(L, case, tile, monkeypatch):
+    """every forced tile of the pipelined convolution (where the shape allows it) against the direct convolution"""
+    monkeypatch.setenv("KNX_CONV_TILE", tile)
+    test_conv(L, case, True)
 
 
 @pytest.mark.parametrize("case", CONV_CASES)
