@@ -18,6 +18,9 @@
  *                           + kernix_bias_act epilogue                          include/kernix.h:951-977,
  *                                                                               include/kernix_model.h:528-550
  *   knx_hip_conv(_t)        kernix_conv_run (im2col → sgemm → bias_act)         include/kernix_model.h:711-771
+ *   knx_hip_sgemm_nt_ep_res, a LINEAR (or CONV, or ATTENTION's output projection)  include/kernix_model.h:1853-1860,
+ *   knx_hip_conv_t_res,     step followed by the BINARY add of another value:    :1005-1048, :877-906
+ *   knx_hip_i8gemm_res      the step's epilogue adds the other operand
  *   knx_hip_layernorm       kernix_layer_norm_rows_into                         include/kernix.h:667-677
  *   knx_hip_softmax         floats_softmax_into                                 include/kernix.h:652-657
  *   knx_hip_bias_act        kernix_bias_act / ACT step                          include/kernix_model.h:528-541, :1866-1869
@@ -84,6 +87,13 @@ KNX_API int knx_hip_i8gemm(int M, int N, int K, const int8_t* A, int lda, const 
                            const float* sw, const float* bias, int act, float alpha, int accumulate, float* Y, int ldy,
                            int32_t* acc_out, int ldacc, void* stream);
 
+/* The same with an elementwise add fused after the activation: Y = act(((float)acc·sa[m])·sw[n] + bias[n]) + R
+ * (R M×N, stride ldr; R may equal Y), the result of this LINEAR followed by the BINARY add of R
+ * (reference include/kernix_model.h:1853-1860 then :877-906, the same two fp32 roundings). */
+KNX_API int knx_hip_i8gemm_res(int M, int N, int K, const int8_t* A, int lda, const float* sa, const int8_t* W,
+                               int ldw, const float* sw, const float* bias, int act, float alpha, const float* R,
+                               int ldr, float* Y, int ldy, void* stream);
+
 /* dst (K×N row-major fp32) = (float)q[n][k] · scale[n]; q is N×K int8 with row stride ldq bytes. */
 KNX_API int knx_hip_dequant(const int8_t* q, int ldq, const float* scale, int K, int N, float* dst, void* stream);
 /* dst (N×K row-major fp32, the layout of the fp32 weights used with knx_hip_sgemm_nt_ep) = (float)q[n][k] · scale[n]. */
@@ -98,6 +108,11 @@ KNX_API int knx_hip_sgemm_ep(int M, int N, int K, const float* A, int lda, const
  * (both GEMM operands K-contiguous, as in kernix_matmul_ep_into with a transposed B, include/kernix.h:951-977). */
 KNX_API int knx_hip_sgemm_nt_ep(int M, int N, int K, const float* A, int lda, const float* Wt, int ldwt,
                                 const float* bias, int act, float alpha, float* C, int ldc, void* stream);
+/* C = act(A·Wtᵀ + bias) + R (R M×N, stride ldr; R may equal C): a LINEAR followed by the BINARY add of R
+ * (reference include/kernix.h:951-977 then include/kernix_model.h:877-906, the same two fp32 roundings). */
+KNX_API int knx_hip_sgemm_nt_ep_res(int M, int N, int K, const float* A, int lda, const float* Wt, int ldwt,
+                                    const float* bias, int act, float alpha, const float* R, int ldr, float* C, int ldc,
+                                    void* stream);
 
 /* ---- convolution (NHWC, groups, dilation, zero padding) ---- */
 typedef struct {
@@ -113,6 +128,10 @@ KNX_API int knx_hip_conv(const knx_conv_geom* g, const float* x, const float* w,
  * Channel counts per group that are multiples of 32 run on the pipelined implicit GEMM (LDS-DMA gathers). */
 KNX_API int knx_hip_conv_t(const knx_conv_geom* g, const float* x, const float* wt, const float* bias, int act,
                            float alpha, float* y, void* stream);
+/* y = act(conv(x, Wt) + bias) + R (R the same shape as y; R may equal y): a CONV followed by the BINARY add of R
+ * (reference include/kernix_model.h:711-771 then :877-906). */
+KNX_API int knx_hip_conv_t_res(const knx_conv_geom* g, const float* x, const float* wt, const float* bias, int act,
+                               float alpha, const float* R, float* y, void* stream);
 
 /* ---- row and elementwise ops (y may equal x unless noted) ---- */
 KNX_API int knx_hip_layernorm(const float* x, float* y, int rows, int cols, const float* gamma, const float* beta,

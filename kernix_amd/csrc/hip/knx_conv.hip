@@ -11,7 +11,7 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 
 // the pipelined implicit-GEMM kernel (knx_sgemm.hip): returns 1 without launching when the shape does not qualify
 int knx_conv_k32(const knx_conv_geom* g, const float* x, const float* wt, const float* bias, int act, float alpha,
-                 float* y, hipStream_t s, const char* name);
+                 const float* R, float* y, hipStream_t s, const char* name);
 
 namespace {
 
@@ -25,6 +25,7 @@ struct ConvArgs {
     float* y;
     int M, N, K, cg;
     int tiles_n;
+    const float* R;  // residual added after the activation (same layout as y), or null
 };
 
 constexpr int BK = 16;
@@ -225,7 +226,9 @@ __global__ void __launch_bounds__(WM * WN * 64) conv_tile(ConvArgs p)
                 if (m >= M) continue;
                 float v = acc[fi][fj][e];
                 if (p.bias) v = v + bn;
-                p.y[(size_t)m * g.Co + co] = knx_act(v, p.act, p.alpha);
+                v = knx_act(v, p.act, p.alpha);
+                if (p.R) v = v + p.R[(size_t)m * g.Co + co];
+                p.y[(size_t)m * g.Co + co] = v;
             }
     }
 }
@@ -241,8 +244,8 @@ int launch(ConvArgs p, bool vec, hipStream_t s, const char* name)
 }
 
 template <bool TB>
-int conv_entry(const knx_conv_geom* g, const float* x, const float* w, const float* bias, int act, float alpha, float* y,
-               void* stream, const char* name)
+int conv_entry(const knx_conv_geom* g, const float* x, const float* w, const float* bias, int act, float alpha,
+               const float* R, float* y, void* stream, const char* name)
 {
     KNX_ENTRY(name);
     KNX_REQUIRE(g != nullptr, name);
@@ -256,11 +259,11 @@ int conv_entry(const knx_conv_geom* g, const float* x, const float* w, const flo
     KNX_REQUIRE(x && w && y && x != y, name);
     hipStream_t s = knx::as_stream(stream);
     if (TB) {
-        const int rc = knx_conv_k32(g, x, w, bias, act, alpha, y, s, name);
+        const int rc = knx_conv_k32(g, x, w, bias, act, alpha, R, y, s, name);
         if (rc != 1) return rc;
     }
     ConvArgs p{};
-    p.g = *g; p.x = x; p.w = w; p.bias = bias; p.act = act; p.alpha = alpha; p.y = y;
+    p.g = *g; p.x = x; p.w = w; p.bias = bias; p.act = act; p.alpha = alpha; p.y = y; p.R = R;
     p.cg = g->C / g->groups;
     p.M = g->B * g->Ho * g->Wo;
     p.N = g->Co / g->groups;
@@ -281,11 +284,20 @@ int conv_entry(const knx_conv_geom* g, const float* x, const float* w, const flo
 extern "C" int knx_hip_conv(const knx_conv_geom* g, const float* x, const float* w, const float* bias, int act,
                             float alpha, float* y, void* stream)
 {
-    return conv_entry<false>(g, x, w, bias, act, alpha, y, stream, "knx_hip_conv");
+    return conv_entry<false>(g, x, w, bias, act, alpha, nullptr, y, stream, "knx_hip_conv");
 }
 
 extern "C" int knx_hip_conv_t(const knx_conv_geom* g, const float* x, const float* wt, const float* bias, int act,
                               float alpha, float* y, void* stream)
 {
-    return conv_entry<true>(g, x, wt, bias, act, alpha, y, stream, "knx_hip_conv_t");
+    return conv_entry<true>(g, x, wt, bias, act, alpha, nullptr, y, stream, "knx_hip_conv_t");
+}
+
+extern "C" int knx_hip_conv_t_res(const knx_conv_geom* g, const float* x, const float* wt, const float* bias, int act,
+                                  float alpha, const float* R, float* y, void* stream)
+{
+    const char* name = "knx_hip_conv_t_res";
+    KNX_ENTRY(name);
+    KNX_REQUIRE(R != nullptr, name);
+    return conv_entry<true>(g, x, wt, bias, act, alpha, R, y, stream, name);
 }

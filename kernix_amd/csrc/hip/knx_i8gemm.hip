@@ -41,6 +41,8 @@ struct I8Args {
     int32_t* acc;
     int ldacc;
     int tiles_m, tiles_n;
+    const float* R;  // residual added after the activation (same layout as Y, stride ldr), or null
+    int ldr;
 };
 
 // 16-byte chunk swizzle within a 64-byte LDS row: distinct chunks for the rows that share a bank group, whether the
@@ -57,7 +59,9 @@ __device__ __forceinline__ void i8_epilogue(const I8Args& p, int m, int n, int32
     if (p.bias) v = v + p.bias[n];
     float* y = p.Y + (size_t)m * p.ldy + n;
     if (p.accumulate) v = *y + v;
-    *y = knx_act(v, p.act, p.alpha);
+    v = knx_act(v, p.act, p.alpha);
+    if (p.R) v = v + p.R[(size_t)m * p.ldr + n];
+    *y = v;
 }
 
 template <int BM, int BN, int WM, int WN>
@@ -209,6 +213,7 @@ __global__ void __launch_bounds__(WM * WN * 64) i8gemm_tile(I8Args p)
                             if (p.bias) v = v + bv[q];
                             if (p.accumulate) v = (&o.x)[q] + v;
                             r[q] = knx_act(v, p.act, p.alpha);
+                            if (p.R) r[q] = r[q] + p.R[(size_t)m * p.ldr + nb + q];
                         }
                         *reinterpret_cast<float4*>(y) = make_float4(r[0], r[1], r[2], r[3]);
                     }
@@ -237,7 +242,33 @@ __device__ __forceinline__ void store_rows(const I8Args& p, const int* stg, cons
                                            int nlo, int rq, int rpi, int srow, int cq, int nb, const float* swv,
                                            const float* bv, bool vec = true)
 {
-    for (int rr = rq; rr < 16; rr += rpi) {
+    // The residual rows of this round are loaded before any store: inside the store loop each load would wait for
+    // the previous row's store (R and Y may alias), one memory round trip per row.  Loading them first is right even
+    // when R is Y: every element is read before its own store, and no other element's store touches it.
+    typedef float v4r_t __attribute__((ext_vector_type(4)));
+    constexpr int MAXJ = 8;  // rpi ≥ 2
+    v4r_t rres[MAXJ];
+    if (p.R) {
+        const bool rvec = nb >= nlo && (nb & 3) == 0 && (p.ldr & 3) == 0 && ((uintptr_t)p.R & 15) == 0;
+#pragma unroll
+        for (int j = 0; j < MAXJ; ++j) {
+            const int rr = rq + j * rpi, m = m0 + mt0 + rr;
+            rres[j] = v4r_t{0.0f, 0.0f, 0.0f, 0.0f};
+            if (rr >= 16 || m < mlo || m >= p.M) continue;
+            const float* rp = p.R + (size_t)m * p.ldr + nb;
+            if (rvec) {
+                rres[j] = *reinterpret_cast<const v4r_t*>(rp);
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    if (nb + q >= nlo && nb + q < p.N) rres[j][q] = rp[q];
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < MAXJ; ++j) {
+        const int rr = rq + j * rpi;
+        if (rr >= 16) break;
         const int mt = mt0 + rr, m = m0 + mt;
         if (m < mlo || m >= p.M) continue;
         const v4i a = *reinterpret_cast<const v4i*>(&stg[rr * srow + cq]);
@@ -250,6 +281,7 @@ __device__ __forceinline__ void store_rows(const I8Args& p, const int* stg, cons
                 v = v * swv[q];
                 if (p.bias) v = v + bv[q];   // no bias: no addition (x + 0 would turn −0 into +0)
                 r[q] = ACT == 0 ? (v >= 0.0f ? v : 0.0f) : v;
+                if (p.R) r[q] = r[q] + rres[j][q];  // residual after the activation
             }
             // streaming store: the output is written once and never re-read by this kernel
             typedef float v4f_t __attribute__((ext_vector_type(4)));
@@ -268,6 +300,7 @@ __device__ __forceinline__ void store_rows(const I8Args& p, const int* stg, cons
                     if (p.bias) v = v + bv[q];
                     if (p.accumulate) v = (&o.x)[q] + v;
                     r[q] = knx_act(v, p.act, p.alpha);
+                    if (p.R) r[q] = r[q] + rres[j][q];
                 }
                 *reinterpret_cast<float4*>(y) = make_float4(r[0], r[1], r[2], r[3]);
             }
@@ -1267,23 +1300,25 @@ extern "C" int knx_hip_quantize_rows(const float* x, int ldx, int rows, int k, i
     return knx::check_launch(name);
 }
 
-extern "C" int knx_hip_i8gemm(int M, int N, int K, const int8_t* A, int lda, const float* sa, const int8_t* W, int ldw,
-                              const float* sw, const float* bias, int act, float alpha, int accumulate, float* Y, int ldy,
-                              int32_t* acc_out, int ldacc, void* stream)
-{
-    const char* name = "knx_hip_i8gemm";
-    KNX_ENTRY(name);
+// the argument checks shared by the int8 GEMM entry points
+static int i8gemm_check(int M, int N, int K, const int8_t* A, int lda, const float* sa, const int8_t* W, int ldw,
+                        const float* sw, int act, float* Y, int ldy, int32_t* acc_out, int ldacc, const char* name)
+{  // KNX_OK, 1 when there is nothing to compute (M or N is 0), or the error of the first failed check
     KNX_REQUIRE(M >= 0 && N >= 0 && K >= 0 && K % 64 == 0 && K <= 131072, name);
     KNX_REQUIRE(lda >= K && ldw >= K && lda % 16 == 0 && ldw % 16 == 0, name);
     KNX_REQUIRE(act >= -1 && act <= 15, name);
-    if (M == 0 || N == 0) return KNX_OK;
+    if (M == 0 || N == 0) return 1;
     KNX_REQUIRE(Y != nullptr || acc_out != nullptr, name);
     KNX_REQUIRE(Y == nullptr || (ldy >= N && sa != nullptr && sw != nullptr), name);
     KNX_REQUIRE(acc_out == nullptr || ldacc >= N, name);
     KNX_REQUIRE(K == 0 || (A != nullptr && W != nullptr), name);
     KNX_REQUIRE(((uintptr_t)A & 15) == 0 && ((uintptr_t)W & 15) == 0, name);
-    I8Args p{M, N, K, A, lda, sa, W, ldw, sw, bias, act, alpha, accumulate, Y, ldy, acc_out, ldacc, 0, 0};
-    hipStream_t s = knx::as_stream(stream);
+    return KNX_OK;
+}
+
+static int i8gemm_run(I8Args p, hipStream_t s, const char* name)
+{
+    const int M = p.M, N = p.N, K = p.K;
     if (K == 0) {
         // empty inner dimension: the accumulators are all zero; run the smallest tile (loop body never executes)
         return launch_tile<64, 64, 1, 1>(p, s, name);
@@ -1329,6 +1364,31 @@ extern "C" int knx_hip_i8gemm(int M, int N, int K, const int8_t* A, int lda, con
     // ring (M = 256: 13.2 µs against 16.8 for the 64-byte k-tile pipeline)
     if (k128_fits<64, 64>(p)) return launch_ring<64, 64, 2, 2, 4, 1>(p, s, name);
     return launch_pipe<64, 64, 2, 2, 4>(p, s, name);
+}
+
+extern "C" int knx_hip_i8gemm(int M, int N, int K, const int8_t* A, int lda, const float* sa, const int8_t* W, int ldw,
+                              const float* sw, const float* bias, int act, float alpha, int accumulate, float* Y, int ldy,
+                              int32_t* acc_out, int ldacc, void* stream)
+{
+    const char* name = "knx_hip_i8gemm";
+    KNX_ENTRY(name);
+    const int rc = i8gemm_check(M, N, K, A, lda, sa, W, ldw, sw, act, Y, ldy, acc_out, ldacc, name);
+    if (rc != KNX_OK) return rc == 1 ? KNX_OK : rc;
+    I8Args p{M, N, K, A, lda, sa, W, ldw, sw, bias, act, alpha, accumulate, Y, ldy, acc_out, ldacc, 0, 0, nullptr, 0};
+    return i8gemm_run(p, knx::as_stream(stream), name);
+}
+
+extern "C" int knx_hip_i8gemm_res(int M, int N, int K, const int8_t* A, int lda, const float* sa, const int8_t* W,
+                                  int ldw, const float* sw, const float* bias, int act, float alpha, const float* R,
+                                  int ldr, float* Y, int ldy, void* stream)
+{
+    const char* name = "knx_hip_i8gemm_res";
+    KNX_ENTRY(name);
+    const int rc = i8gemm_check(M, N, K, A, lda, sa, W, ldw, sw, act, Y, ldy, nullptr, 0, name);
+    if (rc != KNX_OK) return rc == 1 ? KNX_OK : rc;
+    KNX_REQUIRE(Y != nullptr && R != nullptr && ldr >= N, name);
+    I8Args p{M, N, K, A, lda, sa, W, ldw, sw, bias, act, alpha, 0, Y, ldy, nullptr, 0, 0, 0, R, ldr};
+    return i8gemm_run(p, knx::as_stream(stream), name);
 }
 
 extern "C" int knx_hip_dequant_t(const int8_t* q, int ldq, const float* scale, int K, int N, float* dst, void* stream)

@@ -42,6 +42,8 @@ struct SgArgs {
     int cgc;           // input channels per group
     int zh;        // batch index z = zb·zh + zi
     long long sAb, sAh, sBb, sBh, sCb, sCh;
+    const float* R;  // residual added after the activation (same layout as C, stride ldr), or null; batch 1 only
+    int ldr;
 };
 
 constexpr int BK = 16;
@@ -186,7 +188,9 @@ __global__ void __launch_bounds__(WM * WN * 64) sgemm_tile(SgArgs p)
                 if (p.alpha != 1.0f) v = p.alpha * v;
                 if (p.bias) v = v + bn;
                 if (p.causal && n > m) v = -INFINITY;
-                C[(size_t)m * p.ldc + n] = knx_act(v, p.act, p.act_alpha);
+                float o = knx_act(v, p.act, p.act_alpha);
+                if (p.R) o = o + p.R[(size_t)m * p.ldr + n];
+                C[(size_t)m * p.ldc + n] = o;
             }
     }
 }
@@ -248,6 +252,7 @@ __global__ void __launch_bounds__(WM * WN * 64) sgemm_k32(SgArgs p)
     const float* B;
     float* C;
     const float* bias = p.bias;
+    const float* R = p.R;  // batch 1 only (no batch offset)
     int cbase = 0;
     if (CONV) {  // grid.y = group: its channel slice of x, its rows of Wt, its columns of y and of the bias
         const int grp = blockIdx.y;
@@ -256,6 +261,7 @@ __global__ void __launch_bounds__(WM * WN * 64) sgemm_k32(SgArgs p)
         B = p.B + (size_t)grp * p.N * p.ldb;
         C = p.C + (size_t)grp * p.N;
         if (bias) bias += (size_t)grp * p.N;
+        if (R) R += (size_t)grp * p.N;
     } else {
         const int z = blockIdx.y, zb = z / p.zh, zi = z % p.zh;
         A = p.A + zb * p.sAb + zi * p.sAh;
@@ -429,6 +435,8 @@ __global__ void __launch_bounds__(WM * WN * 64) sgemm_k32(SgArgs p)
 #pragma unroll
     for (int q = 0; q < 4; ++q) bv[q] = bias ? bias[nb + q] : 0.0f;
     const bool vec = nb >= nlo && (p.ldc & 3) == 0 && ((uintptr_t)C & 15) == 0;
+    const bool rvec = nb >= nlo && (nb & 3) == 0 && (p.ldr & 3) == 0 && ((uintptr_t)R & 15) == 0;
+    static_assert(16 % RPI == 0, "rows per store instruction");
     KNX_WAIT_LDS();
     knx_barrier_nofence();  // nobody reads the operand stages any more
 #pragma unroll
@@ -442,7 +450,30 @@ __global__ void __launch_bounds__(WM * WN * 64) sgemm_k32(SgArgs p)
                     stg[(8 * ((e >> 2) - 2 * h) + 4 * g + (e & 3)) * SROW + fj * 32 + rl] = acc[fi][fj][e];
             KNX_WAIT_LDS();
             asm volatile("" ::: "memory");
-            for (int rr = rq; rr < 16; rr += RPI) {
+            // the residual rows of this round, loaded before any store (R and C may alias: a load after a store would
+            // wait for it, one memory round trip per row; every element is still read before its own store)
+            constexpr int NJ = (16 + RPI - 1) / RPI;
+            float4 rres[NJ];
+            if (R) {
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) {
+                    const int rr = rq + j * RPI, m = m0 + wm * TM + fi * 32 + 16 * h + rr;
+                    rres[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+                    if (rr >= 16 || m < mlo) continue;
+                    const float* rp = R + (size_t)m * p.ldr + nb;
+                    if (rvec) {
+                        rres[j] = *reinterpret_cast<const float4*>(rp);
+                    } else {
+#pragma unroll
+                        for (int q = 0; q < 4; ++q)
+                            if (nb + q >= nlo) (&rres[j].x)[q] = rp[q];
+                    }
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                const int rr = rq + j * RPI;  // lanes past 64 / LPR · LPR start at row RPI and stop at row 15
+                if (rr >= 16) break;
                 const int m = m0 + wm * TM + fi * 32 + 16 * h + rr;
                 if (m < mlo) continue;
                 const float4 a = *reinterpret_cast<const float4*>(&stg[rr * SROW + cq]);
@@ -454,6 +485,10 @@ __global__ void __launch_bounds__(WM * WN * 64) sgemm_k32(SgArgs p)
                     if (bias) v = v + bv[q];
                     if (p.causal && nb + q > m) v = -INFINITY;
                     r[q] = knx_act(v, p.act, p.act_alpha);
+                }
+                if (R) {  // residual after the activation: the fused form of a following elementwise add
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) r[q] = r[q] + (&rres[j].x)[q];
                 }
                 float* y = C + (size_t)m * p.ldc + nb;
                 if (vec) {
@@ -530,7 +565,9 @@ __global__ void __launch_bounds__(256) sgemm_skinny(SgArgs p)
         if (p.alpha != 1.0f) v = p.alpha * v;
         if (p.bias) v = v + bv;
         if (p.causal && n > m) v = -INFINITY;
-        p.C[(size_t)m * p.ldc + n] = knx_act(v, p.act, p.act_alpha);
+        float o = knx_act(v, p.act, p.act_alpha);
+        if (p.R) o = o + p.R[(size_t)m * p.ldr + n];
+        p.C[(size_t)m * p.ldc + n] = o;
     }
 }
 
@@ -618,7 +655,7 @@ int launch_conv_k32(SgArgs p, hipStream_t s, const char* name)
 // pixels (M = B·Ho·Wo), K = kh·kw·cg with cg % 32 == 0 so a k-tile is 32 channels of one tap, Wt is Co × K.
 // Returns 1 without launching when the shape does not qualify (the caller then runs the general kernel).
 int knx_conv_k32(const knx_conv_geom* g, const float* x, const float* wt, const float* bias, int act, float alpha,
-                 float* y, hipStream_t s, const char* name)
+                 const float* R, float* y, hipStream_t s, const char* name)
 {
     const int cg = g->C / g->groups, N = g->Co / g->groups;
     const long M = (long)g->B * g->Ho * g->Wo;
@@ -629,6 +666,7 @@ int knx_conv_k32(const knx_conv_geom* g, const float* x, const float* wt, const 
     p.M = (int)M; p.N = N; p.K = g->kh * g->kw * cg;
     p.A = x; p.lda = 0; p.B = wt; p.ldb = p.K; p.C = y; p.ldc = g->Co;
     p.bias = bias; p.act = act; p.act_alpha = alpha; p.alpha = 1.0f; p.causal = 0; p.zh = 1;
+    p.R = R; p.ldr = g->Co;
     p.cv = *g; p.cgc = cg;
     const long cus = knx::num_cus(), groups = g->groups;
     auto tiles = [&](int bm, int bn) { return (long)((M + bm - 1) / bm) * ((N + bn - 1) / bn) * groups; };
@@ -679,6 +717,23 @@ extern "C" int knx_hip_sgemm_nt_ep(int M, int N, int K, const float* A, int lda,
     SgArgs p{};
     p.M = M; p.N = N; p.K = K; p.A = A; p.lda = lda; p.B = Wt; p.ldb = ldwt; p.C = C; p.ldc = ldc;
     p.bias = bias; p.act = act; p.act_alpha = alpha; p.alpha = 1.0f; p.causal = 0; p.zh = 1;
+    return dispatch_nt(p, 1, knx::as_stream(stream), name);
+}
+
+extern "C" int knx_hip_sgemm_nt_ep_res(int M, int N, int K, const float* A, int lda, const float* Wt, int ldwt,
+                                       const float* bias, int act, float alpha, const float* R, int ldr, float* C, int ldc,
+                                       void* stream)
+{
+    const char* name = "knx_hip_sgemm_nt_ep_res";
+    KNX_ENTRY(name);
+    KNX_REQUIRE(M >= 0 && N >= 0 && K >= 0 && act >= -1 && act <= 15, name);
+    if (M == 0 || N == 0) return KNX_OK;
+    KNX_REQUIRE(C != nullptr && ldc >= N && R != nullptr && ldr >= N, name);
+    KNX_REQUIRE(K == 0 || (A != nullptr && Wt != nullptr && lda >= K && ldwt >= K), name);
+    SgArgs p{};
+    p.M = M; p.N = N; p.K = K; p.A = A; p.lda = lda; p.B = Wt; p.ldb = ldwt; p.C = C; p.ldc = ldc;
+    p.bias = bias; p.act = act; p.act_alpha = alpha; p.alpha = 1.0f; p.causal = 0; p.zh = 1;
+    p.R = R; p.ldr = ldr;
     return dispatch_nt(p, 1, knx::as_stream(stream), name);
 }
 

@@ -425,22 +425,34 @@ static void hw(const kernix_val* v, int* H, int* W)
     *W = v->nd == 3 ? v->d[1] : 1;
 }
 
+/* y (rows × n) = act(x·Wtᵀ + bias) [+ res]: the fp32 Linear, with a following elementwise add fused when res is set. */
+static int fp32_linear(int rows, int n, int k, const float* x, const float* wt, const float* bias, int act, float alpha,
+                       const float* res, float* y, void* st)
+{
+    if (res != NULL)
+        return hip_ok(knx_hip_sgemm_nt_ep_res(rows, n, k, x, k, wt, k, bias, act, alpha, res, n, y, n, st), "fp32 GEMM + add");
+    return hip_ok(knx_hip_sgemm_nt_ep(rows, n, k, x, k, wt, k, bias, act, alpha, y, n, st), "fp32 GEMM");
+}
+
 /* y (rows × n) = act(x·W + bias) with int8 weights: int8 arithmetic (per-row int8 input, int32 accumulation) or
  * the fp32 copy, per the model's int8 mode; accumulate adds into y (RNN recurrence). */
 static int run_qlinear(const kernix_model* m, const kernix_qweight* q, const int8_t* dq, const float* dscale,
                        const float_tensor* deq, int8_t* xq, float* sx, int xq_rows, const float* x, int rows,
-                       const float* bias, int act, float alpha, int accumulate, float* y, void* st)
+                       const float* bias, int act, float alpha, int accumulate, const float* res, float* y, void* st)
 {
     const int use_i8 = m->int8_mode == KERNIX_INT8_I8 || rows <= KERNIX_INT8_MAX_ROWS;
     if (use_i8) {
         if (rows > xq_rows || xq == NULL) { KNX_LOG("KERNIX: int8 scratch too small (%d > %d rows)\n", rows, xq_rows); return -1; }
         if (hip_ok(knx_hip_quantize_rows(x, q->k, rows, q->k, q->kp, xq, q->kp, sx, st), "int8 input quantization")) return -1;
+        if (res != NULL)
+            return hip_ok(knx_hip_i8gemm_res(rows, q->n, q->kp, xq, q->kp, sx, dq, q->kp, dscale, bias, act, alpha, res,
+                                             q->n, y, q->n, st), "int8 GEMM + add");
         return hip_ok(knx_hip_i8gemm(rows, q->n, q->kp, xq, q->kp, sx, dq, q->kp, dscale, bias, act, alpha, accumulate, y,
                                      q->n, NULL, 0, st), "int8 GEMM");
     }
     if (deq == NULL) { KNX_LOG("KERNIX: missing fp32 copy of an int8 weight\n"); return -1; }
     if (accumulate) return -1; /* the recurrence adds through a separate buffer on this path */
-    return hip_ok(knx_hip_sgemm_nt_ep(rows, q->n, q->k, x, q->k, deq->tensor, q->k, bias, act, alpha, y, q->n, st), "fp32 GEMM");
+    return fp32_linear(rows, q->n, q->k, x, deq->tensor, bias, act, alpha, res, y, st);
 }
 
 /* One direction of an RNN, reference include/kernix_model.h:563-632: the input projection of all timesteps is one
@@ -480,7 +492,7 @@ static int run_rnn_dir(const kernix_model* m, kernix_step* s, int dir, const flo
             }
         } else if (i8) {
             float* target = kind == KERNIX_OP_GRU ? hu : z;
-            if (run_qlinear(m, q, dq, dsc, NULL, xq, sx, d->xq_rows, h, B, brec, -1, 0.0f, kind != KERNIX_OP_GRU, target, st)) return -1;
+            if (run_qlinear(m, q, dq, dsc, NULL, xq, sx, d->xq_rows, h, B, brec, -1, 0.0f, kind != KERNIX_OP_GRU, NULL, target, st)) return -1;
             rec_term = kind == KERNIX_OP_GRU ? hu : NULL;
         } else {
             if (U == NULL) return -1;
@@ -513,12 +525,14 @@ static int run_rnn(const kernix_model* m, kernix_step* s, const float_tensor* x,
     return 0;
 }
 
-static int run_step(kernix_model* m, int i, int B, void* st)
+/* Step i into y (its own output value, or with `res` set the output of the BINARY add that follows it: then the
+ * step's epilogue adds res, see fusable_add). */
+static int run_step(kernix_model* m, int i, int B, void* st, float_tensor* y_into, const float* res)
 {
     kernix_step* s = &m->steps[i];
     struct knx_dstep* d = s->dev;
     const float_tensor* a = &m->views[s->inp[0]];
-    float_tensor* y = &m->views[i + 1];
+    float_tensor* y = y_into != NULL ? y_into : &m->views[i + 1];
     const kernix_val* vi = &m->vals[s->inp[0]];
     const kernix_val* vo = &m->vals[i + 1];
     const int rows = y->row, cols = y->col;
@@ -526,9 +540,8 @@ static int run_step(kernix_model* m, int i, int B, void* st)
     case KERNIX_OP_LINEAR:
         if (s->q != NULL)
             return run_qlinear(m, s->q, d->q, d->qscale, s->deq, d->xq, d->sx, d->xq_rows, a->tensor, a->row, d->bias,
-                               s->act, s->alpha, 0, y->tensor, st);
-        return hip_ok(knx_hip_sgemm_nt_ep(a->row, s->out, s->in, a->tensor, s->in, d->w, s->in, d->bias, s->act, s->alpha,
-                                          y->tensor, s->out, st), "Linear");
+                               s->act, s->alpha, 0, res, y->tensor, st);
+        return fp32_linear(a->row, s->out, s->in, a->tensor, d->w, d->bias, s->act, s->alpha, res, y->tensor, st);
     case KERNIX_OP_ACT:
         return hip_ok(knx_hip_bias_act(a->tensor, y->tensor, rows, cols, NULL, s->act, s->alpha, st), "activation");
     case KERNIX_OP_LAYERNORM:
@@ -541,8 +554,7 @@ static int run_step(kernix_model* m, int i, int B, void* st)
         return run_rnn(m, s, a, y, st);
     case KERNIX_OP_CONV: {
         if (knx_conv_is_gemm(s) == 0) /* 1×1 stride 1: a GEMM on the NHWC rows */
-            return hip_ok(knx_hip_sgemm_nt_ep(a->row, s->out, s->in, a->tensor, s->in, d->w, s->in, d->bias, s->act, s->alpha,
-                                              y->tensor, s->out, st), "convolution");
+            return fp32_linear(a->row, s->out, s->in, a->tensor, d->w, d->bias, s->act, s->alpha, res, y->tensor, st);
         knx_conv_geom g;
         hw(vi, &g.H, &g.W);
         hw(vo, &g.Ho, &g.Wo);
@@ -550,6 +562,9 @@ static int run_step(kernix_model* m, int i, int B, void* st)
         g.C = vi->c; g.Co = vo->c;
         g.kh = s->kh; g.kw = s->kw; g.sh = s->sh; g.sw = s->sw; g.dh = s->dh; g.dw = s->dw; g.pt = s->pt; g.pl = s->pl;
         g.groups = s->groups;
+        if (res != NULL)
+            return hip_ok(knx_hip_conv_t_res(&g, a->tensor, d->w, d->bias, s->act, s->alpha, res, y->tensor, st),
+                          "convolution + add");
         return hip_ok(knx_hip_conv_t(&g, a->tensor, d->w, d->bias, s->act, s->alpha, y->tensor, st), "convolution");
     }
     case KERNIX_OP_POOL: {
@@ -626,8 +641,7 @@ static int run_step(kernix_model* m, int i, int B, void* st)
         if (hip_ok(knx_hip_attention_core_ex(Q, ldq, K, ldk, V, ldv, s->tmp[5]->tensor, ctx, s->tmp[3]->tensor, B, H, Rq, S,
                                              s->dk, s->dv, 1.0f / sqrtf((float)s->dk), s->causal, st), "attention"))
             return -1;
-        return hip_ok(knx_hip_sgemm_nt_ep(vq->row, s->out, hv, ctx, hv, d->wo, hv, d->bo, -1, 0.0f, y->tensor, s->out, st),
-                      "attention output");
+        return fp32_linear(vq->row, s->out, hv, ctx, d->wo, d->bo, -1, 0.0f, res, y->tensor, st);
     }
     case KERNIX_OP_SELECT: {
         const int per = vi->r * vi->c;
@@ -653,6 +667,32 @@ static int run_step(kernix_model* m, int i, int B, void* st)
     }
 }
 
+/* The value the BINARY add after step i adds to step i's output, when the two can run as one pass (else −1): step i
+ * is a Linear, a convolution or an attention (whose last operation is the output projection), step i+1 adds its
+ * output and one other value of the same shape (no broadcast), nothing else reads step i's output, and the add's
+ * output storage is not one that step i reads (the fused epilogue writes it while step i still reads its inputs).
+ * The fused epilogue computes act(step i) and then adds the other value, the two fp32 roundings of the separate
+ * steps (reference include/kernix_model.h:1853-1860 then :877-906), so the result is the same bit for bit. */
+static int fusable_add(const kernix_model* m, int i)
+{
+    if (i + 1 >= m->n_steps) return -1;
+    const kernix_step* s = &m->steps[i];
+    const kernix_step* n = &m->steps[i + 1];
+    if (s->kind != KERNIX_OP_LINEAR && s->kind != KERNIX_OP_CONV && s->kind != KERNIX_OP_ATTENTION) return -1;
+    if (n->kind != KERNIX_OP_BINARY || n->bop != KERNIX_BIN_ADD || n->n_in != 2) return -1;
+    const int own = i + 1; /* value index of step i's output */
+    if ((n->inp[0] == own) == (n->inp[1] == own)) return -1;
+    const int other = n->inp[0] == own ? n->inp[1] : n->inp[0];
+    const kernix_val* vo = &m->vals[own];
+    const kernix_val* vr = &m->vals[other];
+    const kernix_val* vy = &m->vals[i + 2];
+    if (vo->last != i + 1 || m->out_v == own) return -1;
+    if (vr->r != vo->r || vr->c != vo->c || vy->r != vo->r || vy->c != vo->c) return -1;
+    for (int k = 0; k < s->n_in; k++)
+        if (m->vals[s->inp[k]].st == vy->st) return -1;
+    return other;
+}
+
 /* Enqueues every step for one chunk whose input starts at `in` (device). */
 static int run_chunk(kernix_model* m, const float* in, int B, void* st)
 {
@@ -661,8 +701,17 @@ static int run_chunk(kernix_model* m, const float* in, int B, void* st)
         m->views[v] = (float_tensor){ B * val->r, val->c, val->st < 0 ? (float*)in : m->st[val->st]->tensor };
     }
     if (B == 0) return 0;
-    for (int i = 0; i < m->n_steps; i++)
-        if (run_step(m, i, B, st) != 0) return -1;
+    const char* nf = getenv("KNX_NO_FUSE");
+    const int fuse = nf == NULL || *nf == '\0' || *nf == '0';
+    for (int i = 0; i < m->n_steps; i++) {
+        const int r = fuse ? fusable_add(m, i) : -1;
+        if (r >= 0) { /* step i and the add that follows it, in one pass */
+            if (run_step(m, i, B, st, &m->views[i + 2], m->views[r].tensor) != 0) return -1;
+            i++;
+        } else if (run_step(m, i, B, st, NULL, NULL) != 0) {
+            return -1;
+        }
+    }
     return 0;
 }
 

@@ -517,7 +517,11 @@ static int plan(kernix_model* m)
             st = m->vals[s->inp[0]].st;
         } else if (writes_in_place(s->kind)) {
             const int n_try = s->kind == KERNIX_OP_BINARY ? 2 : 1;
-            for (int k = 0; k < n_try && st == -2; k++) {
+            /* a binary op reuses the buffer of the previous step's output first: the runtime can then fold the op
+             * into that step's epilogue (the folded step must not write where it still reads its own inputs) */
+            const int first = n_try == 2 && s->inp[1] == i ? 1 : 0;
+            for (int t = 0; t < n_try && st == -2; t++) {
+                const int k = (first + t) % n_try;
                 const kernix_val* u = &m->vals[s->inp[k]];
                 if (u->st >= 0 && busy_until[u->st] <= i && (size_t)u->r * (size_t)u->c == need) st = u->st;
             }

@@ -29,6 +29,9 @@ SIGS = {
     "knx_hip_sgemm_nt_ep": ([I, I, I, P, I, P, I, P, I, F, P, I, P], I),
     "knx_hip_conv": ([ctypes.POINTER(ConvGeom), P, P, P, I, F, P, P], I),
     "knx_hip_conv_t": ([ctypes.POINTER(ConvGeom), P, P, P, I, F, P, P], I),
+    "knx_hip_conv_t_res": ([ctypes.POINTER(ConvGeom), P, P, P, I, F, P, P, P], I),
+    "knx_hip_sgemm_nt_ep_res": ([I, I, I, P, I, P, I, P, I, F, P, I, P, I, P], I),
+    "knx_hip_i8gemm_res": ([I, I, I, P, I, P, P, I, P, P, I, F, P, I, P, I, P], I),
     "knx_hip_layernorm": ([P, P, I, I, P, P, F, P], I),
     "knx_hip_softmax": ([P, P, I, I, P], I),
     "knx_hip_bias_act": ([P, P, I, I, P, I, F, P], I),

@@ -125,6 +125,30 @@ def test_i8gemm_skinny_variants(L, monkeypatch, variant, M, N, K):
     assert np.array_equal(host(Y), want_y)
 
 
+@pytest.mark.parametrize("variant", ["default", "k128w8t", "k128w8ta3e", "k128m", "ring64s4", "pipe64", "tile64", "pp",
+                                     "skinny"])
+@pytest.mark.parametrize("M,N,K,inplace", [(300, 300, 1024, False), (520, 700, 320, True), (2048, 2048, 2048, False),
+                                           (48, 520, 192, True)])
+def test_i8gemm_residual(L, monkeypatch, variant, M, N, K, inplace):
+    """Y = relu(epilogue) + R (the LINEAR + BINARY add fusion), bit-exact: the float32 add of R to the oracle's output;
+    R may be Y itself"""
+    monkeypatch.setenv("KNX_I8_KERNEL", variant)
+    rng = np.random.default_rng(M + 17 * N + K)
+    A = rng.integers(-127, 128, (M, K), dtype=np.int8)
+    W = rng.integers(-128, 128, (N, K), dtype=np.int8)
+    sa = rng.uniform(0.001, 0.01, M).astype(np.float32)
+    sw = rng.uniform(0.001, 0.01, N).astype(np.float32)
+    bias = rng.normal(0, 0.1, N).astype(np.float32)
+    R = rng.normal(0, 1, (M, N)).astype(np.float32)
+    want_y, _ = knx_ref.i8gemm(A, W, sa, sw, bias, act_id=0)
+    want = (want_y + R).astype(np.float32)
+    dA, dW, dsa, dsw, db, dR = dev(A), dev(W), dev(sa), dev(sw), dev(bias), dev(R)
+    Y = dR if inplace else torch.full((M, N), 7.0, dtype=torch.float32, device="cuda")
+    hipabi.check(L.knx_hip_i8gemm_res(M, N, K, ptr(dA), K, ptr(dsa), ptr(dW), K, ptr(dsw), ptr(db), 0, 0.0, ptr(dR), N,
+                                      ptr(Y), N, hipabi.stream()))
+    assert np.array_equal(host(Y), want)
+
+
 def test_i8gemm_accumulate_and_no_bias(L):
     rng = np.random.default_rng(3)
     M, N, K = 37, 70, 128
@@ -224,6 +248,25 @@ def test_sgemm_nt_variants(L, M, N, K, kernel, monkeypatch):
     _sgemm_nt_case(L, M, N, K, 1)
 
 
+@pytest.mark.parametrize("kernel", ["", "t128", "t64", "t256", "skinny", "general"])
+@pytest.mark.parametrize("M,N,K,inplace", [(1024, 768, 512, False), (520, 700, 96, True), (64, 256, 512, True),
+                                           (100, 77, 50, False)])
+def test_sgemm_nt_residual(L, M, N, K, inplace, kernel, monkeypatch):
+    """C = act(A·Wtᵀ + b) + R on every fp32 kernel (the LINEAR + BINARY add fusion); R may be C itself"""
+    monkeypatch.setenv("KNX_SGEMM_KERNEL", kernel)
+    rng = np.random.default_rng(M + 7 * N + 3 * K)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    W = (rng.standard_normal((K, N)) / np.sqrt(K)).astype(np.float32)
+    b = rng.normal(0, 0.1, N).astype(np.float32)
+    R = rng.standard_normal((M, N)).astype(np.float32)
+    want = knx_ref.act(knx_ref.dense64(A, W, b), 1).astype(np.float32) + R
+    dA, dWt, db, dR = dev(A), dev(np.ascontiguousarray(W.T)), dev(b), dev(R)
+    C = dR if inplace else torch.full((M, N), 7.0, dtype=torch.float32, device="cuda")
+    hipabi.check(L.knx_hip_sgemm_nt_ep_res(M, N, K, ptr(dA), K, ptr(dWt), K, ptr(db), 1, 0.0, ptr(dR), N, ptr(C), N,
+                                           hipabi.stream()))
+    assert rel_err(host(C), want) <= 1e-4
+
+
 def _sgemm_nt_case(L, M, N, K, act):
     rng = np.random.default_rng(M + 5 * N + 11 * K)
     A = rng.standard_normal((M, K)).astype(np.float32)
@@ -320,6 +363,29 @@ CONV_CASES = [
     (128, 16, 16, 64, 128, 3, 1, 1, 1, 1),
     (256, 16, 16, 128, 256, 3, 2, 1, 1, 1),
 ]
+
+
+@pytest.mark.parametrize("case", [(64, 32, 32, 64, 64, 3, 1, 1, 1, 1), (2, 8, 8, 3, 64, 3, 1, 1, 1, 1),
+                                  (128, 16, 16, 128, 128, 3, 1, 1, 2, 1), (2, 11, 13, 5, 7, 2, 3, 0, 1, 1)])
+def test_conv_residual(L, case):
+    """y = relu(conv(x) + b) + R on the pipelined and the general kernel (the CONV + BINARY add fusion)"""
+    B, H, W, C, Co, k, s, p, g, dil = case
+    rng = np.random.default_rng(sum(case) + 1)
+    Ho = (H + 2 * p - dil * (k - 1) - 1) // s + 1
+    Wo = (W + 2 * p - dil * (k - 1) - 1) // s + 1
+    x = rng.standard_normal((B * H * W, C)).astype(np.float32)
+    w = (rng.standard_normal((k * k * (C // g), Co)) / np.sqrt(k * k * C / g)).astype(np.float32)
+    b = rng.normal(0, 0.1, Co).astype(np.float32)
+    R = rng.standard_normal((B * Ho * Wo, Co)).astype(np.float32)
+    op = dict(cin=C, cout=Co, k=(k, k), s=(s, s), d=(dil, dil), p=(p, p, p, p), g=g, w=w, b=b)
+    want, _ = knx_ref._conv(x, B, H, W, op, act_id=0)
+    want = want.astype(np.float32) + R
+    geom = hipabi.ConvGeom(B, H, W, C, Ho, Wo, Co, k, k, s, s, dil, dil, p, p, g)
+    y = torch.empty((B * Ho * Wo, Co), dtype=torch.float32, device="cuda")
+    dx, dwt, db, dR = dev(x), dev(np.ascontiguousarray(w.T)), dev(b), dev(R)
+    hipabi.check(L.knx_hip_conv_t_res(ctypes.byref(geom), ptr(dx), ptr(dwt), ptr(db), 0, 0.0, ptr(dR), ptr(y),
+                                      hipabi.stream()))
+    assert rel_err(host(y), want) <= 1e-4
 
 
 CONV_TILES = ["256x256", "256x128", "128x128", "256x64", "128x64", "128x64w2"]

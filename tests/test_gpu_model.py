@@ -111,6 +111,34 @@ def test_transformer_full_size_subset(tmp_path):
     check(p, x, workspace_mb=0, subset=4, mode="i8", tol=1e-2)
 
 
+# ---------------------------------------------------------------- fused residual add
+FUSE_CASES = {
+    "cnn": lambda p: configs.cnn(p, batch=64, hw=16, widths=(64, 64, 128, 256)),  # conv2 + add: pipelined conv
+    "cnn_small": lambda p: configs.cnn(p, batch=8, hw=16, widths=(16, 16, 32, 64)),  # conv2 + add: general conv
+    "transformer": lambda p: configs.transformer(p, batch=8, seq=64, d=128, heads=4, ffn=256, layers=2),
+}
+
+
+@pytest.mark.parametrize("name", sorted(FUSE_CASES))
+@pytest.mark.parametrize("mode", ["ref", "i8"])
+def test_fused_residual_add_is_bit_identical(tmp_path, monkeypatch, name, mode):
+    """a step followed by the BINARY add of its output runs as one pass (the add in the step's epilogue); the result
+    is the same bits as the two separate steps (KNX_NO_FUSE=1), and both match the oracle"""
+    p = str(tmp_path / "m.knx")
+    x = FUSE_CASES[name](p)
+    outs = []
+    for no_fuse in ("0", "1"):
+        monkeypatch.setenv("KNX_NO_FUSE", no_fuse)
+        m = Model(p)
+        if mode == "i8":
+            m.set_int8_mode(INT8_I8)
+        outs.append(np.array(m(x)))
+        m.close()
+    assert np.array_equal(outs[0], outs[1]), name
+    want, _ = knx_ref.forward(knx_ref.parse(p), to_rows(Model(p), x), mode=mode)
+    assert rel_err(outs[0].reshape(len(want), -1), want) <= (1e-4 if mode == "ref" else 1e-2)
+
+
 # ---------------------------------------------------------------- runtime behaviour (reference test/model_test.c)
 def test_chunking_reuse_and_trim(tmp_path):
     """chunked == unchunked (reference test/model_test.c:296-360)"""
