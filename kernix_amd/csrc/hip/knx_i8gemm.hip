@@ -3,13 +3,16 @@
 //   knx_hip_quantize_rows  dynamic per-row int8 input (reference include/kernix_model.h:112-142)
 //   knx_hip_i8gemm         int32 accumulation on v_mfma_i32_32x32x32_i8 with the dequant · bias · act epilogue
 //                          fused (reference include/kernix_model.h:143-178 and the activation pass :1854-1856)
+//   knx_hip_i8gemm_res     the same followed by the add of another value (a LINEAR + BINARY add pair, :877-906)
 //   knx_hip_dequant        fp32 copy w = q·scale (reference include/kernix_model.h:91-95)
 //
 // GEMM kernels (one workgroup per output tile; both operands K-contiguous — A: M×K activations, W: N×K weights — so
 // no transposes anywhere; int32 accumulation on MFMA, the dequant · bias · act epilogue fused):
 //   i8gemm_k128    the default whenever its tiles fill the chip: 256×256 (or 128×128) tiles, 128-byte k-tiles moved
-//                  HBM → LDS by global_load_lds (two stages, 16-byte chunks XOR-swizzled), 32×32×32 i8 MFMAs
-//   i8gemm_pipe    64-byte k-tiles through a 4-stage LDS ring; any M, N (64×64 tiles for mid-size shapes)
+//                  HBM → LDS by global_load_lds (three A and two W stages at 256×256 for long K, 16-byte chunks
+//                  XOR-swizzled), 32×32×32 i8 MFMAs
+//   i8gemm_ring    fewer tiles than CUs at 128×128 (e.g. M = 256): 64×64 tiles on a deep ring of 128-byte k-tiles
+//   i8gemm_pipe    64-byte k-tiles through a 4-stage LDS ring (shapes below 64×64; forced variants)
 //   i8gemm_skinny  M ≤ 64: every W byte read once, K split across the waves of a workgroup
 //   i8gemm_tile    VGPR-staged kernel (K == 0, and forced variants for tests)
 #include <stdlib.h>
@@ -513,10 +516,12 @@ int launch_pipe(I8Args p, hipStream_t s, const char* name)
 // Why three A stages: the L2 → LDS path of a CU moves a 64-KB k-tile (256 A + 256 W rows) in about the time the
 // MFMAs need for it, so with two stages of both operands the loads of k-tile kt+2, which can only start once every
 // wave is done with stage kt, arrive just when they are needed and the barrier waits for them.  160 KB of LDS holds
-// three 32-KB A stages and two 32-KB W stages: the loads of A k-tile kt+3 are issued together with those of W k-tile
-// kt+2 and have two k-tiles to arrive, and the W loads, issued first, only half the bytes within one k-tile.
-// Vector-memory loads retire in issue order, so the wait for k-tile kt+1 leaves exactly this wave's A loads of
-// k-tile kt+2 outstanding (SA of them).
+// three 32-KB A stages and two 32-KB W stages.  Without EARLY the loads of A k-tile kt+3 are issued after the barrier
+// of k-tile kt together with those of W k-tile kt+2 (W first); with EARLY (the default for long K) the A loads of
+// k-tile kt+2 go out during k-steps 0..2 of k-tile kt, into the stage k-tile kt−1 left, and only the W loads follow
+// the barrier: the A loads have more than a k-tile to arrive, only 32 KB must land within one k-tile, and the loads
+// are not issued as one burst.  Vector-memory loads retire in issue order, so the wait for k-tile kt+1 leaves exactly
+// this wave's SA younger A loads outstanding in both schemes.
 //
 // LDS layout: a row holds 8 chunks of 16 bytes, global chunk c of row r at position c ^ swz8(r).  The 16 rows that
 // one quarter-wave of a ds_read_b128 touches (same chunk, consecutive rows) then fall on 16 distinct 16-byte bank
