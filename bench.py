@@ -351,6 +351,10 @@ def main():
         fwarm = max(3, args.warmup // 10)
         fw["int8_mlp_784_512_256_10_b64"] = forward_bench(
             "mlp", lambda p: configs.int8_mlp(p, batch=64), configs.mlp_flops(64, (784, 512, 256, 10)), st, fwarm)
+        # batch 1: the reference's int8 latency path (int8 arithmetic at ≤ 2 rows), quantize fused into the GEMM
+        fw["int8_mlp_784_512_256_10_b1"] = forward_bench(
+            "mlp", lambda p: configs.int8_mlp(p, batch=1), configs.mlp_flops(1, (784, 512, 256, 10)), st, fwarm,
+            i8_ops=configs.mlp_flops(1, (784, 512, 256, 10)))
         fw["int8_mlp_784_512_256_10_b64_i8"] = forward_bench(
             "mlp", lambda p: configs.int8_mlp(p, batch=64), configs.mlp_flops(64, (784, 512, 256, 10)), st, fwarm,
             mode="i8", i8_ops=configs.mlp_flops(64, (784, 512, 256, 10)))

@@ -16,6 +16,7 @@
 //   i8gemm_skinny  M ≤ 64: every W byte read once, K split across the waves of a workgroup
 //   i8gemm_tile    VGPR-staged kernel (K == 0, and forced variants for tests)
 #include <stdlib.h>
+#include <string.h>
 
 #include <string>
 #include <type_traits>
@@ -1128,6 +1129,134 @@ __global__ void __launch_bounds__(KS * 64) i8gemm_skinny(I8Args p)
     }
 }
 
+// ---------------------------------------------------------------- fused quantize + skinny GEMM (≤ 4 rows)
+// kernix_qmatmul at the few rows the reference runs int8 arithmetic on (≤ 2, its batch-1 latency path) as one kernel
+// instead of the row quantizer followed by the skinny GEMM.  Every workgroup (16 output channels) first finds the
+// absolute maxima of its ≤ 4 fp32 input rows (each row split over the waves, the partial maxima combined through LDS:
+// a maximum is exact in any order), then runs the skinny K loop with each lane quantizing its 16 inputs of a k-step
+// on the fly with the operations of knx_hip_quantize_rows (s = m/127 or 1 for an all-zero row, inv = 1/s, rint,
+// clamp ±127; a row holding NaN or ±inf gets s = NaN and q = 0, so its whole output row is NaN).  The int32 sums and
+// outputs are therefore bit-exact against the two-kernel path.  The fp32 rows are read once per workgroup (16 KB
+// per row at K = 4096, from L2), which is why the fused form stops at 4 rows.
+template <int KS, int KT>
+__global__ void __launch_bounds__(KS * 64) i8gemm_skinny_q(I8Args p, const float* __restrict__ X, int ldx, int kx)
+{
+    constexpr int MR = 4;
+    __shared__ int part[KS][16][17];
+    __shared__ float pmax[MR][KS];
+    __shared__ int pbad[MR][KS];
+    __shared__ float row_s[MR], row_inv[MR];
+    __shared__ int row_bad[MR];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int M = p.M;
+    // row maxima: row m, wave w covers elements [w·seg, (w+1)·seg)
+    const int seg = (kx + KS - 1) / KS;
+    for (int m = 0; m < M; ++m) {
+        const float* xr = X + (size_t)m * ldx;
+        float mx = 0.0f;
+        int bad = 0;
+        const int j1 = min(kx, (wave + 1) * seg);
+        for (int j = wave * seg + lane; j < j1; j += 64) {
+            const float a = fabsf(xr[j]);
+            if (!(a <= 3.402823466e38f)) bad = 1;  // NaN or ±inf
+            else mx = a > mx ? a : mx;
+        }
+        mx = knx_wave_max(mx);
+        bad = __any(bad);
+        if (lane == 0) {
+            pmax[m][wave] = mx;
+            pbad[m][wave] = bad;
+        }
+    }
+    __syncthreads();
+    if ((int)threadIdx.x < M) {
+        const int m = threadIdx.x;
+        float mx = 0.0f;
+        int bad = 0;
+        for (int w = 0; w < KS; ++w) {
+            mx = pmax[m][w] > mx ? pmax[m][w] : mx;
+            bad |= pbad[m][w];
+        }
+        const float s = mx > 0.0f ? __fdiv_rn(mx, 127.0f) : 1.0f;
+        row_s[m] = bad ? __int_as_float(0x7fc00000) : s;
+        row_inv[m] = __fdiv_rn(1.0f, s);
+        row_bad[m] = bad;
+    }
+    __syncthreads();
+
+    // K loop of the skinny kernel (one block of 16 rows, rows ≥ M are zero); lane (r, c) holds row r, bytes
+    // [64·kk + 16c, +16) of k-step kk
+    const int r = lane & 15, c = lane >> 4;
+    const int n0 = blockIdx.x * 16;
+    const int gn = min(n0 + r, p.N - 1);
+    const int8_t* wrow = p.W + (size_t)gn * p.ldw + c * 16;
+    const bool rok = r < M && !row_bad[r < M ? r : 0];
+    const float* xrow = X + (size_t)(r < M ? r : 0) * ldx;
+    const float inv = r < M ? row_inv[r] : 0.0f;
+    const bool xvec = (ldx & 3) == 0 && ((uintptr_t)X & 15) == 0;
+    // the 16 inputs of k-step kk of this lane, quantized and packed four per int
+    auto quant16 = [&](int kk) -> v4i {
+        const int j0 = kk * 64 + c * 16;
+        float v[16];
+        if (xvec && j0 + 16 <= kx) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float4 f = *reinterpret_cast<const float4*>(xrow + j0 + 4 * u);
+                v[4 * u] = f.x; v[4 * u + 1] = f.y; v[4 * u + 2] = f.z; v[4 * u + 3] = f.w;
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) v[e] = j0 + e < kx ? xrow[j0 + e] : 0.0f;
+        }
+        v4i out;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            int packed = 0;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const float q = rintf(v[4 * u + b] * inv);
+                const int qi = (int)(q > 127.0f ? 127.0f : q < -127.0f ? -127.0f : q);
+                packed |= (qi & 0xff) << (8 * b);
+            }
+            out[u] = packed;
+        }
+        return out;
+    };
+    v4i acc = v4i{0, 0, 0, 0};
+    const v4i z = v4i{0, 0, 0, 0};
+    const int nk = p.K / 64;
+    for (int k0 = wave; k0 < nk; k0 += KS * KT) {
+        v4i wf[KT], af[KT];
+#pragma unroll
+        for (int j = 0; j < KT; ++j) {
+            const int kk = k0 + j * KS;
+            wf[j] = kk < nk ? *(const v4i*)(wrow + (size_t)kk * 64) : z;
+            af[j] = (kk < nk && rok) ? quant16(kk) : z;
+        }
+#pragma unroll
+        for (int j = 0; j < KT; ++j) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[j], wf[j], acc, 0, 0, 0);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) part[wave][4 * c + e][r] = acc[e];
+    __syncthreads();
+    // rows < M × 16 columns: the exact int32 sum of the waves' partial tiles, then the epilogue with the row scale
+    for (int i = threadIdx.x; i < 16 * 16; i += KS * 64) {
+        const int row = i >> 4, col = i & 15, n = n0 + col;
+        if (row >= M || n >= p.N) continue;
+        int a = 0;
+#pragma unroll
+        for (int w = 0; w < KS; ++w) a += part[w][row][col];
+        float v = (float)a * row_s[row];  // ((float)acc · sx) · scale + bias, each step rounded
+        v = v * p.sw[n];
+        if (p.bias) v = v + p.bias[n];
+        float* y = p.Y + (size_t)row * p.ldy + n;
+        if (p.accumulate) v = *y + v;
+        v = knx_act(v, p.act, p.alpha);
+        if (p.R) v = v + p.R[(size_t)row * p.ldr + n];
+        *y = v;
+    }
+}
+
 template <int MB>
 int launch_skinny(I8Args p, hipStream_t s, const char* name)
 {
@@ -1394,6 +1523,33 @@ extern "C" int knx_hip_i8gemm_res(int M, int N, int K, const int8_t* A, int lda,
     KNX_REQUIRE(Y != nullptr && R != nullptr && ldr >= N, name);
     I8Args p{M, N, K, A, lda, sa, W, ldw, sw, bias, act, alpha, 0, Y, ldy, nullptr, 0, 0, 0, R, ldr};
     return i8gemm_run(p, knx::as_stream(stream), name);
+}
+
+extern "C" int knx_hip_qlinear(const float* x, int ldx, int rows, int k, int kp, int8_t* xq, float* sx, const int8_t* W,
+                               int ldw, int n, const float* sw, const float* bias, int act, float alpha, int accumulate,
+                               const float* R, int ldr, float* Y, int ldy, void* stream)
+{
+    const char* name = "knx_hip_qlinear";
+    KNX_ENTRY(name);
+    KNX_REQUIRE(rows >= 0 && n >= 0 && k >= 1 && kp >= k && kp % 64 == 0 && kp <= 131072 && ldx >= k, name);
+    KNX_REQUIRE(ldw >= kp && ldw % 16 == 0 && act >= -1 && act <= 15, name);
+    if (rows == 0 || n == 0) return KNX_OK;
+    KNX_REQUIRE(x != nullptr && W != nullptr && sw != nullptr && Y != nullptr && ldy >= n, name);
+    KNX_REQUIRE(((uintptr_t)W & 15) == 0 && (R == nullptr || ldr >= n) && !(R != nullptr && accumulate), name);
+    hipStream_t s = knx::as_stream(stream);
+    // KNX_QLINEAR=split: always the quantizer followed by the GEMM (tests)
+    const char* mode = getenv("KNX_QLINEAR");
+    const bool split = mode != nullptr && strcmp(mode, "split") == 0;
+    if (rows <= 4 && !split) {
+        I8Args p{rows, n, kp, nullptr, 0, nullptr, W, ldw, sw, bias, act, alpha, accumulate, Y, ldy, nullptr, 0, 0, 0, R, ldr};
+        hipLaunchKernelGGL((i8gemm_skinny_q<8, 4>), dim3((unsigned)((n + 15) / 16)), dim3(8 * 64), 0, s, p, x, ldx, k);
+        return knx::check_launch(name);
+    }
+    KNX_REQUIRE(xq != nullptr && sx != nullptr, name);
+    int rc = knx_hip_quantize_rows(x, ldx, rows, k, kp, xq, kp, sx, stream);
+    if (rc != KNX_OK) return rc;
+    if (R != nullptr) return knx_hip_i8gemm_res(rows, n, kp, xq, kp, sx, W, ldw, sw, bias, act, alpha, R, ldr, Y, ldy, stream);
+    return knx_hip_i8gemm(rows, n, kp, xq, kp, sx, W, ldw, sw, bias, act, alpha, accumulate, Y, ldy, nullptr, 0, stream);
 }
 
 extern "C" int knx_hip_dequant_t(const int8_t* q, int ldq, const float* scale, int K, int N, float* dst, void* stream)

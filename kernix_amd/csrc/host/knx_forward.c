@@ -443,12 +443,8 @@ static int run_qlinear(const kernix_model* m, const kernix_qweight* q, const int
     const int use_i8 = m->int8_mode == KERNIX_INT8_I8 || rows <= KERNIX_INT8_MAX_ROWS;
     if (use_i8) {
         if (rows > xq_rows || xq == NULL) { KNX_LOG("KERNIX: int8 scratch too small (%d > %d rows)\n", rows, xq_rows); return -1; }
-        if (hip_ok(knx_hip_quantize_rows(x, q->k, rows, q->k, q->kp, xq, q->kp, sx, st), "int8 input quantization")) return -1;
-        if (res != NULL)
-            return hip_ok(knx_hip_i8gemm_res(rows, q->n, q->kp, xq, q->kp, sx, dq, q->kp, dscale, bias, act, alpha, res,
-                                             q->n, y, q->n, st), "int8 GEMM + add");
-        return hip_ok(knx_hip_i8gemm(rows, q->n, q->kp, xq, q->kp, sx, dq, q->kp, dscale, bias, act, alpha, accumulate, y,
-                                     q->n, NULL, 0, st), "int8 GEMM");
+        return hip_ok(knx_hip_qlinear(x, q->k, rows, q->k, q->kp, xq, sx, dq, q->kp, q->n, dscale, bias, act, alpha,
+                                      accumulate, res, q->n, y, q->n, st), res ? "int8 GEMM + add" : "int8 GEMM");
     }
     if (deq == NULL) { KNX_LOG("KERNIX: missing fp32 copy of an int8 weight\n"); return -1; }
     if (accumulate) return -1; /* the recurrence adds through a separate buffer on this path */
@@ -848,8 +844,8 @@ int kernix_qmatmul(const float* x, int rows, const kernix_qweight* w, const floa
         knx_hip_memcpy_h2d(dsc, w->scale, np * 4, st) || (bias && knx_hip_memcpy_h2d(db, bias, n * 4, st)) ||
         (accumulate && knx_hip_memcpy_h2d(dy, y, R * n * 4, st)))
         goto done;
-    if (knx_hip_quantize_rows(dx, (int)k, rows, (int)k, (int)kp, dxq, (int)kp, dsx, st) ||
-        knx_hip_i8gemm(rows, (int)n, (int)kp, dxq, (int)kp, dsx, dq, (int)kp, dsc, db, -1, 0.0f, accumulate, dy, (int)n, NULL, 0, st) ||
+    if (knx_hip_qlinear(dx, (int)k, rows, (int)k, (int)kp, dxq, dsx, dq, (int)kp, (int)n, dsc, db, -1, 0.0f, accumulate,
+                        NULL, 0, dy, (int)n, st) ||
         knx_hip_memcpy_d2h(y, dy, R * n * 4, st) || knx_hip_stream_sync(st))
         goto done;
     rc = 0;

@@ -149,6 +149,39 @@ def test_i8gemm_residual(L, monkeypatch, variant, M, N, K, inplace):
     assert np.array_equal(host(Y), want)
 
 
+@pytest.mark.parametrize("rows", [1, 2, 3, 4, 5, 9])
+@pytest.mark.parametrize("k,n", [(784, 512), (4096, 4096), (64, 10), (200, 33)])
+@pytest.mark.parametrize("path", ["fused", "split"])
+def test_qlinear(L, monkeypatch, rows, k, n, path):
+    """knx_hip_qlinear (kernix_qmatmul + act) against the oracle's kernix_qmatmul, bit-exact: one-kernel quantize-on-
+    the-fly path at ≤ 4 rows, quantizer + GEMM above and when forced; a zero row and (from 3 rows) a row with inf"""
+    if path == "split":
+        monkeypatch.setenv("KNX_QLINEAR", "split")
+    rng = np.random.default_rng(rows * 131 + k + n)
+    kp = (k + 63) // 64 * 64
+    x = rng.normal(0, 1, (rows, k)).astype(np.float32)
+    x[0, :] = 0.0
+    if rows >= 3:
+        x[2, k // 2] = np.inf
+    q = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    scale = rng.uniform(0.001, 0.01, n).astype(np.float32)
+    bias = rng.normal(0, 0.1, n).astype(np.float32)
+    want = knx_ref.qmatmul(x, q.T.copy(), scale, bias)  # no activation: the inf row must come out all NaN
+    qp = np.zeros((n, kp), np.int8)
+    qp[:, :k] = q
+    dx, dq, ds, db = dev(x), dev(qp), dev(scale), dev(bias)
+    xq = torch.empty((rows, kp), dtype=torch.int8, device="cuda")
+    sx = torch.empty(rows, dtype=torch.float32, device="cuda")
+    Y = torch.full((rows, n), 7.0, dtype=torch.float32, device="cuda")
+    hipabi.check(L.knx_hip_qlinear(ptr(dx), k, rows, k, kp, ptr(xq), ptr(sx), ptr(dq), kp, n, ptr(ds), ptr(db), -1,
+                                   0.0, 0, None, 0, ptr(Y), n, hipabi.stream()))
+    got = host(Y)
+    if rows >= 3:
+        assert np.isnan(got[2]).all()
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    assert np.array_equal(got[~np.isnan(got)], want[~np.isnan(want)])
+
+
 def test_i8gemm_accumulate_and_no_bias(L):
     rng = np.random.default_rng(3)
     M, N, K = 37, 70, 128
