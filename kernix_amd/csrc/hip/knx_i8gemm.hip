@@ -246,50 +246,66 @@ __device__ __forceinline__ void store_rows(const I8Args& p, const int* stg, cons
                                            int nlo, int rq, int rpi, int srow, int cq, int nb, const float* swv,
                                            const float* bv, bool vec = true)
 {
-    // The residual rows of this round are loaded before any store: inside the store loop each load would wait for
-    // the previous row's store (R and Y may alias), one memory round trip per row.  Loading them first is right even
-    // when R is Y: every element is read before its own store, and no other element's store touches it.
-    typedef float v4r_t __attribute__((ext_vector_type(4)));
-    constexpr int MAXJ = 8;  // rpi ≥ 2
-    v4r_t rres[MAXJ];
-    if (p.R) {
+    typedef float v4f_t __attribute__((ext_vector_type(4)));
+    if (ACT >= -1 && p.R) {
+        // Residual after no activation or ReLU: the round's residual rows are loaded before any store (R and Y may
+        // alias, and a load after a store waits for it: one memory round trip per row).  Loading first is right when
+        // R is Y, since each element is read before its own store and no other store touches it.  Unrolled, so the
+        // loads sit in registers; the per-row code is a few instructions.
+        constexpr int MAXJ = 8;  // rpi ≥ 2
+        v4f_t rres[MAXJ];
         const bool rvec = nb >= nlo && (nb & 3) == 0 && (p.ldr & 3) == 0 && ((uintptr_t)p.R & 15) == 0;
 #pragma unroll
         for (int j = 0; j < MAXJ; ++j) {
             const int rr = rq + j * rpi, m = m0 + mt0 + rr;
-            rres[j] = v4r_t{0.0f, 0.0f, 0.0f, 0.0f};
+            rres[j] = v4f_t{0.0f, 0.0f, 0.0f, 0.0f};
             if (rr >= 16 || m < mlo || m >= p.M) continue;
             const float* rp = p.R + (size_t)m * p.ldr + nb;
             if (rvec) {
-                rres[j] = *reinterpret_cast<const v4r_t*>(rp);
+                rres[j] = *reinterpret_cast<const v4f_t*>(rp);
             } else {
 #pragma unroll
                 for (int q = 0; q < 4; ++q)
                     if (nb + q >= nlo && nb + q < p.N) rres[j][q] = rp[q];
             }
         }
-    }
 #pragma unroll
-    for (int j = 0; j < MAXJ; ++j) {
-        const int rr = rq + j * rpi;
-        if (rr >= 16) break;
+        for (int j = 0; j < MAXJ; ++j) {
+            const int rr = rq + j * rpi;
+            if (rr >= 16) break;
+            const int mt = mt0 + rr, m = m0 + mt;
+            if (m < mlo || m >= p.M) continue;
+            const v4i a = *reinterpret_cast<const v4i*>(&stg[rr * srow + cq]);
+            const float sx = row_scale[mt];
+            v4f_t r;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                float v = (float)a[q] * sx;  // ((float)acc · sx) · scale + bias, each step rounded
+                v = v * swv[q];
+                if (p.bias) v = v + bv[q];
+                r[q] = (ACT == 0 ? (v >= 0.0f ? v : 0.0f) : v) + rres[j][q];
+            }
+            __builtin_nontemporal_store(r, reinterpret_cast<v4f_t*>(p.Y + (size_t)m * p.ldy + nb));
+        }
+        return;
+    }
+    // one row per iteration, a rolled loop (the general path's activation switch appears once)
+    for (int rr = rq; rr < 16; rr += rpi) {
         const int mt = mt0 + rr, m = m0 + mt;
         if (m < mlo || m >= p.M) continue;
         const v4i a = *reinterpret_cast<const v4i*>(&stg[rr * srow + cq]);
         if (ACT >= -1) {
             const float sx = row_scale[mt];
-            float r[4];
+            v4f_t r;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 float v = (float)a[q] * sx;  // ((float)acc · sx) · scale + bias, each step rounded
                 v = v * swv[q];
                 if (p.bias) v = v + bv[q];   // no bias: no addition (x + 0 would turn −0 into +0)
                 r[q] = ACT == 0 ? (v >= 0.0f ? v : 0.0f) : v;
-                if (p.R) r[q] = r[q] + rres[j][q];  // residual after the activation
             }
             // streaming store: the output is written once and never re-read by this kernel
-            typedef float v4f_t __attribute__((ext_vector_type(4)));
-            __builtin_nontemporal_store(v4f_t{r[0], r[1], r[2], r[3]}, reinterpret_cast<v4f_t*>(p.Y + (size_t)m * p.ldy + nb));
+            __builtin_nontemporal_store(r, reinterpret_cast<v4f_t*>(p.Y + (size_t)m * p.ldy + nb));
         } else if (vec) {
             if (p.acc) *reinterpret_cast<v4i*>(p.acc + (size_t)m * p.ldacc + nb) = a;
             if (p.Y) {
@@ -304,7 +320,7 @@ __device__ __forceinline__ void store_rows(const I8Args& p, const int* stg, cons
                     if (p.bias) v = v + bv[q];
                     if (p.accumulate) v = (&o.x)[q] + v;
                     r[q] = knx_act(v, p.act, p.alpha);
-                    if (p.R) r[q] = r[q] + rres[j][q];
+                    if (p.R) r[q] = r[q] + p.R[(size_t)m * p.ldr + nb + q];  // residual after the activation
                 }
                 *reinterpret_cast<float4*>(y) = make_float4(r[0], r[1], r[2], r[3]);
             }

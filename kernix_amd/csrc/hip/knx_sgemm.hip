@@ -429,13 +429,17 @@ __global__ void __launch_bounds__(WM * WN * 64) sgemm_k32(SgArgs p)
     // then every lane writes 4 consecutive columns of a row with one 16-byte store.
     constexpr int SROW = TN + 4, LPR = TN / 4, RPI = 64 / LPR;
     float* stg = reinterpret_cast<float*>(lds) + wave * 16 * SROW;
-    const int cq = (lane % LPR) * 4, rq = lane / LPR;
+    // lanes from LPR·RPI on (when LPR does not divide 64) would repeat rows of other lanes: they store nothing, so with
+    // R aliasing C no lane reads a residual element that another lane has already overwritten
+    const int cq = (lane % LPR) * 4, rq = lane < LPR * RPI ? lane / LPR : 16;
     const int nb = n0 + wn * TN + cq;
     float bv[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) bv[q] = bias ? bias[nb + q] : 0.0f;
     const bool vec = nb >= nlo && (p.ldc & 3) == 0 && ((uintptr_t)C & 15) == 0;
     const bool rvec = nb >= nlo && (nb & 3) == 0 && (p.ldr & 3) == 0 && ((uintptr_t)R & 15) == 0;
+    const bool relu = p.act == 0;
+    const bool fast_res = R && p.alpha == 1.0f && !p.causal && (p.act == -1 || relu);
     static_assert(16 % RPI == 0, "rows per store instruction");
     KNX_WAIT_LDS();
     knx_barrier_nofence();  // nobody reads the operand stages any more
@@ -450,14 +454,17 @@ __global__ void __launch_bounds__(WM * WN * 64) sgemm_k32(SgArgs p)
                     stg[(8 * ((e >> 2) - 2 * h) + 4 * g + (e & 3)) * SROW + fj * 32 + rl] = acc[fi][fj][e];
             KNX_WAIT_LDS();
             asm volatile("" ::: "memory");
-            // the residual rows of this round, loaded before any store (R and C may alias: a load after a store would
-            // wait for it, one memory round trip per row; every element is still read before its own store)
-            constexpr int NJ = (16 + RPI - 1) / RPI;
-            float4 rres[NJ];
-            if (R) {
+            const int mt0 = m0 + wm * TM + fi * 32 + 16 * h;
+            if (fast_res) {
+                // Residual with no activation or ReLU: the round's residual rows are loaded before any store (R and C
+                // may alias, and a load after a store waits for it: one memory round trip per row).  Loading first is
+                // right when R is C, since each element is read before its own store and no other store touches it.
+                // Unrolled, so the loads sit in registers; the per-row code is a few instructions.
+                constexpr int NJ = (16 + RPI - 1) / RPI;
+                float4 rres[NJ];
 #pragma unroll
                 for (int j = 0; j < NJ; ++j) {
-                    const int rr = rq + j * RPI, m = m0 + wm * TM + fi * 32 + 16 * h + rr;
+                    const int rr = rq + j * RPI, m = mt0 + rr;
                     rres[j] = make_float4(0.f, 0.f, 0.f, 0.f);
                     if (rr >= 16 || m < mlo) continue;
                     const float* rp = R + (size_t)m * p.ldr + nb;
@@ -469,34 +476,58 @@ __global__ void __launch_bounds__(WM * WN * 64) sgemm_k32(SgArgs p)
                             if (nb + q >= nlo) (&rres[j].x)[q] = rp[q];
                     }
                 }
-            }
 #pragma unroll
-            for (int j = 0; j < NJ; ++j) {
-                const int rr = rq + j * RPI;  // lanes past 64 / LPR · LPR start at row RPI and stop at row 15
-                if (rr >= 16) break;
-                const int m = m0 + wm * TM + fi * 32 + 16 * h + rr;
-                if (m < mlo) continue;
-                const float4 a = *reinterpret_cast<const float4*>(&stg[rr * SROW + cq]);
-                float r[4];
+                for (int j = 0; j < NJ; ++j) {
+                    const int rr = rq + j * RPI;  // idle lanes have rq = 16
+                    if (rr >= 16) break;
+                    const int m = mt0 + rr;
+                    if (m < mlo) continue;
+                    const float4 a = *reinterpret_cast<const float4*>(&stg[rr * SROW + cq]);
+                    float r[4];
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    float v = (&a.x)[q];
-                    if (p.alpha != 1.0f) v = p.alpha * v;
-                    if (bias) v = v + bv[q];
-                    if (p.causal && nb + q > m) v = -INFINITY;
-                    r[q] = knx_act(v, p.act, p.act_alpha);
+                    for (int q = 0; q < 4; ++q) {
+                        float v = (&a.x)[q];
+                        if (bias) v = v + bv[q];
+                        if (relu) v = v >= 0.0f ? v : 0.0f;  // the ReLU of knx_act (NaN → 0)
+                        r[q] = v + (&rres[j].x)[q];
+                    }
+                    float* y = C + (size_t)m * p.ldc + nb;
+                    if (vec) {
+                        *reinterpret_cast<float4*>(y) = make_float4(r[0], r[1], r[2], r[3]);
+                    } else {
+#pragma unroll
+                        for (int q = 0; q < 4; ++q)
+                            if (nb + q >= nlo) y[q] = r[q];
+                    }
                 }
-                if (R) {  // residual after the activation: the fused form of a following elementwise add
+            } else {
+                // General epilogue: one row per iteration, a rolled loop (the activation switch appears once).
+                for (int rr = rq; rr < 16; rr += RPI) {
+                    const int m = mt0 + rr;
+                    if (m < mlo) continue;
+                    const float4 a = *reinterpret_cast<const float4*>(&stg[rr * SROW + cq]);
+                    float r[4];
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) r[q] = r[q] + (&rres[j].x)[q];
-                }
-                float* y = C + (size_t)m * p.ldc + nb;
-                if (vec) {
-                    *reinterpret_cast<float4*>(y) = make_float4(r[0], r[1], r[2], r[3]);
-                } else {
+                    for (int q = 0; q < 4; ++q) {
+                        float v = (&a.x)[q];
+                        if (p.alpha != 1.0f) v = p.alpha * v;
+                        if (bias) v = v + bv[q];
+                        if (p.causal && nb + q > m) v = -INFINITY;
+                        r[q] = knx_act(v, p.act, p.act_alpha);
+                    }
+                    float* y = C + (size_t)m * p.ldc + nb;
+                    if (R) {  // residual after the activation; each element is read before its own store
 #pragma unroll
-                    for (int q = 0; q < 4; ++q)
-                        if (nb + q >= nlo) y[q] = r[q];
+                        for (int q = 0; q < 4; ++q)
+                            if (nb + q >= nlo) r[q] = r[q] + R[(size_t)m * p.ldr + nb + q];
+                    }
+                    if (vec) {
+                        *reinterpret_cast<float4*>(y) = make_float4(r[0], r[1], r[2], r[3]);
+                    } else {
+#pragma unroll
+                        for (int q = 0; q < 4; ++q)
+                            if (nb + q >= nlo) y[q] = r[q];
+                    }
                 }
             }
             asm volatile("" ::: "memory");

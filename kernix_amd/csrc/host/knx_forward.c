@@ -675,6 +675,9 @@ static int fusable_add(const kernix_model* m, int i)
     const kernix_step* s = &m->steps[i];
     const kernix_step* n = &m->steps[i + 1];
     if (s->kind != KERNIX_OP_LINEAR && s->kind != KERNIX_OP_CONV && s->kind != KERNIX_OP_ATTENTION) return -1;
+    /* the GEMM epilogues load the residual ahead of their stores only after no activation or ReLU (the producers of
+     * residual adds in practice); after another activation the add stays a step of its own */
+    if (s->kind != KERNIX_OP_ATTENTION && s->act != KERNIX_ACT_NONE && s->act != KERNIX_ACT_RELU) return -1;
     if (n->kind != KERNIX_OP_BINARY || n->bop != KERNIX_BIN_ADD || n->n_in != 2) return -1;
     const int own = i + 1; /* value index of step i's output */
     if ((n->inp[0] == own) == (n->inp[1] == own)) return -1;
