@@ -661,8 +661,9 @@ int dispatch_nt(SgArgs p, int batch, hipStream_t s, const char* name)
     if (t64x64 * 4 < cus && skinny_ok(p, batch)) return launch_skinny(p, s, name);
     const long t64 = (long)((p.M + 127) / 128) * ((p.N + 63) / 64) * batch;
     // short K: 128×64 tiles, at least two per CU, so that several workgroups share a CU and one's prologue and
-    // epilogue overlap another's multiplies (Transformer layers at 8192 rows: 8192×512×512 41 µs against 48.5 for
-    // 128×128, 8192×2048×512 151 against 159 for 256×256, 8192×512×2048 134 against 143)
+    // epilogue overlap another's multiplies (Transformer layers at 8192 rows, one box after a 2 s warm-up:
+    // 8192×1536×512 105 µs against 113 for 128×128, 8192×512×512 41 against 47, 8192×2048×512 + GELU 145 against
+    // 153, 8192×512×2048 131 against 137; 2×2 waves of 64×32 time the same as these 4×1 waves of 32×64)
     if (p.K <= 2048 && t64 >= 2 * cus && k32_ok(p, 128, 64)) return launch_k32<128, 64, 4, 1>(p, batch, s, name);
     if (t256 >= cus && k32_ok(p, 256, 256)) return launch_k32<256, 256, 4, 2>(p, batch, s, name);
     if (t128 >= cus && k32_ok(p, 128, 128)) return launch_k32<128, 128, 2, 2>(p, batch, s, name);
