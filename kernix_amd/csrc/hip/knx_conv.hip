@@ -5,6 +5,10 @@
 // A[m][k] = x[b, oy·sh − pt + ky·dh, ox·sw − pl + kx·dw, ci] (0 outside the image).  Each workgroup gathers its
 // BM×16 slice of A directly from the input into LDS, so the column matrix never exists in HBM; bias and activation
 // are applied in the epilogue.  Groups run as grid.y (each group is an independent GEMM over its channel slice).
+#include <algorithm>
+#include <cstdlib>
+#include <cstring>
+
 #include "knx_common.hpp"
 
 typedef float v16f __attribute__((ext_vector_type(16)));
@@ -233,6 +237,179 @@ __global__ void __launch_bounds__(WM * WN * 64) conv_tile(ConvArgs p)
     }
 }
 
+// ---------------------------------------------------------------- convolution with few inputs per output
+// A first layer such as 3×3 over RGB (K = 27) is a poor fit for the k-tiled kernels: K pads to whole k-tiles of
+// LDS-staged operands while the output, Co fp32 channels per pixel, is what costs.  Here each wave owns 32 output
+// pixels at a time and multiplies straight from registers on v_mfma_f32_32x32x2f32: lane l gathers, for pixel
+// l & 31, the inputs k = 2p + (l >> 5) of every k pair p (the A fragments, K ≤ 32 so at most 16 pairs), the weights
+// sit in registers as the B fragments for the whole kernel (Co = 32·NB, NB ≤ 4), and every accumulator register is
+// stored directly (two 128-byte row segments per instruction).  Epilogue: bias, then ReLU or nothing, then the
+// residual, each an fp32 rounding as in the other convolution kernels.
+constexpr int SMALL_K = 32;
+
+struct SmallConvArgs {
+    const float* x;
+    const float* w;
+    const float* bias;
+    const float* R;  // residual added after the activation (same layout as y), or null
+    float* y;
+    int H, W, C, Ho, Wo, Co, sh, sw, pt, pl;
+    int relu;
+    int M;                          // B·Ho·Wo
+    int K;                          // kh·kw·C ≤ 32
+    int wsc, wsk;                   // weight element (co, k) at w[co·wsc + k·wsk]
+    int dyx[SMALL_K];               // per k: input row and column offset of its tap, ky·dh << 16 | kx·dw
+    int off[SMALL_K];               // per k: element offset from the pixel's top-left input element
+};
+
+__device__ float conv_zero_word = 0.0f;  // what the gather reads for padding: never written
+
+template <int NB, bool RES>
+__global__ void __launch_bounds__(256) conv_small(SmallConvArgs a)
+{
+    constexpr int KP = SMALL_K / 2, CO = 32 * NB;
+    __shared__ float wl[SMALL_K * CO];  // the weights, [k][co]: staged once per workgroup with coalesced loads
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int rl = lane & 31, g = lane >> 5;
+    for (int i = threadIdx.x; i < a.K * CO; i += 256) {
+        // i walks the weight in memory order: Wt rows (co, then k) or W rows (k, then co)
+        const int co = a.wsk == 1 ? i / a.K : i % CO, k = a.wsk == 1 ? i % a.K : i / CO;
+        wl[k * CO + co] = a.w[i];
+    }
+    __syncthreads();
+    float wb[KP][NB], bv[NB];
+    int dyx[KP], off[KP];
+#pragma unroll
+    for (int p = 0; p < KP; ++p) {
+        const int k = 2 * p + g;
+        dyx[p] = g ? a.dyx[2 * p + 1] : a.dyx[2 * p];
+        off[p] = g ? a.off[2 * p + 1] : a.off[2 * p];
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) wb[p][nb] = k < a.K ? wl[k * CO + 32 * nb + rl] : 0.0f;
+    }
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) bv[nb] = a.bias ? a.bias[32 * nb + rl] : 0.0f;
+    // A row of lane rl: pixel m0 + rl (rows past M gather zeros and are not stored)
+    // Branch-free: a lane whose k is padding, past K or of a pixel past M loads the zero word instead, so the loads
+    // issue back to back under one exec mask and their values feed the MFMAs unchanged (no select after the load).
+    auto gather = [&](long long m0, float (&av)[KP]) {
+        const long long mp = m0 + rl;
+        const bool pok = mp < a.M;
+        const int m = pok ? (int)mp : 0;
+        const int ox = m % a.Wo, r = m / a.Wo, oy = r % a.Ho, b = r / a.Ho;
+        const int iy0 = oy * a.sh - a.pt, ix0 = ox * a.sw - a.pl;
+        const float* px = a.x + (((long long)b * a.H + iy0) * a.W + ix0) * a.C;  // never read at a padded corner
+#pragma unroll
+        for (int p = 0; p < KP; ++p) {
+            const int iy = iy0 + (dyx[p] >> 16), ix = ix0 + (dyx[p] & 0xffff);
+            const bool in = pok & (2 * p + g < a.K) & ((unsigned)iy < (unsigned)a.H) & ((unsigned)ix < (unsigned)a.W);
+            av[p] = *(in ? px + off[p] : &conv_zero_word);
+        }
+    };
+    // multiply the gathered group at m0 and write it
+    auto group = [&](long long m0, const float (&av)[KP]) {
+        v16f acc[NB];
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[nb][e] = 0.0f;
+#pragma unroll
+        for (int p = 0; p < KP; ++p)  // all 16 pairs: pairs past K multiply zeros (no branch between the MFMAs)
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[p], wb[p][nb], acc[nb], 0, 0, 0);
+        // accumulator e of block nb: pixel m0 + 8·(e >> 2) + 4·g + (e & 3), channel 32·nb + rl; Co = 32·NB, so
+        // every element's offset from this lane's first one is a constant
+        const size_t first = (size_t)(m0 + 4 * g) * CO + rl;
+        float* yl = a.y + first;
+        const int left = (int)std::min<long long>(a.M - m0 - 4 * g, 32);  // rows of this lane's half still in M
+        auto write = [&](bool all) {  // all: the whole group is inside M (no per-row test)
+            float rres[NB][16];
+            if (RES) {  // every residual element this lane adds is loaded before its stores (R may be y)
+                const float* rlp = a.R + first;
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) {
+                        const int row = 8 * (e >> 2) + (e & 3);
+                        rres[nb][e] = all || row < left ? rlp[row * CO + 32 * nb] : 0.0f;
+                    }
+            }
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int row = 8 * (e >> 2) + (e & 3);
+                    float v = acc[nb][e];
+                    if (a.bias) v = v + bv[nb];
+                    if (a.relu) v = v >= 0.0f ? v : 0.0f;  // the ReLU of knx_act (NaN → 0)
+                    if (RES) v = v + rres[nb][e];
+                    if (all || row < left) yl[row * CO + 32 * nb] = v;
+                }
+        };
+        if (m0 + 32 <= a.M) write(true);  // m0 is the same in every lane: a scalar branch
+        else write(false);
+    };
+    // Each wave takes the groups of 32 pixels m0, m0 + step, …; the next group's inputs are in flight while one
+    // multiplies and stores (two input buffers, alternating).
+    const long long step = (long long)gridDim.x * 128;
+    long long m0 = ((long long)blockIdx.x * 4 + wave) * 32;
+    float av0[KP], av1[KP];
+    gather(m0, av0);
+    while (m0 < a.M) {
+        gather(m0 + step, av1);
+        group(m0, av0);
+        m0 += step;
+        if (m0 >= a.M) break;
+        gather(m0 + step, av0);
+        group(m0, av1);
+        m0 += step;
+    }
+}
+
+// Runs the MFMA kernel above when the shape qualifies (one group, K ≤ 32, Co ∈ {32, 64, 96, 128}, no activation or
+// ReLU, offsets within int); returns 1 without launching otherwise.  KNX_CONV_SMALL=0 turns it off, "g<N>" launches
+// N workgroups per CU instead of 2 (tests, tuning).  3×3 over 3 channels to 64, 256×32×32 pixels: 25.5 µs with 2 per
+// CU (1: 27.9, 3: 30.0, 4: 29.0) against 43 µs for the tile kernel.
+int conv_small_entry(const knx_conv_geom* g, const float* x, const float* w, bool transposed, const float* bias,
+                     int act, const float* R, float* y, hipStream_t s, const char* name)
+{
+    const char* env = getenv("KNX_CONV_SMALL");
+    if (env != nullptr && strcmp(env, "0") == 0) return 1;
+    const int K = g->kh * g->kw * g->C;
+    if (g->groups != 1 || K > SMALL_K || g->Co % 32 != 0 || g->Co > 128 || (act != -1 && act != 0)) return 1;
+    const long long span = ((long long)(g->kh - 1) * g->dh * g->W + (long long)(g->kw - 1) * g->dw + 1) * g->C;
+    if (span > 0x7fffffffLL || (g->kh - 1) * g->dh > 0x7fff || (g->kw - 1) * g->dw > 0xffff) return 1;
+    SmallConvArgs a{};
+    a.x = x; a.w = w; a.bias = bias; a.R = R; a.y = y;
+    a.H = g->H; a.W = g->W; a.C = g->C; a.Ho = g->Ho; a.Wo = g->Wo; a.Co = g->Co;
+    a.sh = g->sh; a.sw = g->sw; a.pt = g->pt; a.pl = g->pl; a.relu = act == 0;
+    a.M = g->B * g->Ho * g->Wo;
+    a.K = K;
+    a.wsc = transposed ? K : 1;
+    a.wsk = transposed ? 1 : g->Co;
+    for (int k = 0; k < K; ++k) {  // k = (ky, kx, ci), the im2col order
+        const int tap = k / g->C, ci = k % g->C, ky = tap / g->kw, kx = tap % g->kw;
+        a.dyx[k] = ky * g->dh << 16 | kx * g->dw;
+        a.off[k] = (int)(((long long)ky * g->dh * g->W + (long long)kx * g->dw) * g->C + ci);
+    }
+    const long groups32 = ((long)a.M + 31) / 32;
+    long per_cu = 2;  // about the resident workgroups
+    if (env != nullptr && env[0] == 'g') per_cu = std::max(1L, strtol(env + 1, nullptr, 10));
+    const long blocks = std::min<long>((groups32 + 3) / 4, per_cu * knx::num_cus());
+    const dim3 grid((unsigned)blocks);
+    switch (g->Co / 32 * 2 + (R != nullptr)) {
+    case 2: hipLaunchKernelGGL((conv_small<1, false>), grid, dim3(256), 0, s, a); break;
+    case 3: hipLaunchKernelGGL((conv_small<1, true>), grid, dim3(256), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((conv_small<2, false>), grid, dim3(256), 0, s, a); break;
+    case 5: hipLaunchKernelGGL((conv_small<2, true>), grid, dim3(256), 0, s, a); break;
+    case 6: hipLaunchKernelGGL((conv_small<3, false>), grid, dim3(256), 0, s, a); break;
+    case 7: hipLaunchKernelGGL((conv_small<3, true>), grid, dim3(256), 0, s, a); break;
+    case 8: hipLaunchKernelGGL((conv_small<4, false>), grid, dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL((conv_small<4, true>), grid, dim3(256), 0, s, a); break;
+    }
+    return knx::check_launch(name);
+}
+
 template <int BM, int BN, int WM, int WN, bool TB>
 int launch(ConvArgs p, bool vec, hipStream_t s, const char* name)
 {
@@ -258,6 +435,10 @@ int conv_entry(const knx_conv_geom* g, const float* x, const float* w, const flo
     if (g->B == 0) return KNX_OK;
     KNX_REQUIRE(x && w && y && x != y, name);
     hipStream_t s = knx::as_stream(stream);
+    {
+        const int rc = conv_small_entry(g, x, w, TB, bias, act, R, y, s, name);
+        if (rc != 1) return rc;
+    }
     if (TB) {
         const int rc = knx_conv_k32(g, x, w, bias, act, alpha, R, y, s, name);
         if (rc != 1) return rc;

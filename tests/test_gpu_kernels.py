@@ -395,11 +395,20 @@ CONV_CASES = [
     (64, 32, 32, 64, 64, 3, 1, 2, 1, 2),
     (128, 16, 16, 64, 128, 3, 1, 1, 1, 1),
     (256, 16, 16, 128, 256, 3, 2, 1, 1, 1),
+    # the register-operand MFMA kernel (one group, K ≤ 32, Co ∈ {32, 64, 96, 128}): K = 25, 18 (even), 16 and 32
+    # (1×1 over 32 channels), Co = 32, 96, 128, stride 3 with dilation 3; pixel counts not a multiple of 32
+    (3, 7, 5, 1, 32, 5, 1, 2, 1, 1),
+    (2, 9, 11, 2, 96, 3, 2, 1, 1, 1),
+    (2, 6, 6, 4, 128, 2, 1, 0, 1, 1),
+    (3, 5, 5, 32, 32, 1, 1, 0, 1, 1),
+    (2, 10, 10, 3, 64, 3, 3, 2, 1, 3),
 ]
+SMALL_CONV_CASES = [c for c in CONV_CASES if c[8] == 1 and c[5] * c[5] * c[3] <= 32 and c[4] in (32, 64, 96, 128)]
 
 
 @pytest.mark.parametrize("case", [(64, 32, 32, 64, 64, 3, 1, 1, 1, 1), (2, 8, 8, 3, 64, 3, 1, 1, 1, 1),
-                                  (128, 16, 16, 128, 128, 3, 1, 1, 2, 1), (2, 11, 13, 5, 7, 2, 3, 0, 1, 1)])
+                                  (128, 16, 16, 128, 128, 3, 1, 1, 2, 1), (2, 11, 13, 5, 7, 2, 3, 0, 1, 1),
+                                  (2, 9, 11, 2, 96, 3, 2, 1, 1, 1)])
 def test_conv_residual(L, case):
     """y = relu(conv(x) + b) + R on the pipelined and the general kernel (the CONV + BINARY add fusion)"""
     B, H, W, C, Co, k, s, p, g, dil = case
@@ -419,6 +428,10 @@ def test_conv_residual(L, case):
     hipabi.check(L.knx_hip_conv_t_res(ctypes.byref(geom), ptr(dx), ptr(dwt), ptr(db), 0, 0.0, ptr(dR), ptr(y),
                                       hipabi.stream()))
     assert rel_err(host(y), want) <= 1e-4
+    # in place (R is y), as the fused forward runs an in-place residual add: the same bits
+    hipabi.check(L.knx_hip_conv_t_res(ctypes.byref(geom), ptr(dx), ptr(dwt), ptr(db), 0, 0.0, ptr(dR), ptr(dR),
+                                      hipabi.stream()))
+    assert np.array_equal(host(dR), host(y))
 
 
 CONV_TILES = ["256x256", "256x128", "128x128", "256x64", "128x64", "128x64w2"]
@@ -432,6 +445,35 @@ def test_conv_tiles(L, case, tile, monkeypatch):
     """every forced tile of the pipelined convolution (where the shape allows it) against the direct convolution"""
     monkeypatch.setenv("KNX_CONV_TILE", tile)
     test_conv(L, case, True)
+
+
+@pytest.mark.parametrize("case", SMALL_CONV_CASES)
+def test_conv_small_off(L, case, monkeypatch):
+    """the shapes of the direct small-K kernel on the implicit-GEMM tile kernel instead (KNX_CONV_SMALL=0)"""
+    monkeypatch.setenv("KNX_CONV_SMALL", "0")
+    test_conv(L, case, True)
+    test_conv(L, case, False)
+
+
+@pytest.mark.parametrize("act", [-1, 1, 6])
+@pytest.mark.parametrize("case", [(2, 8, 8, 3, 64, 3, 1, 1, 1, 1), (2, 9, 11, 2, 96, 3, 2, 1, 1, 1)])
+def test_conv_small_act(L, case, act):
+    """small-K shapes without activation (the register-operand kernel) and with GELU and leaky ReLU (alpha 0.1,
+    the tile kernel)"""
+    B, H, W, C, Co, k, s, p, g, dil = case
+    rng = np.random.default_rng(sum(case) + act)
+    Ho = (H + 2 * p - dil * (k - 1) - 1) // s + 1
+    Wo = (W + 2 * p - dil * (k - 1) - 1) // s + 1
+    x = rng.standard_normal((B * H * W, C)).astype(np.float32)
+    w = (rng.standard_normal((k * k * C, Co)) / np.sqrt(k * k * C)).astype(np.float32)
+    b = rng.normal(0, 0.1, Co).astype(np.float32)
+    op = dict(cin=C, cout=Co, k=(k, k), s=(s, s), d=(dil, dil), p=(p, p, p, p), g=g, w=w, b=b)
+    want, _ = knx_ref._conv(x, B, H, W, op, act_id=act, alpha=0.1)
+    geom = hipabi.ConvGeom(B, H, W, C, Ho, Wo, Co, k, k, s, s, dil, dil, p, p, g)
+    y = torch.empty((B * Ho * Wo, Co), dtype=torch.float32, device="cuda")
+    dx, dwt, db = dev(x), dev(np.ascontiguousarray(w.T)), dev(b)
+    hipabi.check(L.knx_hip_conv_t(ctypes.byref(geom), ptr(dx), ptr(dwt), ptr(db), act, 0.1, ptr(y), hipabi.stream()))
+    assert rel_err(host(y), want) <= 1e-4
 
 
 @pytest.mark.parametrize("case", CONV_CASES)
