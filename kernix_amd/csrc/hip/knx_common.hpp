@@ -38,20 +38,23 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 __device__ __forceinline__ float knx_relu6(float v) { return v < 0.0f ? 0.0f : v > 6.0f ? 6.0f : v; }
 __device__ __forceinline__ float knx_softplus(float v) { return v > 20.0f ? v : log1pf(expf(v)); }
 
+// GELU with Abramowitz–Stegun 7.1.26 erf; exp and 1/(1 + p·z) on the hardware exp2 / reciprocal (≤ 1-2 ulp each; the
+// formula's own error is 1.5e-7), as the epilogue of large GEMMs evaluates it once per output element
+__device__ __forceinline__ float knx_gelu(float x)
+{
+    const float z = fabsf(x) * 0.70710678f;
+    const float t = __builtin_amdgcn_exp2f(-(z * z) * 1.44269504f);
+    const float k = __builtin_amdgcn_rcpf(1.0f + 0.3275911f * z);
+    const float p = k * (0.254829592f + k * (-0.284496736f + k * (1.421413741f + k * (-1.453152027f + k * 1.061405429f))));
+    const float e = 1.0f - p * t;
+    return 0.5f * x * (1.0f + (x < 0.0f ? -e : e));
+}
+
 __device__ __forceinline__ float knx_act(float x, int act, float alpha)
 {
     switch (act) {
     case 0: return x >= 0.0f ? x : 0.0f;  // threshold at 0 (NaN → 0, as vDSP_vthr and Metal max)
-    case 1: {  // GELU with Abramowitz–Stegun 7.1.26 erf; exp and 1/(1 + p·z) on the hardware exp2 / reciprocal
-               // (≤ 1-2 ulp each; the formula's own error is 1.5e-7), as the epilogue of large GEMMs evaluates it
-               // once per output element
-        const float z = fabsf(x) * 0.70710678f;
-        const float t = __builtin_amdgcn_exp2f(-(z * z) * 1.44269504f);
-        const float k = __builtin_amdgcn_rcpf(1.0f + 0.3275911f * z);
-        const float p = k * (0.254829592f + k * (-0.284496736f + k * (1.421413741f + k * (-1.453152027f + k * 1.061405429f))));
-        const float e = 1.0f - p * t;
-        return 0.5f * x * (1.0f + (x < 0.0f ? -e : e));
-    }
+    case 1: return knx_gelu(x);
     case 2: { const float s = 1.0f / (1.0f + expf(-x)); return x * s; }
     case 3: return 1.0f / (1.0f + expf(-x));
     case 4: return tanhf(x);

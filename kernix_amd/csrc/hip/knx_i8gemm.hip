@@ -240,7 +240,8 @@ __global__ void __launch_bounds__(WM * WN * 64) i8gemm_tile(I8Args p)
 #define KERNIX_ACT_RELU_ID 0
 
 // Writes the 16 staged rows [mt0, mt0+16) of a tile: 4 consecutive columns per lane, one 16-byte store per row.
-// ACT ≥ −1 is a compile-time activation for the common case (vector path, no accumulation); −2 is the general path.
+// ACT ≥ −1 is a compile-time activation for the common case (vector path, no accumulation): none, ReLU or GELU;
+// −2 is the general path.
 template <int ACT>
 __device__ __forceinline__ void store_rows(const I8Args& p, const int* stg, const float* row_scale, int mt0, int m0, int mlo,
                                            int nlo, int rq, int rpi, int srow, int cq, int nb, const float* swv,
@@ -248,7 +249,7 @@ __device__ __forceinline__ void store_rows(const I8Args& p, const int* stg, cons
 {
     typedef float v4f_t __attribute__((ext_vector_type(4)));
     if (ACT >= -1 && p.R) {
-        // Residual after no activation or ReLU: the round's residual rows are loaded before any store (R and Y may
+        // Residual after no activation, ReLU or GELU: the round's residual rows are loaded before any store (R and Y may
         // alias, and a load after a store waits for it: one memory round trip per row).  Loading first is right when
         // R is Y, since each element is read before its own store and no other store touches it.  Unrolled, so the
         // loads sit in registers; the per-row code is a few instructions.
@@ -283,7 +284,7 @@ __device__ __forceinline__ void store_rows(const I8Args& p, const int* stg, cons
                 float v = (float)a[q] * sx;  // ((float)acc · sx) · scale + bias, each step rounded
                 v = v * swv[q];
                 if (p.bias) v = v + bv[q];
-                r[q] = (ACT == 0 ? (v >= 0.0f ? v : 0.0f) : v) + rres[j][q];
+                r[q] = (ACT == 0 ? (v >= 0.0f ? v : 0.0f) : ACT == 1 ? knx_gelu(v) : v) + rres[j][q];
             }
             __builtin_nontemporal_store(r, reinterpret_cast<v4f_t*>(p.Y + (size_t)m * p.ldy + nb));
         }
@@ -302,7 +303,7 @@ __device__ __forceinline__ void store_rows(const I8Args& p, const int* stg, cons
                 float v = (float)a[q] * sx;  // ((float)acc · sx) · scale + bias, each step rounded
                 v = v * swv[q];
                 if (p.bias) v = v + bv[q];   // no bias: no addition (x + 0 would turn −0 into +0)
-                r[q] = ACT == 0 ? (v >= 0.0f ? v : 0.0f) : v;
+                r[q] = ACT == 0 ? (v >= 0.0f ? v : 0.0f) : ACT == 1 ? knx_gelu(v) : v;
             }
             // streaming store: the output is written once and never re-read by this kernel
             __builtin_nontemporal_store(r, reinterpret_cast<v4f_t*>(p.Y + (size_t)m * p.ldy + nb));
@@ -371,6 +372,8 @@ __device__ __forceinline__ void tile_epilogue(const I8Args& p, const v16i (&acc)
             const bool fast = vec && p.Y && !p.acc && !p.accumulate;  // plain Y store (no raw accumulators requested)
             if (fast && p.act == KERNIX_ACT_RELU_ID)
                 store_rows<0>(p, stg, row_scale, mt0, m0, mlo, nlo, rq, RPI, SROW, cq, nb, swv, bv);
+            else if (fast && p.act == 1)  // GELU
+                store_rows<1>(p, stg, row_scale, mt0, m0, mlo, nlo, rq, RPI, SROW, cq, nb, swv, bv);
             else if (fast && p.act == -1)
                 store_rows<-1>(p, stg, row_scale, mt0, m0, mlo, nlo, rq, RPI, SROW, cq, nb, swv, bv);
             else
@@ -1509,7 +1512,11 @@ static int i8gemm_run(I8Args p, hipStream_t s, const char* name)
         return launch_k128<256, 256, 4, 2, 2>(p, s, name);
     }
     const long tiles128 = (long)((M + 127) / 128) * ((N + 127) / 128);
-    if (tiles128 >= knx::num_cus() && k128_fits<128, 128>(p)) return launch_k128<128, 128, 2, 2, 2>(p, s, name);
+    // 128×128: three A stages once K is long (8192×512×2048 + residual: 19.5 against 21.3 µs)
+    if (tiles128 >= knx::num_cus() && k128_fits<128, 128>(p)) {
+        if (K >= 2048) return launch_k128<128, 128, 2, 2, 3>(p, s, name);
+        return launch_k128<128, 128, 2, 2, 2>(p, s, name);
+    }
     // fewer tiles than CUs even at 128×128 (e.g. M = 256, N = 4096): one 64×64 tile per workgroup on the deep LDS
     // ring (M = 256: 13.2 µs against 16.8 for the 64-byte k-tile pipeline)
     if (k128_fits<64, 64>(p)) return launch_ring<64, 64, 2, 2, 4, 1>(p, s, name);

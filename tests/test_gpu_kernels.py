@@ -182,6 +182,32 @@ def test_qlinear(L, monkeypatch, rows, k, n, path):
     assert np.array_equal(got[~np.isnan(got)], want[~np.isnan(want)])
 
 
+@pytest.mark.parametrize("act", [1, 5])
+@pytest.mark.parametrize("M,N,K", [(2048, 2048, 512), (1024, 1024, 2048), (520, 700, 320)])
+def test_i8gemm_activation_epilogues(L, act, M, N, K):
+    """GELU (its own compile-time epilogue) and leaky ReLU (the general one) on the tile kernels: the plain call is
+    bit-identical to the general epilogue (forced by asking for the raw int32 accumulators too) and within the GELU
+    formula's hardware-exp2/reciprocal error of the oracle"""
+    rng = np.random.default_rng(M + N + K + act)
+    A = rng.integers(-127, 128, (M, K), dtype=np.int8)
+    W = rng.integers(-128, 128, (N, K), dtype=np.int8)
+    sa = rng.uniform(0.001, 0.01, M).astype(np.float32)
+    sw = rng.uniform(0.001, 0.01, N).astype(np.float32)
+    bias = rng.normal(0, 0.1, N).astype(np.float32)
+    want_y, want_acc = knx_ref.i8gemm(A, W, sa, sw, bias, act_id=act, alpha=0.1)
+    dA, dW, dsa, dsw, db = dev(A), dev(W), dev(sa), dev(sw), dev(bias)
+    Y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    Y2 = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    acc = torch.empty((M, N), dtype=torch.int32, device="cuda")
+    hipabi.check(L.knx_hip_i8gemm(M, N, K, ptr(dA), K, ptr(dsa), ptr(dW), K, ptr(dsw), ptr(db), act, 0.1, 0,
+                                  ptr(Y), N, None, 0, hipabi.stream()))
+    hipabi.check(L.knx_hip_i8gemm(M, N, K, ptr(dA), K, ptr(dsa), ptr(dW), K, ptr(dsw), ptr(db), act, 0.1, 0,
+                                  ptr(Y2), N, ptr(acc), N, hipabi.stream()))
+    assert np.array_equal(host(acc), want_acc)
+    assert np.array_equal(host(Y), host(Y2))
+    assert rel_err(host(Y), want_y) <= 1e-6
+
+
 def test_i8gemm_accumulate_and_no_bias(L):
     rng = np.random.default_rng(3)
     M, N, K = 37, 70, 128
@@ -458,8 +484,8 @@ def test_conv_small_off(L, case, monkeypatch):
 @pytest.mark.parametrize("act", [-1, 1, 6])
 @pytest.mark.parametrize("case", [(2, 8, 8, 3, 64, 3, 1, 1, 1, 1), (2, 9, 11, 2, 96, 3, 2, 1, 1, 1)])
 def test_conv_small_act(L, case, act):
-    """small-K shapes without activation (the register-operand kernel) and with GELU and leaky ReLU (alpha 0.1,
-    the tile kernel)"""
+    """small-K shapes without activation (the register-operand kernel) and with GELU and ELU (alpha 0.1, the tile
+    kernel)"""
     B, H, W, C, Co, k, s, p, g, dil = case
     rng = np.random.default_rng(sum(case) + act)
     Ho = (H + 2 * p - dil * (k - 1) - 1) // s + 1
