@@ -501,34 +501,44 @@ __global__ void __launch_bounds__(WM * WN * 64) sgemm_k32(SgArgs p)
                     }
                 }
             } else {
-                // General epilogue: one row per iteration, a rolled loop (the activation switch appears once).
-                for (int rr = rq; rr < 16; rr += RPI) {
-                    const int m = mt0 + rr;
-                    if (m < mlo) continue;
-                    const float4 a = *reinterpret_cast<const float4*>(&stg[rr * SROW + cq]);
-                    float r[4];
+                // General epilogue: one row per iteration, a rolled loop; GELU, ReLU and no activation are
+                // compile-time cases (an activation switch per element costs as much as GELU itself), any other
+                // activation goes through the switch
+                auto rows = [&](auto actc) {
+                    constexpr int ACT = decltype(actc)::value;
+                    for (int rr = rq; rr < 16; rr += RPI) {
+                        const int m = mt0 + rr;
+                        if (m < mlo) continue;
+                        const float4 a = *reinterpret_cast<const float4*>(&stg[rr * SROW + cq]);
+                        float r[4];
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        float v = (&a.x)[q];
-                        if (p.alpha != 1.0f) v = p.alpha * v;
-                        if (bias) v = v + bv[q];
-                        if (p.causal && nb + q > m) v = -INFINITY;
-                        r[q] = knx_act(v, p.act, p.act_alpha);
-                    }
-                    float* y = C + (size_t)m * p.ldc + nb;
-                    if (R) {  // residual after the activation; each element is read before its own store
+                        for (int q = 0; q < 4; ++q) {
+                            float v = (&a.x)[q];
+                            if (p.alpha != 1.0f) v = p.alpha * v;
+                            if (bias) v = v + bv[q];
+                            if (p.causal && nb + q > m) v = -INFINITY;
+                            r[q] = ACT == 1 ? knx_gelu(v) : ACT == 0 ? (v >= 0.0f ? v : 0.0f) : ACT == -1 ? v
+                                                                        : knx_act(v, p.act, p.act_alpha);
+                        }
+                        float* y = C + (size_t)m * p.ldc + nb;
+                        if (R) {  // residual after the activation; each element is read before its own store
 #pragma unroll
-                        for (int q = 0; q < 4; ++q)
-                            if (nb + q >= nlo) r[q] = r[q] + R[(size_t)m * p.ldr + nb + q];
-                    }
-                    if (vec) {
-                        *reinterpret_cast<float4*>(y) = make_float4(r[0], r[1], r[2], r[3]);
-                    } else {
+                            for (int q = 0; q < 4; ++q)
+                                if (nb + q >= nlo) r[q] = r[q] + R[(size_t)m * p.ldr + nb + q];
+                        }
+                        if (vec) {
+                            *reinterpret_cast<float4*>(y) = make_float4(r[0], r[1], r[2], r[3]);
+                        } else {
 #pragma unroll
-                        for (int q = 0; q < 4; ++q)
-                            if (nb + q >= nlo) y[q] = r[q];
+                            for (int q = 0; q < 4; ++q)
+                                if (nb + q >= nlo) y[q] = r[q];
+                        }
                     }
-                }
+                };
+                if (p.act == 1) rows(std::integral_constant<int, 1>{});
+                else if (p.act == 0) rows(std::integral_constant<int, 0>{});
+                else if (p.act == -1) rows(std::integral_constant<int, -1>{});
+                else rows(std::integral_constant<int, -2>{});
             }
             asm volatile("" ::: "memory");
         }
