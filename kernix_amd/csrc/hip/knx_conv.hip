@@ -240,11 +240,12 @@ __global__ void __launch_bounds__(WM * WN * 64) conv_tile(ConvArgs p)
 // ---------------------------------------------------------------- convolution with few inputs per output
 // A first layer such as 3×3 over RGB (K = 27) is a poor fit for the k-tiled kernels: K pads to whole k-tiles of
 // LDS-staged operands while the output, Co fp32 channels per pixel, is what costs.  Here each wave owns 32 output
-// pixels at a time and multiplies straight from registers on v_mfma_f32_32x32x2f32: lane l gathers, for pixel
-// l & 31, the inputs k = 2p + (l >> 5) of every k pair p (the A fragments, K ≤ 32 so at most 16 pairs), the weights
-// sit in registers as the B fragments for the whole kernel (Co = 32·NB, NB ≤ 4), and every accumulator register is
-// stored directly (two 128-byte row segments per instruction).  Epilogue: bias, then ReLU or nothing, then the
-// residual, each an fp32 rounding as in the other convolution kernels.
+// pixels at a time and multiplies its gathered inputs straight from registers on v_mfma_f32_32x32x2f32: lane l
+// gathers, for pixel l & 31, the inputs k = 2p + (l >> 5) of every k pair p (the A fragments, K ≤ 32 so at most 16
+// pairs); the weights are staged once per workgroup in LDS and read from there as the B fragments (Co = 32·NB,
+// NB ≤ 4; holding them in registers cost a wave per SIMD of occupancy); every accumulator register is stored
+// directly (two 128-byte row segments per instruction).  Epilogue: bias, then ReLU or nothing, then the residual,
+// each an fp32 rounding as in the other convolution kernels.
 constexpr int SMALL_K = 32;
 
 struct SmallConvArgs {
@@ -277,15 +278,15 @@ __global__ void __launch_bounds__(256) conv_small(SmallConvArgs a)
         wl[k * CO + co] = a.w[i];
     }
     __syncthreads();
-    float wb[KP][NB], bv[NB];
+    // rows k ≥ K of the staged weights are zero, so every k pair can be multiplied
+    for (int i = a.K * CO + threadIdx.x; i < SMALL_K * CO; i += 256) wl[i] = 0.0f;
+    __syncthreads();
+    float bv[NB];
     int dyx[KP], off[KP];
 #pragma unroll
     for (int p = 0; p < KP; ++p) {
-        const int k = 2 * p + g;
         dyx[p] = g ? a.dyx[2 * p + 1] : a.dyx[2 * p];
         off[p] = g ? a.off[2 * p + 1] : a.off[2 * p];
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) wb[p][nb] = k < a.K ? wl[k * CO + 32 * nb + rl] : 0.0f;
     }
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) bv[nb] = a.bias ? a.bias[32 * nb + rl] : 0.0f;
@@ -316,7 +317,8 @@ __global__ void __launch_bounds__(256) conv_small(SmallConvArgs a)
 #pragma unroll
         for (int p = 0; p < KP; ++p)  // all 16 pairs: pairs past K multiply zeros (no branch between the MFMAs)
 #pragma unroll
-            for (int nb = 0; nb < NB; ++nb) acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[p], wb[p][nb], acc[nb], 0, 0, 0);
+            for (int nb = 0; nb < NB; ++nb)  // B fragment: weight (k = 2p + g, channel 32·nb + rl) from LDS
+                acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[p], wl[(2 * p + g) * CO + 32 * nb + rl], acc[nb], 0, 0, 0);
         // accumulator e of block nb: pixel m0 + 8·(e >> 2) + 4·g + (e & 3), channel 32·nb + rl; Co = 32·NB, so
         // every element's offset from this lane's first one is a constant
         const size_t first = (size_t)(m0 + 4 * g) * CO + rl;
@@ -368,8 +370,8 @@ __global__ void __launch_bounds__(256) conv_small(SmallConvArgs a)
 
 // Runs the MFMA kernel above when the shape qualifies (one group, K ≤ 32, Co ∈ {32, 64, 96, 128}, no activation or
 // ReLU, offsets within int); returns 1 without launching otherwise.  KNX_CONV_SMALL=0 turns it off, "g<N>" launches
-// N workgroups per CU instead of 2 (tests, tuning).  3×3 over 3 channels to 64, 256×32×32 pixels: 25.5 µs with 2 per
-// CU (1: 27.9, 3: 30.0, 4: 29.0) against 43 µs for the tile kernel.
+// N workgroups per CU instead of 3 (tests, tuning).  3×3 over 3 channels to 64, 256×32×32 pixels: 24.5 µs with 3 per
+// CU (2: 25.1, 4: 26.1, 6: 27.7) against 43 µs for the tile kernel.
 int conv_small_entry(const knx_conv_geom* g, const float* x, const float* w, bool transposed, const float* bias,
                      int act, const float* R, float* y, hipStream_t s, const char* name)
 {
@@ -393,7 +395,7 @@ int conv_small_entry(const knx_conv_geom* g, const float* x, const float* w, boo
         a.off[k] = (int)(((long long)ky * g->dh * g->W + (long long)kx * g->dw) * g->C + ci);
     }
     const long groups32 = ((long)a.M + 31) / 32;
-    long per_cu = 2;  // about the resident workgroups
+    long per_cu = 3;  // about the resident workgroups
     if (env != nullptr && env[0] == 'g') per_cu = std::max(1L, strtol(env + 1, nullptr, 10));
     const long blocks = std::min<long>((groups32 + 3) / 4, per_cu * knx::num_cus());
     const dim3 grid((unsigned)blocks);
