@@ -116,12 +116,14 @@ __global__ void __launch_bounds__(256) attention_fused(const float* __restrict__
         const float w = __shfl_xor(m, 32, 64);
         m = w > m ? w : m;
     }
+    // exp(x − max) as the hardware exp2 of (x − max)·log2(e) (≤ 1-2 ulp): a libm expf is some twenty instructions, and
+    // with 64 of them per lane the softmax took as long as the two products; masked keys give exp2(−inf) = 0
     float sum = 0.0f;
 #pragma unroll
     for (int t = 0; t < NS; ++t)
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-            sc[t][e] = expf(sc[t][e] - m);
+            sc[t][e] = __builtin_amdgcn_exp2f((sc[t][e] - m) * 1.44269504f);
             sum += sc[t][e];
         }
     sum += __shfl_xor(sum, 32, 64);
