@@ -22,6 +22,8 @@
  *   knx_hip_conv_t_res,     step followed by the BINARY add of another value:    :1005-1048, :877-906
  *   knx_hip_i8gemm_res      the step's epilogue adds the other operand
  *   knx_hip_layernorm       kernix_layer_norm_rows_into                         include/kernix.h:667-677
+ *   knx_hip_layernorm_quantize  a LAYERNORM whose rows feed only an int8 LINEAR: include/kernix.h:667-677, then
+ *                           kernix_qmatmul's row quantization               include/kernix_model.h:112-142
  *   knx_hip_softmax         floats_softmax_into                                 include/kernix.h:652-657
  *   knx_hip_bias_act        kernix_bias_act / ACT step                          include/kernix_model.h:528-541, :1866-1869
  *   knx_hip_binary          kernix_binary_run                                   include/kernix_model.h:877-906
@@ -145,6 +147,12 @@ KNX_API int knx_hip_conv_t_res(const knx_conv_geom* g, const float* x, const flo
 /* ---- row and elementwise ops (y may equal x unless noted) ---- */
 KNX_API int knx_hip_layernorm(const float* x, float* y, int rows, int cols, const float* gamma, const float* beta,
                               float eps, void* stream);
+/* layer_norm of each row followed by kernix_qmatmul's per-row int8 quantization of the normalized row (the steps of
+ * knx_hip_quantize_rows): xq (rows × kp, zero past cols) and sx (rows) get the bits of knx_hip_layernorm then
+ * knx_hip_quantize_rows, and the fp32 rows are not written.  cols % 4 == 0, cols ≤ 2048, kp ≥ cols, kp % 4 == 0,
+ * x, gamma and beta 16-byte aligned. */
+KNX_API int knx_hip_layernorm_quantize(const float* x, int rows, int cols, const float* gamma, const float* beta,
+                                       float eps, int kp, int8_t* xq, float* sx, void* stream);
 KNX_API int knx_hip_softmax(const float* x, float* y, int rows, int cols, void* stream);
 KNX_API int knx_hip_bias_act(const float* x, float* y, int rows, int cols, const float* bias, int act, float alpha,
                              void* stream);

@@ -74,14 +74,12 @@ __device__ __forceinline__ float group_max(float v)
 }
 __device__ __forceinline__ float f4(const float4& v, int e) { return e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w; }
 
-// layer_norm, same formulas as layernorm_kernel (x may alias y: every lane reads its whole row before writing)
+// layer_norm of one row, same formulas as layernorm_kernel: lane l of the row's G lanes gets its float4 chunks
+// l, l + G, … of the normalized row in o (chunks past the row are left unset)
 template <int G, int NV>
-__global__ void __launch_bounds__(256) layernorm_vec(const float* x, float* y, int rows, int cols,
-                                                      const float* __restrict__ gamma, const float* __restrict__ beta,
-                                                      float eps)
+__device__ __forceinline__ void ln_row(const float* x, int row, int cols, int l, const float* __restrict__ gamma,
+                                       const float* __restrict__ beta, float eps, float4 (&o)[NV])
 {
-    const int row = blockIdx.x * (256 / G) + (int)threadIdx.x / G, l = threadIdx.x % G;
-    if (row >= rows) return;
     const float4* xr = reinterpret_cast<const float4*>(x + (size_t)row * cols);
     const int nq = cols >> 2;
     float4 v[NV];
@@ -100,7 +98,6 @@ __global__ void __launch_bounds__(256) layernorm_vec(const float* x, float* y, i
 #pragma unroll
             for (int e = 0; e < 4; ++e) { const float d = f4(v[i], e) - mean; ss += d * d; }
     const float rstd = 1.0f / sqrtf(group_sum<G>(ss) / (float)cols + eps);
-    float4* yr = reinterpret_cast<float4*>(y + (size_t)row * cols);
     const float4* g4 = reinterpret_cast<const float4*>(gamma);  // 16-byte aligned (checked by the caller)
     const float4* b4 = reinterpret_cast<const float4*>(beta);
 #pragma unroll
@@ -109,17 +106,88 @@ __global__ void __launch_bounds__(256) layernorm_vec(const float* x, float* y, i
         if (q >= nq) continue;
         const float4 gq = gamma ? g4[q] : make_float4(1.f, 1.f, 1.f, 1.f);
         const float4 bq = beta ? b4[q] : make_float4(0.f, 0.f, 0.f, 0.f);
-        float o[4];
+        float t4[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             float t = (f4(v[i], e) - mean) * rstd;
             if (gamma && beta) t = t * f4(gq, e) + f4(bq, e);
             else if (gamma) t = t * f4(gq, e);
             else if (beta) t = t + f4(bq, e);
-            o[e] = t;
+            t4[e] = t;
         }
-        yr[q] = make_float4(o[0], o[1], o[2], o[3]);
+        o[i] = make_float4(t4[0], t4[1], t4[2], t4[3]);
     }
+}
+
+// layer_norm (x may alias y: every lane reads its whole row before writing)
+template <int G, int NV>
+__global__ void __launch_bounds__(256) layernorm_vec(const float* x, float* y, int rows, int cols,
+                                                      const float* __restrict__ gamma, const float* __restrict__ beta,
+                                                      float eps)
+{
+    const int row = blockIdx.x * (256 / G) + (int)threadIdx.x / G, l = threadIdx.x % G;
+    if (row >= rows) return;
+    float4 o[NV];
+    ln_row<G, NV>(x, row, cols, l, gamma, beta, eps, o);
+    float4* yr = reinterpret_cast<float4*>(y + (size_t)row * cols);
+    const int nq = cols >> 2;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+        if (i * G + l < nq) yr[i * G + l] = o[i];
+}
+
+// layer_norm followed by the per-row int8 quantization of kernix_qmatmul (the steps of knx_hip_quantize_rows: s = m/127
+// from the row's largest magnitude m, or 1 for an all-zero row; inv = 1/s; rint(x·inv) clamped to ±127; a row with
+// NaN or ±inf gets s = NaN and zeros) on the normalized row while it is still in registers: the int8 row (kp bytes,
+// zero past cols) and its scale are the result, the fp32 row is never written.  Same G, NV and arithmetic as
+// layernorm_vec and a maximum is exact in any order, so the bits are those of layer_norm then quantize_rows.
+template <int G, int NV>
+__global__ void __launch_bounds__(256) layernorm_quant_vec(const float* x, int rows, int cols,
+                                                            const float* __restrict__ gamma,
+                                                            const float* __restrict__ beta, float eps, int kp,
+                                                            int8_t* __restrict__ xq, float* __restrict__ sx)
+{
+    const int row = blockIdx.x * (256 / G) + (int)threadIdx.x / G, l = threadIdx.x % G;
+    if (row >= rows) return;
+    float4 o[NV];
+    ln_row<G, NV>(x, row, cols, l, gamma, beta, eps, o);
+    const int nq = cols >> 2, nqp = kp >> 2;
+    float m = 0.0f;
+    float bad = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+        if (i * G + l < nq)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float a = fabsf(f4(o[i], e));
+                if (!(a <= 3.402823466e38f)) bad = 1.0f;  // NaN or ±inf
+                else m = a > m ? a : m;
+            }
+    m = group_max<G>(m);
+    bad = group_max<G>(bad);
+    int* qr = reinterpret_cast<int*>(xq + (size_t)row * kp);
+    if (bad != 0.0f) {
+        for (int q = l; q < nqp; q += G) qr[q] = 0;
+        if (l == 0) sx[row] = __int_as_float(0x7fc00000);
+        return;
+    }
+    const float s = m > 0.0f ? __fdiv_rn(m, 127.0f) : 1.0f;
+    const float inv = __fdiv_rn(1.0f, s);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int q = i * G + l;
+        if (q >= nq) continue;
+        unsigned w = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float r = rintf(f4(o[i], e) * inv);
+            const int b = (int)(r > 127.0f ? 127.0f : r < -127.0f ? -127.0f : r);
+            w |= (unsigned)(b & 0xff) << (8 * e);
+        }
+        qr[q] = (int)w;
+    }
+    for (int q = nq + l; q < nqp; q += G) qr[q] = 0;
+    if (l == 0) sx[row] = s;
 }
 
 // softmax, same formulas as softmax_kernel; exp(x − max) is computed once and kept
@@ -445,6 +513,18 @@ extern "C" int knx_hip_layernorm(const float* x, float* y, int rows, int cols, c
         return knx::check_launch(name);
     }
     KNX_LAUNCH(name, layernorm_kernel, (rows + 3) / 4, x, y, rows, cols, gamma, beta, eps);
+}
+
+extern "C" int knx_hip_layernorm_quantize(const float* x, int rows, int cols, const float* gamma, const float* beta,
+                                          float eps, int kp, int8_t* xq, float* sx, void* stream)
+{
+    const char* name = "knx_hip_layernorm_quantize";
+    KNX_ENTRY(name);
+    KNX_REQUIRE(rows >= 0 && cols >= 4 && cols % 4 == 0 && cols / 4 <= 512 && kp >= cols && kp % 4 == 0, name);
+    if (rows == 0) return KNX_OK;
+    KNX_REQUIRE(x && xq && sx && aligned16(x) && aligned16(gamma) && aligned16(beta) && ((uintptr_t)xq & 3) == 0, name);
+    KNX_ROWVEC_DISPATCH(layernorm_quant_vec, cols / 4, rows, stream, x, rows, cols, gamma, beta, eps, kp, xq, sx);
+    return knx::check_launch(name);
 }
 
 extern "C" int knx_hip_softmax(const float* x, float* y, int rows, int cols, void* stream)

@@ -692,6 +692,55 @@ static int fusable_add(const kernix_model* m, int i)
     return other;
 }
 
+/* LAYERNORM step i whose output is read only by step i + 1, an int8 LINEAR that runs int8 arithmetic at more than 4
+ * rows (i8 mode) and so quantizes its input rows anyway: both run as knx_hip_layernorm_quantize into the LINEAR's
+ * int8 scratch and the int8 GEMM, and the fp32 LAYERNORM output is never written.  The normalized rows are computed
+ * by the same vector kernel as the separate layer_norm (cols % 4 == 0, ≤ 2048, 16-byte aligned), so the int8 rows,
+ * their scales and the outputs are the same bits. */
+static int ln_quant_fusable(const kernix_model* m, int i)
+{
+    if (i + 1 >= m->n_steps) return 0;
+    const kernix_step* s = &m->steps[i];
+    const kernix_step* n = &m->steps[i + 1];
+    if (s->kind != KERNIX_OP_LAYERNORM || n->kind != KERNIX_OP_LINEAR || n->q == NULL) return 0;
+    if (n->n_in != 1 || n->inp[0] != i + 1) return 0;
+    const kernix_val* v = &m->vals[i + 1];
+    if (v->last != i + 1 || m->out_v == i + 1) return 0;
+    const float_tensor* a = &m->views[s->inp[0]];
+    const struct knx_dstep* dl = s->dev;
+    const struct knx_dstep* d = n->dev;
+    if (m->int8_mode != KERNIX_INT8_I8 || a->row <= 4 || d->xq == NULL || a->row > d->xq_rows) return 0;
+    if (a->col % 4 != 0 || a->col > 2048 || a->col != n->q->k) return 0;
+    return (((uintptr_t)a->tensor | (uintptr_t)dl->gamma | (uintptr_t)dl->beta) & 15) == 0;
+}
+
+/* Runs LAYERNORM step i with the int8 LINEAR step i + 1 (see ln_quant_fusable), and the BINARY add after the LINEAR
+ * when fusable_add allows.  Returns the number of steps run, or -1. */
+static int run_ln_quant(kernix_model* m, int i, int fuse, void* st)
+{
+    const kernix_step* ln = &m->steps[i];
+    const kernix_step* s = &m->steps[i + 1];
+    const struct knx_dstep* dl = ln->dev;
+    const struct knx_dstep* d = s->dev;
+    const kernix_qweight* q = s->q;
+    const float_tensor* a = &m->views[ln->inp[0]];
+    if (hip_ok(knx_hip_layernorm_quantize(a->tensor, a->row, a->col, dl->gamma, dl->beta, ln->eps, q->kp, d->xq, d->sx,
+                                          st), "layer_norm + quantize"))
+        return -1;
+    const int r = fuse ? fusable_add(m, i + 1) : -1;
+    if (r >= 0) {
+        if (hip_ok(knx_hip_i8gemm_res(a->row, q->n, q->kp, d->xq, q->kp, d->sx, d->q, q->kp, d->qscale, d->bias, s->act,
+                                      s->alpha, m->views[r].tensor, q->n, m->views[i + 3].tensor, q->n, st),
+                   "int8 GEMM + add"))
+            return -1;
+        return 3;
+    }
+    if (hip_ok(knx_hip_i8gemm(a->row, q->n, q->kp, d->xq, q->kp, d->sx, d->q, q->kp, d->qscale, d->bias, s->act, s->alpha,
+                              0, m->views[i + 2].tensor, q->n, NULL, 0, st), "int8 GEMM"))
+        return -1;
+    return 2;
+}
+
 /* Enqueues every step for one chunk whose input starts at `in` (device). */
 static int run_chunk(kernix_model* m, const float* in, int B, void* st)
 {
@@ -703,6 +752,12 @@ static int run_chunk(kernix_model* m, const float* in, int B, void* st)
     const char* nf = getenv("KNX_NO_FUSE");
     const int fuse = nf == NULL || *nf == '\0' || *nf == '0';
     for (int i = 0; i < m->n_steps; i++) {
+        if (fuse && ln_quant_fusable(m, i)) {
+            const int c = run_ln_quant(m, i, fuse, st);
+            if (c < 0) return -1;
+            i += c - 1;
+            continue;
+        }
         const int r = fuse ? fusable_add(m, i) : -1;
         if (r >= 0) { /* step i and the add that follows it, in one pass */
             if (run_step(m, i, B, st, &m->views[i + 2], m->views[r].tensor) != 0) return -1;

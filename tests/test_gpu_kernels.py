@@ -253,6 +253,33 @@ def test_quantize_rows_bit_exact(L, rows, k):
         assert not got_q[r, k:].any()
 
 
+@pytest.mark.parametrize("rows,cols", [(5, 64), (37, 128), (64, 512), (9, 1000), (16, 2048)])
+def test_layernorm_quantize_bit_exact(L, rows, cols):
+    """layer_norm + quantize in one pass against knx_hip_layernorm then knx_hip_quantize_rows, bit for bit (int8 rows
+    with their zero padding to kp, scales, rows that normalize to NaN), at each lanes-per-row width of the row
+    kernels"""
+    rng = np.random.default_rng(rows * 7 + cols)
+    x = rng.normal(0, 2, (rows, cols)).astype(np.float32)
+    x[1, 3] = np.inf  # a row that normalizes to NaN
+    gamma = rng.normal(1, 0.2, cols).astype(np.float32)
+    beta = rng.normal(0, 0.2, cols).astype(np.float32)
+    kp = (cols + 63) // 64 * 64 + 64
+    dx, dg, db = dev(x), dev(gamma), dev(beta)
+    y = torch.empty((rows, cols), dtype=torch.float32, device="cuda")
+    q1 = torch.full((rows, kp), 99, dtype=torch.int8, device="cuda")
+    s1 = torch.empty(rows, dtype=torch.float32, device="cuda")
+    q2 = torch.full((rows, kp), 77, dtype=torch.int8, device="cuda")
+    s2 = torch.empty(rows, dtype=torch.float32, device="cuda")
+    hipabi.check(L.knx_hip_layernorm(ptr(dx), ptr(y), rows, cols, ptr(dg), ptr(db), 1e-5, hipabi.stream()))
+    hipabi.check(L.knx_hip_quantize_rows(ptr(y), cols, rows, cols, kp, ptr(q1), kp, ptr(s1), hipabi.stream()))
+    hipabi.check(L.knx_hip_layernorm_quantize(ptr(dx), rows, cols, ptr(dg), ptr(db), 1e-5, kp, ptr(q2), ptr(s2),
+                                              hipabi.stream()))
+    assert np.array_equal(host(q1), host(q2))
+    a, b = host(s1), host(s2)
+    assert np.isnan(a[1]) and np.isnan(b[1])
+    assert np.array_equal(a[~np.isnan(a)], b[~np.isnan(b)])
+
+
 # ---------------------------------------------------------------- fp32 GEMM
 SG_SHAPES = [(1, 1, 1), (3, 10, 7), (64, 512, 784), (37, 96, 128), (130, 1000, 256), (512, 512, 512),
              (2048, 1024, 128), (8, 3, 0)]
