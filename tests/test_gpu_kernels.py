@@ -461,7 +461,8 @@ SMALL_CONV_CASES = [c for c in CONV_CASES if c[8] == 1 and c[5] * c[5] * c[3] <=
 
 @pytest.mark.parametrize("case", [(64, 32, 32, 64, 64, 3, 1, 1, 1, 1), (2, 8, 8, 3, 64, 3, 1, 1, 1, 1),
                                   (128, 16, 16, 128, 128, 3, 1, 1, 2, 1), (2, 11, 13, 5, 7, 2, 3, 0, 1, 1),
-                                  (2, 9, 11, 2, 96, 3, 2, 1, 1, 1)])
+                                  (2, 9, 11, 2, 96, 3, 2, 1, 1, 1), (3, 7, 5, 1, 32, 5, 1, 2, 1, 1),
+                                  (2, 6, 6, 4, 128, 2, 1, 0, 1, 1)])
 def test_conv_residual(L, case):
     """y = relu(conv(x) + b) + R on the pipelined and the general kernel (the CONV + BINARY add fusion)"""
     B, H, W, C, Co, k, s, p, g, dil = case
