@@ -64,6 +64,31 @@ def test_i8gemm_bit_exact(L, M, N, K):
     assert np.array_equal(host(Y), want_y)
 
 
+@pytest.mark.parametrize("M", [1, 16, 256, 4096])
+def test_i8gemm_standalone_config(L, M):
+    """The standalone int8 GEMM workload, K = N = 4096 at every benchmarked M, through the default dispatch (the
+    skinny kernel at M <= 16, the 64x64 ring at M = 256, the three-stage 256x256 kernel at M = 4096): the config's
+    inputs (A, W uniform int8 in [-127, 127], scales U[0.001, 0.01], bias N(0, 0.1), seed 12345), ReLU epilogue;
+    int32 accumulators and outputs bit-exact against the oracle (reference include/kernix_model.h:143-178)."""
+    from kernix_amd import configs
+
+    A, W, sa, sw, bias = configs.i8gemm_inputs(M)
+    N, K = W.shape
+    want_y, want_acc = knx_ref.i8gemm(A, W, sa, sw, bias, act_id=0, threads=16)
+    dA, dW, dsa, dsw, db = dev(A), dev(W), dev(sa), dev(sw), dev(bias)
+    Y = torch.full((M, N), 7.0, dtype=torch.float32, device="cuda")
+    acc = torch.zeros((M, N), dtype=torch.int32, device="cuda")
+    # accumulators and outputs together, then the output-only path the benchmark times
+    hipabi.check(L.knx_hip_i8gemm(M, N, K, ptr(dA), K, ptr(dsa), ptr(dW), K, ptr(dsw), ptr(db), 0, 0.0, 0,
+                                  ptr(Y), N, ptr(acc), N, hipabi.stream()))
+    assert np.array_equal(host(acc), want_acc)
+    assert np.array_equal(host(Y), want_y)
+    Y.fill_(7.0)
+    hipabi.check(L.knx_hip_i8gemm(M, N, K, ptr(dA), K, ptr(dsa), ptr(dW), K, ptr(dsw), ptr(db), 0, 0.0, 0,
+                                  ptr(Y), N, None, 0, hipabi.stream()))
+    assert np.array_equal(host(Y), want_y)
+
+
 I8_VARIANTS = ["default", "pp", "k128", "k128w8", "k128w8t", "k128m", "k128w8ta3", "k128ma3", "k128w8ta3e", "k128w16", "ring64s4", "ring64s8k2",
                "pipe256", "pipe256w8", "pipe128", "pipe64", "tile64"]
 # tiles moved back at the M/N edges, half k-tiles (K % 128 == 64), N % 4 != 0, one whole 256x256 tile, 2..4 k-tiles
