@@ -105,6 +105,17 @@ KNX_API int knx_hip_qlinear(const float* x, int ldx, int rows, int k, int kp, in
                             int ldw, int n, const float* sw, const float* bias, int act, float alpha, int accumulate,
                             const float* R, int ldr, float* Y, int ldy, void* stream);
 
+/* knx_hip_qlinear without caller scratch and without allocating: no counterpart in the reference; for callers that
+ * cannot allocate device memory (code under HIP graph capture, fixed serving loops, harnesses that forbid hipMalloc).
+ * The int8 rows and row scales go to a device array owned by the library (one per GPU, KNX_QLINEAR_NOALLOC_BYTES,
+ * held until the process ends); a call needs ⌈4·rows/256⌉·256 + rows·kp bytes of it and is rejected (KNX_EINVAL)
+ * beyond that.  Same kernels, same bits as knx_hip_qlinear.  Every call on one GPU shares the array: calls that
+ * overlap on one GPU (different streams or threads) race, so the caller orders them. */
+#define KNX_QLINEAR_NOALLOC_BYTES ((size_t)32 << 20)
+KNX_API int knx_hip_qlinear_noalloc(const float* x, int ldx, int rows, int k, int kp, const int8_t* W, int ldw, int n,
+                                    const float* sw, const float* bias, int act, float alpha, int accumulate,
+                                    const float* R, int ldr, float* Y, int ldy, void* stream);
+
 /* dst (K×N row-major fp32) = (float)q[n][k] · scale[n]; q is N×K int8 with row stride ldq bytes. */
 KNX_API int knx_hip_dequant(const int8_t* q, int ldq, const float* scale, int K, int N, float* dst, void* stream);
 /* dst (N×K row-major fp32, the layout of the fp32 weights used with knx_hip_sgemm_nt_ep) = (float)q[n][k] · scale[n]. */

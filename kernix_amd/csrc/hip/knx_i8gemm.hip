@@ -19,6 +19,7 @@
 #include <string.h>
 
 #include <string>
+#include <mutex>
 #include <type_traits>
 
 #include "knx_pipe.hpp"
@@ -1605,4 +1606,73 @@ extern "C" int knx_hip_dequant(const int8_t* q, int ldq, const float* scale, int
     hipLaunchKernelGGL(dequant_kernel, dim3((K + 31) / 32, (N + 31) / 32), dim3(256), 0, knx::as_stream(stream), q, ldq,
                        scale, K, N, dst);
     return knx::check_launch(name);
+}
+
+// ---------------------------------------------------------------------------------------------------------------------
+// knx_hip_qlinear_noalloc: knx_hip_qlinear with its int8 rows and row scales in a library-owned device array instead
+// of caller scratch, for callers that cannot allocate (code under stream capture, fixed serving loops).  The array
+// is file-scope device memory, one copy per GPU, held until the process ends.  Layout: the row scales (rows floats,
+// rounded up to 256 bytes) at offset 0, then the int8 rows (rows × kp bytes).  Every byte a call reads is written
+// by the same call first (the quantizer writes every scale and every column of [0, kp) of every row), so nothing
+// needs clearing between calls.  Calls that overlap on one GPU (two streams, or two threads) share the array and
+// race: the caller orders them.
+constexpr size_t kNoAllocScratchBytes = KNX_QLINEAR_NOALLOC_BYTES;
+static_assert(kNoAllocScratchBytes % 256 == 0, "scratch size");
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+unsigned char* g_scratch_ptr[kMaxDevices];  // device address of `scratch` per device, resolved once
+}  // namespace
+
+// The device address of `scratch` on the current device (resolved on this device's first call), or nullptr with
+// the error recorded.
+static unsigned char* noalloc_scratch(const char* name)
+{
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        knx::fail(KNX_EHIP, "%s: no current device", name);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr) {
+            knx::fail(KNX_EHIP, "%s: hipGetSymbolAddress(scratch): %s", name, hipGetErrorString(e));
+            return nullptr;
+        }
+        g_scratch_ptr[dev] = static_cast<unsigned char*>(p);
+    }
+    return g_scratch_ptr[dev];
+}
+
+// bytes of scratch a call with `rows` rows of kp int8 values uses (scales first, then the rows)
+static size_t noalloc_bytes(int rows, int kp)
+{
+    return ((size_t)rows * sizeof(float) + 255) / 256 * 256 + (size_t)rows * (size_t)kp;
+}
+
+extern "C" int knx_hip_qlinear_noalloc(const float* x, int ldx, int rows, int k, int kp, const int8_t* W, int ldw, int n,
+                                       const float* sw, const float* bias, int act, float alpha, int accumulate,
+                                       const float* R, int ldr, float* Y, int ldy, void* stream)
+{
+    const char* name = "knx_hip_qlinear_noalloc";
+    KNX_ENTRY(name);
+    KNX_REQUIRE(rows >= 0 && k >= 1 && kp >= k && kp % 64 == 0 && kp <= 131072, name);
+    if (noalloc_bytes(rows, kp) > kNoAllocScratchBytes)
+        return knx::fail(KNX_EINVAL, "%s: %d rows of %d int8 values need %zu bytes of scratch, the limit is %zu", name,
+                         rows, kp, noalloc_bytes(rows, kp), kNoAllocScratchBytes);
+    int8_t* xq = nullptr;
+    float* sx = nullptr;
+    if (rows > 0) {
+        unsigned char* base = noalloc_scratch(name);
+        if (base == nullptr) return KNX_EHIP;
+        sx = reinterpret_cast<float*>(base);
+        xq = reinterpret_cast<int8_t*>(base + ((size_t)rows * sizeof(float) + 255) / 256 * 256);
+    }
+    // the same kernels and arguments as knx_hip_qlinear (rows <= 4 quantize inside the GEMM and use no scratch)
+    return knx_hip_qlinear(x, ldx, rows, k, kp, xq, sx, W, ldw, n, sw, bias, act, alpha, accumulate, R, ldr, Y, ldy,
+                           stream);
 }

@@ -33,6 +33,7 @@ SIGS = {
     "knx_hip_sgemm_nt_ep_res": ([I, I, I, P, I, P, I, P, I, F, P, I, P, I, P], I),
     "knx_hip_i8gemm_res": ([I, I, I, P, I, P, P, I, P, P, I, F, P, I, P, I, P], I),
     "knx_hip_qlinear": ([P, I, I, I, I, P, P, P, I, I, P, P, I, F, I, P, I, P, I, P], I),
+    "knx_hip_qlinear_noalloc": ([P, I, I, I, I, P, I, I, P, P, I, F, I, P, I, P, I, P], I),
     "knx_hip_layernorm": ([P, P, I, I, P, P, F, P], I),
     "knx_hip_layernorm_quantize": ([P, I, I, P, P, F, I, P, P, P], I),
     "knx_hip_softmax": ([P, P, I, I, P], I),
