@@ -73,6 +73,7 @@ typedef struct kernix_qweight {
     int kp, np;
     int8_t* q;
     float* scale;
+    struct knx_qdev* dev;      /* device copy made by the first kernix_qmatmul, released by kernix_qweight_free */
 } kernix_qweight;
 
 /* One graph value (edge). Stored as (batch·r) × c. */
@@ -156,6 +157,9 @@ typedef struct kernix_model {
     int n_st;
     size_t* st_cap;            /* floats per sample of each storage buffer */
     float_tensor** st;         /* device storage buffers */
+    size_t* st_off;            /* per-sample float offset of each storage buffer in the value region (buffers whose
+                                  values are never live at the same step may overlap) */
+    size_t st_span;            /* floats per sample of the value region */
     int in_nd, in_shape[KERNIX_MAX_DIMS];
     int out_nd, out_shape[KERNIX_MAX_DIMS];
     int layout;                /* 0 channels-last input, 1 PyTorch channels-first (the binding moves the axis) */

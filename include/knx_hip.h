@@ -72,6 +72,12 @@ KNX_API int knx_hip_memcpy_d2d(void* dst, const void* src, size_t bytes, void* s
 KNX_API int knx_hip_stream_create(void** stream);
 KNX_API int knx_hip_stream_destroy(void* stream);
 KNX_API int knx_hip_stream_sync(void* stream);
+/* Events (hipEvent_t as void*, created without timing): the runtime orders forwards issued on different streams. */
+KNX_API int knx_hip_event_create(void** event);
+KNX_API int knx_hip_event_destroy(void* event);
+KNX_API int knx_hip_event_record(void* event, void* stream);
+KNX_API int knx_hip_stream_wait_event(void* stream, void* event); /* later work on stream waits for the event */
+KNX_API int knx_hip_event_sync(void* event);                      /* the host waits for the event */
 
 /* ---- int8 path ---- */
 /* Per row r < rows of x (row stride ldx floats, k values): m = max|x|; a NaN or ±inf makes sx[r] = NaN (the whole

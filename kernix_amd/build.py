@@ -20,7 +20,7 @@ LIB = os.path.join(PKG, "libkernix.so")
 INC = os.path.join(ROOT, "include")
 
 HIP_SOURCES = ["knx_runtime", "knx_i8gemm", "knx_sgemm", "knx_conv", "knx_rows", "knx_attn"]
-C_SOURCES = ["knx_load", "knx_forward", "knx_capi"]
+C_SOURCES = ["knx_decode", "knx_graph", "knx_forward", "knx_capi"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 HIP_FLAGS = [

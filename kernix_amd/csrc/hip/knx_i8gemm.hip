@@ -254,40 +254,44 @@ __device__ __forceinline__ void store_rows(const I8Args& p, const int* stg, cons
         // alias, and a load after a store waits for it: one memory round trip per row).  Loading first is right when
         // R is Y, since each element is read before its own store and no other store touches it.  Unrolled, so the
         // loads sit in registers; the per-row code is a few instructions.
-        constexpr int MAXJ = 8;  // rpi ≥ 2
-        v4f_t rres[MAXJ];
+        // A lane owns rows rq, rq + rpi, ... < 16 of the round: at most MAXJ of them per pass (one pass when rpi ≥ 2,
+        // two when rpi == 1), so every row is covered whatever the tile's lanes per row.
+        constexpr int MAXJ = 8;
         const bool rvec = nb >= nlo && (nb & 3) == 0 && (p.ldr & 3) == 0 && ((uintptr_t)p.R & 15) == 0;
+        for (int j0 = 0; rq + j0 * rpi < 16; j0 += MAXJ) {
+            v4f_t rres[MAXJ];
 #pragma unroll
-        for (int j = 0; j < MAXJ; ++j) {
-            const int rr = rq + j * rpi, m = m0 + mt0 + rr;
-            rres[j] = v4f_t{0.0f, 0.0f, 0.0f, 0.0f};
-            if (rr >= 16 || m < mlo || m >= p.M) continue;
-            const float* rp = p.R + (size_t)m * p.ldr + nb;
-            if (rvec) {
-                rres[j] = *reinterpret_cast<const v4f_t*>(rp);
-            } else {
+            for (int j = 0; j < MAXJ; ++j) {
+                const int rr = rq + (j0 + j) * rpi, m = m0 + mt0 + rr;
+                rres[j] = v4f_t{0.0f, 0.0f, 0.0f, 0.0f};
+                if (rr >= 16 || m < mlo || m >= p.M) continue;
+                const float* rp = p.R + (size_t)m * p.ldr + nb;
+                if (rvec) {
+                    rres[j] = *reinterpret_cast<const v4f_t*>(rp);
+                } else {
 #pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    if (nb + q >= nlo && nb + q < p.N) rres[j][q] = rp[q];
+                    for (int q = 0; q < 4; ++q)
+                        if (nb + q >= nlo && nb + q < p.N) rres[j][q] = rp[q];
+                }
             }
-        }
 #pragma unroll
-        for (int j = 0; j < MAXJ; ++j) {
-            const int rr = rq + j * rpi;
-            if (rr >= 16) break;
-            const int mt = mt0 + rr, m = m0 + mt;
-            if (m < mlo || m >= p.M) continue;
-            const v4i a = *reinterpret_cast<const v4i*>(&stg[rr * srow + cq]);
-            const float sx = row_scale[mt];
-            v4f_t r;
+            for (int j = 0; j < MAXJ; ++j) {
+                const int rr = rq + (j0 + j) * rpi;
+                if (rr >= 16) break;
+                const int mt = mt0 + rr, m = m0 + mt;
+                if (m < mlo || m >= p.M) continue;
+                const v4i a = *reinterpret_cast<const v4i*>(&stg[rr * srow + cq]);
+                const float sx = row_scale[mt];
+                v4f_t r;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                float v = (float)a[q] * sx;  // ((float)acc · sx) · scale + bias, each step rounded
-                v = v * swv[q];
-                if (p.bias) v = v + bv[q];
-                r[q] = (ACT == 0 ? (v >= 0.0f ? v : 0.0f) : ACT == 1 ? knx_gelu(v) : v) + rres[j][q];
+                for (int q = 0; q < 4; ++q) {
+                    float v = (float)a[q] * sx;  // ((float)acc · sx) · scale + bias, each step rounded
+                    v = v * swv[q];
+                    if (p.bias) v = v + bv[q];
+                    r[q] = (ACT == 0 ? (v >= 0.0f ? v : 0.0f) : ACT == 1 ? knx_gelu(v) : v) + rres[j][q];
+                }
+                __builtin_nontemporal_store(r, reinterpret_cast<v4f_t*>(p.Y + (size_t)m * p.ldy + nb));
             }
-            __builtin_nontemporal_store(r, reinterpret_cast<v4f_t*>(p.Y + (size_t)m * p.ldy + nb));
         }
         return;
     }

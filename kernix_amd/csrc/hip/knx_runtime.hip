@@ -177,3 +177,44 @@ extern "C" int knx_hip_stream_sync(void* stream)
     const hipError_t e = hipStreamSynchronize(knx::as_stream(stream));
     return e == hipSuccess ? KNX_OK : knx::fail(KNX_EHIP, "knx_hip_stream_sync: %s", hipGetErrorString(e));
 }
+
+extern "C" int knx_hip_event_create(void** event)
+{
+    KNX_ENTRY("knx_hip_event_create");
+    KNX_REQUIRE(event != nullptr, "knx_hip_event_create");
+    hipEvent_t e = nullptr;
+    const hipError_t rc = hipEventCreateWithFlags(&e, hipEventDisableTiming);
+    if (rc != hipSuccess) return knx::fail(KNX_EHIP, "knx_hip_event_create: %s", hipGetErrorString(rc));
+    *event = e;
+    return KNX_OK;
+}
+
+extern "C" int knx_hip_event_destroy(void* event)
+{
+    if (event == nullptr) return KNX_OK;
+    const hipError_t rc = hipEventDestroy(static_cast<hipEvent_t>(event));
+    return rc == hipSuccess ? KNX_OK : knx::fail(KNX_EHIP, "knx_hip_event_destroy: %s", hipGetErrorString(rc));
+}
+
+extern "C" int knx_hip_event_record(void* event, void* stream)
+{
+    KNX_ENTRY("knx_hip_event_record");
+    KNX_REQUIRE(event != nullptr, "knx_hip_event_record");
+    const hipError_t rc = hipEventRecord(static_cast<hipEvent_t>(event), knx::as_stream(stream));
+    return rc == hipSuccess ? KNX_OK : knx::fail(KNX_EHIP, "knx_hip_event_record: %s", hipGetErrorString(rc));
+}
+
+extern "C" int knx_hip_stream_wait_event(void* stream, void* event)
+{
+    KNX_ENTRY("knx_hip_stream_wait_event");
+    KNX_REQUIRE(event != nullptr, "knx_hip_stream_wait_event");
+    const hipError_t rc = hipStreamWaitEvent(knx::as_stream(stream), static_cast<hipEvent_t>(event), 0);
+    return rc == hipSuccess ? KNX_OK : knx::fail(KNX_EHIP, "knx_hip_stream_wait_event: %s", hipGetErrorString(rc));
+}
+
+extern "C" int knx_hip_event_sync(void* event)
+{
+    if (event == nullptr) return KNX_OK;
+    const hipError_t rc = hipEventSynchronize(static_cast<hipEvent_t>(event));
+    return rc == hipSuccess ? KNX_OK : knx::fail(KNX_EHIP, "knx_hip_event_sync: %s", hipGetErrorString(rc));
+}

@@ -11,6 +11,7 @@
  */
 #include <limits.h>
 #include <math.h>
+#include <pthread.h>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
@@ -182,7 +183,9 @@ static int ensure_device(kernix_model* m)
     if (m->dev == NULL) {
         m->dev = calloc(1, sizeof *m->dev);
         if (m->dev == NULL) return -1;
-        if (hip_ok(knx_hip_stream_create(&m->dev->stream), "stream creation") != 0) return -1;
+        if (hip_ok(knx_hip_stream_create(&m->dev->stream), "stream creation") != 0 ||
+            hip_ok(knx_hip_event_create(&m->dev->done), "event creation") != 0)
+            return -1;
     }
     for (int i = 0; i < m->n_steps; i++) {
         if (m->steps[i].dev != NULL) continue;
@@ -240,8 +243,19 @@ static int int8_rows(const kernix_model* m, size_t rows)
  * reference allocates them only when the chunk has more than KERNIX_INT8_MAX_ROWS rows, and so does this). */
 static int ws_walk(kernix_model* m, size_t B, ws_ctx* c)
 {
-    for (int k = 0; k < m->n_st; k++)
-        if (ws_tensor(c, &m->st[k], B, m->st_cap[k]) != 0) return -1;
+    /* the value region: B × st_span floats, storage buffer k at float offset st_off[k]·B */
+    if (m->st_span > SIZE_MAX / 8 / (B ? B : 1)) return -1;
+    c->floats += B * m->st_span;
+    if (c->mode == WS_SIZE || c->mode == WS_ALLOC) {
+        float* region = ws_take(c, B * m->st_span * sizeof(float));
+        for (int k = 0; c->mode == WS_ALLOC && k < m->n_st; k++) {
+            if ((m->st[k] = malloc(sizeof(float_tensor))) == NULL) return -1;
+            *m->st[k] = (float_tensor){ (int)B, (int)m->st_cap[k], region + m->st_off[k] * B };
+        }
+    } else if (c->mode == WS_VIEW) {
+        for (int k = 0; k < m->n_st; k++)
+            if (m->st[k]) m->st[k]->row = (int)B;
+    }
     for (int i = 0; i < m->n_steps; i++) {
         kernix_step* s = &m->steps[i];
         const kernix_val* vi = &m->vals[s->inp[0]];
@@ -355,6 +369,7 @@ void knx_model_release_device_ws(kernix_model* m)
     m->batch = -1;
     if (m->dev != NULL) {
         if (m->dev->stream) knx_hip_stream_sync(m->dev->stream);
+        if (m->dev->done_recorded) knx_hip_event_sync(m->dev->done); /* a forward on a caller's stream */
         knx_hip_free(m->dev->arena);
         m->dev->arena = NULL;
         m->dev->arena_bytes = 0;
@@ -375,6 +390,7 @@ void knx_model_release_device_all(kernix_model* m)
     for (int i = 0; m->steps != NULL && i < m->n_steps; i++) free_dstep(&m->steps[i]);
     if (m->dev != NULL) {
         knx_hip_stream_destroy(m->dev->stream);
+        knx_hip_event_destroy(m->dev->done);
         free(m->dev);
         m->dev = NULL;
     }
@@ -472,7 +488,7 @@ static int run_rnn_dir(const kernix_model* m, kernix_step* s, int dir, const flo
     float* c = kind == KERNIX_OP_LSTM ? s->tmp[2]->tensor : NULL;
     float* h = s->tmp[3]->tensor;
     float* hu = s->tmp[4]->tensor;
-    /* the backward direction's int8 scratch sits right after the forward one's; both hold xq_rows rows */
+    /* both directions use the step's one int8 scratch (xq_rows rows): they run one after the other on one stream */
     int8_t* xq = d->xq;
     float* sx = d->sx;
     if (hip_ok(knx_hip_sgemm_ep(x->row, gu, s->in, x->tensor, s->in, W, gu, bias, -1, 0.0f, zx, gu, st), "RNN input projection")) return -1;
@@ -688,7 +704,7 @@ static int fusable_add(const kernix_model* m, int i)
     if (vo->last != i + 1 || m->out_v == own) return -1;
     if (vr->r != vo->r || vr->c != vo->c || vy->r != vo->r || vy->c != vo->c) return -1;
     for (int k = 0; k < s->n_in; k++)
-        if (m->vals[s->inp[k]].st == vy->st) return -1;
+        if (knx_storage_overlaps(m, s->inp[k], i + 2)) return -1;
     return other;
 }
 
@@ -769,118 +785,220 @@ static int run_chunk(kernix_model* m, const float* in, int B, void* st)
     return 0;
 }
 
-/* Samples per chunk under ws_limit (reference include/kernix_model.h:2036-2043). */
-static int chunk_samples(const kernix_model* m, int samples)
+/* ---------------------------------------------------------------- ordering between forwards
+ * Every forward (host or device buffers, on the model's stream or a caller's) uses the model's one workspace, so
+ * forwards run one after the other on the device, in the order they were called.  The model remembers the stream of
+ * the last forward.  A forward on the same stream is ordered by the stream itself.  A forward on another stream first
+ * makes its stream wait for the event `done`: recorded right after every forward that ran on a caller's stream, and,
+ * when the previous forward ran on the model's own stream, recorded on that stream at the switch.  Freeing the
+ * workspace waits for the model's stream and for `done` on the host. */
+static int order_after_previous(kernix_model* m, void* st)
 {
-    int chunk = samples;
-    if (m->ws_limit > 0 && m->ws_per_sample > 0) {
-        const size_t fixed = m->ws_fixed * sizeof(float), avail = m->ws_limit > fixed ? m->ws_limit - fixed : 0;
-        size_t c = avail / (m->ws_per_sample * sizeof(float));
-        if (c < 1) c = 1;
-        if (c < (size_t)samples) chunk = (int)c;
+    struct knx_dmodel* d = m->dev;
+    if (!d->have_last || d->last_stream == st) return 0;
+    if (!d->done_recorded) { /* the previous forward ran on the model's stream (which is still alive: it is ours) */
+        if (hip_ok(knx_hip_event_record(d->done, d->last_stream), "event record")) return -1;
+        d->done_recorded = 1;
     }
-    return chunk;
+    return hip_ok(knx_hip_stream_wait_event(st, d->done), "stream wait");
 }
 
-static int ensure_host_out(kernix_model* m, int B)
+/* after the last operation of a forward (or of the workspace set-up) enqueued on st */
+static int mark_done(kernix_model* m, void* st)
 {
-    const size_t need = (size_t)B * (size_t)m->out_dim;
-    if (m->dev->h_out != NULL && m->dev->h_out_floats >= need) return 0;
-    knx_hip_host_free(m->dev->h_out);
-    m->dev->h_out = NULL;
-    m->dev->h_out_floats = 0;
-    void* p = NULL;
-    if (hip_ok(knx_hip_host_malloc(&p, need * sizeof(float)), "pinned output allocation")) return -1;
-    m->dev->h_out = p;
-    m->dev->h_out_floats = need;
+    struct knx_dmodel* d = m->dev;
+    d->have_last = 1;
+    d->last_stream = st;
+    d->done_recorded = 0;
+    if (st == d->stream) return 0; /* recorded lazily, when another stream comes next */
+    if (hip_ok(knx_hip_event_record(d->done, st), "event record")) return -1;
+    d->done_recorded = 1;
     return 0;
 }
 
-static int ensure_out_all(kernix_model* m, int samples)
+/* ---------------------------------------------------------------- forward
+ * A batch of `samples` runs as consecutive pieces of at most `per` samples each, `per` the most the workspace limit
+ * holds (ws_fixed + per·ws_per_sample floats ≤ ws_limit bytes; at least one sample; the whole batch when there is no
+ * limit).  The workspace is sized for `per` samples and the last, shorter piece uses a prefix of it — the reference's
+ * chunking rule (include/kernix_model.h:2036-2062), so m->batch reads the same. */
+static int piece_samples(const kernix_model* m, int samples)
 {
-    if (m->out_all != NULL && m->out_all->row == samples) return 0;
+    if (m->ws_limit == 0 || m->ws_per_sample == 0) return samples;
+    const size_t fixed = m->ws_fixed * sizeof(float), each = m->ws_per_sample * sizeof(float);
+    const size_t fit = m->ws_limit > fixed ? (m->ws_limit - fixed) / each : 0;
+    if (fit >= (size_t)samples) return samples;
+    return fit ? (int)fit : 1;
+}
+
+/* Device state, weights and a workspace for pieces of `per` samples (reallocated only when `per` changes); the
+ * workspace's own setup (dequantized copies) is ordered before the next forward through `done`. */
+static int prepare(kernix_model* m, int per)
+{
+    if (ensure_device(m) != 0) return -1;
+    const int rows = per * m->seq_len;
+    if (rows == m->batch) return 0;
+    if (alloc_ws(m, rows) != 0) return -1;
+    return mark_done(m, m->dev->stream);
+}
+
+/* One piece: samples [s0, s0 + n) of the batch, whose input rows start at x (device memory); the output is copied
+ * to dst (device or pinned host memory, `to_host` says which, holding the whole batch's output) at the piece's rows. */
+static int run_piece(kernix_model* m, const float* x, int s0, int n, float* dst, int to_host, void* st)
+{
+    const size_t out_row = (size_t)m->out_dim;
+    ws_view(m, n * m->seq_len);
+    if (run_chunk(m, x, n, st) != 0) return -1;
+    const float* y = m->views[m->out_v].tensor;
+    const size_t bytes = (size_t)n * out_row * sizeof(float);
+    float* at = dst + (size_t)s0 * out_row;
+    return hip_ok(to_host ? knx_hip_memcpy_d2h(at, y, bytes, st) : knx_hip_memcpy_d2d(at, y, bytes, st), "output copy");
+}
+
+/* Pinned host memory for `samples` outputs.  An unchunked forward returns a view of h_out (kept, grown when a
+ * larger batch needs more); a chunked one returns out_all, a host tensor of exactly the batch's rows. */
+static float* host_output(kernix_model* m, int samples, int chunked)
+{
+    const size_t floats = (size_t)samples * (size_t)m->out_dim;
+    void* p = NULL;
+    if (!chunked) {
+        if (m->dev->h_out == NULL || m->dev->h_out_floats < floats) {
+            knx_hip_host_free(m->dev->h_out);
+            m->dev->h_out = NULL;
+            m->dev->h_out_floats = 0;
+            if (hip_ok(knx_hip_host_malloc(&p, floats * sizeof(float)), "pinned output allocation")) return NULL;
+            m->dev->h_out = p;
+            m->dev->h_out_floats = floats;
+        }
+        return m->dev->h_out;
+    }
+    if (m->out_all != NULL && m->out_all->row == samples) return m->out_all->tensor;
     free_out_all(m);
     float_tensor* t = malloc(sizeof *t);
-    void* p = NULL;
-    if (t == NULL || hip_ok(knx_hip_host_malloc(&p, (size_t)samples * (size_t)m->out_dim * sizeof(float)), "pinned output allocation")) {
+    if (t == NULL || hip_ok(knx_hip_host_malloc(&p, floats * sizeof(float)), "pinned output allocation")) {
         free(t);
-        return -1;
+        return NULL;
     }
     *t = (float_tensor){ samples, m->out_dim, p };
     m->out_all = t;
     m->dev->out_all_pinned = 1;
-    return 0;
+    return p;
 }
 
 const float_tensor* kernix_model_forward(kernix_model* m, const float_tensor* x)
 {
-    if (m == NULL || x == NULL || x->tensor == NULL || x->row < 0 || x->col != m->in_dim || x->row % m->seq_len != 0) return NULL;
-    int own = m->out_all != NULL && x->tensor == m->out_all->tensor;
-    own |= m->dev != NULL && m->dev->h_out != NULL && x->tensor == m->dev->h_out;
-    if (own) {
+    if (m == NULL || x == NULL || x->tensor == NULL || x->row < 0 || x->col != m->in_dim || x->row % m->seq_len != 0)
+        return NULL;
+    const int mine = (m->out_all != NULL && x->tensor == m->out_all->tensor) ||
+                     (m->dev != NULL && m->dev->h_out != NULL && x->tensor == m->dev->h_out);
+    if (mine) {
         KNX_LOG("forward: this model's output buffer cannot be its own input (pass a copy)\n");
         return NULL;
     }
-    if (ensure_device(m) != 0) return NULL;
-    void* st = m->dev->stream;
     const int samples = x->row / m->seq_len;
-    const int chunk = chunk_samples(m, samples);
-    const int crow = chunk * m->seq_len;
-    if (crow != m->batch && alloc_ws(m, crow) != 0) return NULL;
-    const size_t in_per = (size_t)m->seq_len * (size_t)m->in_dim;
-
-    if (chunk == samples) {
-        ws_view(m, crow);
-        if (ensure_host_out(m, samples) != 0) return NULL;
-        if (samples > 0) {
-            if (hip_ok(knx_hip_memcpy_h2d(m->dev->d_in, x->tensor, (size_t)samples * in_per * sizeof(float), st), "input copy") ||
-                run_chunk(m, m->dev->d_in, samples, st) != 0 ||
-                hip_ok(knx_hip_memcpy_d2h(m->dev->h_out, m->views[m->out_v].tensor, (size_t)samples * m->out_dim * sizeof(float), st), "output copy") ||
-                hip_ok(knx_hip_stream_sync(st), "forward"))
-                return NULL;
-        }
-        m->out_view = (float_tensor){ samples, m->out_dim, m->dev->h_out };
-        return &m->out_view;
-    }
-    if (ensure_out_all(m, samples) != 0) return NULL;
-    for (int s0 = 0; s0 < samples; s0 += chunk) {
-        const int n = samples - s0 < chunk ? samples - s0 : chunk;
-        ws_view(m, n * m->seq_len);
-        if (hip_ok(knx_hip_memcpy_h2d(m->dev->d_in, x->tensor + (size_t)s0 * in_per, (size_t)n * in_per * sizeof(float), st), "input copy") ||
-            run_chunk(m, m->dev->d_in, n, st) != 0 ||
-            hip_ok(knx_hip_memcpy_d2h(m->out_all->tensor + (size_t)s0 * m->out_dim, m->views[m->out_v].tensor,
-                                      (size_t)n * m->out_dim * sizeof(float), st), "output copy"))
+    const int per = piece_samples(m, samples);
+    if (prepare(m, per) != 0) return NULL;
+    void* st = m->dev->stream;
+    const int chunked = per < samples;
+    float* out = host_output(m, samples, chunked);
+    if (out == NULL || order_after_previous(m, st) != 0) return NULL;
+    const size_t in_row = (size_t)m->seq_len * (size_t)m->in_dim;
+    for (int s0 = 0; s0 < samples; s0 += per) {
+        const int n = samples - s0 < per ? samples - s0 : per;
+        /* the staged input holds one piece: piece s0 is copied to its start */
+        if (hip_ok(knx_hip_memcpy_h2d(m->dev->d_in, x->tensor + (size_t)s0 * in_row, (size_t)n * in_row * sizeof(float), st),
+                   "input copy") ||
+            run_piece(m, m->dev->d_in, s0, n, out, 1, st) != 0)
             return NULL;
     }
-    if (hip_ok(knx_hip_stream_sync(st), "forward")) return NULL;
-    return m->out_all;
+    if (mark_done(m, st) != 0 || hip_ok(knx_hip_stream_sync(st), "forward")) return NULL;
+    if (chunked) return m->out_all;
+    m->out_view = (float_tensor){ samples, m->out_dim, out };
+    return &m->out_view;
 }
 
 int kernix_model_forward_device(kernix_model* m, const float* d_x, int rows, float* d_out, void* stream)
 {
     if (m == NULL || d_x == NULL || d_out == NULL || rows < 0 || rows % m->seq_len != 0) return -1;
-    if (ensure_device(m) != 0) return -1;
-    void* st = stream ? stream : m->dev->stream;
     const int samples = rows / m->seq_len;
-    const int chunk = chunk_samples(m, samples);
-    const int crow = chunk * m->seq_len;
-    if (crow != m->batch) {
-        if (stream) knx_hip_stream_sync(stream); /* the old workspace may still be in use on the caller's stream */
-        if (alloc_ws(m, crow) != 0) return -1;
-        if (hip_ok(knx_hip_stream_sync(m->dev->stream), "dequantization")) return -1;
+    const int per = piece_samples(m, samples);
+    if (prepare(m, per) != 0) return -1;
+    void* st = stream ? stream : m->dev->stream;
+    if (order_after_previous(m, st) != 0) return -1;
+    const size_t in_row = (size_t)m->seq_len * (size_t)m->in_dim;
+    for (int s0 = 0; s0 < samples; s0 += per) {
+        const int n = samples - s0 < per ? samples - s0 : per;
+        if (run_piece(m, d_x + (size_t)s0 * in_row, s0, n, d_out, 0, st) != 0) return -1;
     }
-    const size_t in_per = (size_t)m->seq_len * (size_t)m->in_dim;
-    for (int s0 = 0; s0 < samples; s0 += chunk) {
-        const int n = samples - s0 < chunk ? samples - s0 : chunk;
-        ws_view(m, n * m->seq_len);
-        if (run_chunk(m, d_x + (size_t)s0 * in_per, n, st) != 0 ||
-            hip_ok(knx_hip_memcpy_d2d(d_out + (size_t)s0 * m->out_dim, m->views[m->out_v].tensor, (size_t)n * m->out_dim * sizeof(float), st), "output copy"))
-            return -1;
-    }
-    return 0;
+    return mark_done(m, st);
 }
 
-/* ---------------------------------------------------------------- kernel-level int8 contract */
+/* ---------------------------------------------------------------- kernel-level int8 contract
+ * kernix_qmatmul on host pointers.  The packed weight is uploaded once per kernix_qweight (kept in w->dev until
+ * kernix_qweight_free); the input, output, bias and int8 scratch live in one growable device buffer shared by all
+ * calls (kept until the process ends), used on one stream under a lock, so a call allocates only when it needs more
+ * scratch than any call before it. */
+struct knx_qdev {
+    int8_t* q;
+    float* scale;
+};
+
+static struct {
+    pthread_mutex_t lock;
+    void* stream;
+    char* buf;
+    size_t bytes;
+} g_qm = { PTHREAD_MUTEX_INITIALIZER, NULL, NULL, 0 };
+
+void knx_qweight_release_device(kernix_qweight* w)
+{
+    if (w == NULL || w->dev == NULL) return;
+    pthread_mutex_lock(&g_qm.lock);
+    if (g_qm.stream) knx_hip_stream_sync(g_qm.stream); /* a call may still read it */
+    knx_hip_free(w->dev->q);
+    knx_hip_free(w->dev->scale);
+    pthread_mutex_unlock(&g_qm.lock);
+    free(w->dev);
+    w->dev = NULL;
+}
+
+static size_t qm_round(size_t b) { return (b + KNX_ALIGN - 1) / KNX_ALIGN * KNX_ALIGN; }
+
+static int qm_call(const float* x, int rows, kernix_qweight* w, const float* bias, int accumulate, float* y)
+{
+    const size_t k = (size_t)w->k, n = (size_t)w->n, kp = (size_t)w->kp, R = (size_t)rows;
+    if (g_qm.stream == NULL && knx_hip_stream_create(&g_qm.stream) != KNX_OK) return -1;
+    if (w->dev == NULL) {
+        struct knx_qdev* d = calloc(1, sizeof *d);
+        if (d == NULL) return -1;
+        w->dev = d;
+        if (up((void**)&d->q, w->q, (size_t)w->np * kp, g_qm.stream) || up_f(&d->scale, w->scale, (size_t)w->np, g_qm.stream))
+            return -1;
+    }
+    const size_t sz_x = qm_round(R * k * 4), sz_y = qm_round(R * n * 4), sz_b = qm_round(n * 4), sz_q = qm_round(R * kp);
+    const size_t need = sz_x + sz_y + sz_b + sz_q + qm_round(R * 4);
+    if (need > g_qm.bytes) {
+        knx_hip_stream_sync(g_qm.stream);
+        knx_hip_free(g_qm.buf);
+        g_qm.buf = NULL;
+        g_qm.bytes = 0;
+        if (knx_hip_malloc((void**)&g_qm.buf, need) != KNX_OK) return -1;
+        g_qm.bytes = need;
+    }
+    float* dx = (float*)g_qm.buf;
+    float* dy = (float*)(g_qm.buf + sz_x);
+    float* db = bias ? (float*)(g_qm.buf + sz_x + sz_y) : NULL;
+    int8_t* dxq = (int8_t*)(g_qm.buf + sz_x + sz_y + sz_b);
+    float* dsx = (float*)(g_qm.buf + sz_x + sz_y + sz_b + sz_q);
+    void* st = g_qm.stream;
+    if (knx_hip_memcpy_h2d(dx, x, R * k * 4, st) || (db && knx_hip_memcpy_h2d(db, bias, n * 4, st)) ||
+        (accumulate && knx_hip_memcpy_h2d(dy, y, R * n * 4, st)))
+        return -1;
+    if (knx_hip_qlinear(dx, (int)k, rows, (int)k, (int)kp, dxq, dsx, w->dev->q, (int)kp, (int)n, w->dev->scale, db, -1,
+                        0.0f, accumulate, NULL, 0, dy, (int)n, st) != KNX_OK)
+        return -1;
+    return knx_hip_memcpy_d2h(y, dy, R * n * 4, st) == KNX_OK && knx_hip_stream_sync(st) == KNX_OK ? 0 : -1;
+}
+
 int kernix_qmatmul(const float* x, int rows, const kernix_qweight* w, const float* bias, int accumulate, float* y)
 {
     if (w == NULL || rows < 0 || (rows > 0 && (x == NULL || y == NULL))) return -1;
@@ -889,28 +1007,10 @@ int kernix_qmatmul(const float* x, int rows, const kernix_qweight* w, const floa
         KNX_LOG("KERNIX: no usable MI355X (gfx950) device: %s\n", knx_hip_last_error());
         return -1;
     }
-    const size_t k = (size_t)w->k, n = (size_t)w->n, kp = (size_t)w->kp, np = (size_t)w->np, R = (size_t)rows;
-    float *dx = NULL, *dsx = NULL, *dsc = NULL, *db = NULL, *dy = NULL;
-    int8_t *dxq = NULL, *dq = NULL;
-    void* st = NULL;
-    int rc = -1;
-    if (knx_hip_stream_create(&st) != KNX_OK || knx_hip_malloc((void**)&dx, R * k * 4) || knx_hip_malloc((void**)&dxq, R * kp) ||
-        knx_hip_malloc((void**)&dsx, R * 4) || knx_hip_malloc((void**)&dq, np * kp) || knx_hip_malloc((void**)&dsc, np * 4) ||
-        knx_hip_malloc((void**)&dy, R * n * 4) || (bias && knx_hip_malloc((void**)&db, n * 4)))
-        goto done;
-    if (knx_hip_memcpy_h2d(dx, x, R * k * 4, st) || knx_hip_memcpy_h2d(dq, w->q, np * kp, st) ||
-        knx_hip_memcpy_h2d(dsc, w->scale, np * 4, st) || (bias && knx_hip_memcpy_h2d(db, bias, n * 4, st)) ||
-        (accumulate && knx_hip_memcpy_h2d(dy, y, R * n * 4, st)))
-        goto done;
-    if (knx_hip_qlinear(dx, (int)k, rows, (int)k, (int)kp, dxq, dsx, dq, (int)kp, (int)n, dsc, db, -1, 0.0f, accumulate,
-                        NULL, 0, dy, (int)n, st) ||
-        knx_hip_memcpy_d2h(y, dy, R * n * 4, st) || knx_hip_stream_sync(st))
-        goto done;
-    rc = 0;
-done:
+    pthread_mutex_lock(&g_qm.lock);
+    /* the device copy is a cache attached to the weight: the weight's values are not changed */
+    const int rc = qm_call(x, rows, (kernix_qweight*)w, bias, accumulate, y);
+    pthread_mutex_unlock(&g_qm.lock);
     if (rc != 0) KNX_LOG("KERNIX: kernix_qmatmul failed: %s\n", knx_hip_last_error());
-    if (st) knx_hip_stream_sync(st);
-    knx_hip_free(dx); knx_hip_free(dxq); knx_hip_free(dsx); knx_hip_free(dq); knx_hip_free(dsc); knx_hip_free(db); knx_hip_free(dy);
-    knx_hip_stream_destroy(st);
     return rc;
 }

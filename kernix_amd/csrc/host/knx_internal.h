@@ -49,12 +49,33 @@ struct knx_dmodel {
     float* h_out;     /* pinned host output of an unchunked forward (batch × out_dim) */
     size_t h_out_floats;
     int out_all_pinned; /* out_all->tensor was allocated pinned */
+    void* done;         /* event marking the end of the last forward (see knx_forward.c, ordering between forwards) */
+    int done_recorded;  /* `done` has been recorded after the last forward */
+    int have_last;      /* a forward (or workspace set-up) has been enqueued */
+    void* last_stream;  /* the stream it was enqueued on */
 };
 
-/* loader (knx_load.c) */
-int knx_model_count_ws(kernix_model* m, size_t* per_sample); /* floats per sample of workspace, 0 or -1 */
+/* A decoded .knx file: its header and op records in file order (inputs, arguments, host weights). */
+typedef struct {
+    int version;                    /* 1, 2 or 3 */
+    int layout;                     /* KNX3 input layout (0 channels-last, 1 channels-first) */
+    int in_nd, in_d[KERNIX_MAX_DIMS]; /* KNX3 per-sample input shape */
+    int n_ops;
+    kernix_step* ops;
+} knx_file;
+
+/* decoder (knx_decode.c) */
+int knx_decode(const char* path, knx_file* f, const char** why); /* 0, or -1 with the reason in *why */
+void knx_file_release(knx_file* f);
+
+/* graph, shapes and storage plan (knx_graph.c) */
 size_t knx_conv_is_gemm(const kernix_step* s);
 void knx_step_host_free(kernix_step* s);
+int knx_storage_overlaps(const kernix_model* m, int a, int b); /* values a, b share storage in a chunk */
+
+/* workspace / device (knx_forward.c) */
+int knx_model_count_ws(kernix_model* m, size_t* per_sample); /* floats per sample of workspace, 0 or -1 */
+void knx_qweight_release_device(kernix_qweight* w);          /* kernix_qmatmul's cached device copy */
 
 /* workspace / device (knx_forward.c) */
 void knx_model_release_device_ws(kernix_model* m);

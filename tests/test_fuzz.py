@@ -45,7 +45,7 @@ def harness(tmp_path_factory):
     if not os.path.exists(os.path.join(LIBDIR, "libkernix.so")):
         pytest.fail("kernix_amd/libkernix.so is not built (run __graft_entry__.build())")
     out = str(tmp_path_factory.mktemp("fuzzbin") / "knx_fuzz")
-    srcs = [os.path.join(HOST, f) for f in ("knx_load.c", "knx_forward.c", "knx_capi.c")]
+    srcs = [os.path.join(HOST, f) for f in ("knx_decode.c", "knx_graph.c", "knx_forward.c", "knx_capi.c")]
     cmd = ["gcc", "-O1", "-g", "-std=c11", "-D_GNU_SOURCE", "-fsanitize=address,undefined", "-fno-omit-frame-pointer",
            "-I", os.path.join(ROOT, "include"), "-I", HOST, os.path.join(ROOT, "tests", "c", "knx_fuzz.c"), *srcs,
            "-o", out, "-L", LIBDIR, "-lkernix", f"-Wl,-rpath,{LIBDIR}", "-lm"]

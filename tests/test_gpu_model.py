@@ -184,3 +184,49 @@ def test_workspace_identical_across_batch_sizes(tmp_path):
     b = m(x[:37])
     assert np.array_equal(a, b)
     m.close()
+
+
+@pytest.mark.parametrize("name", ["cnn", "transformer"])
+def test_forward_device_matches_host_forward(tmp_path, name):
+    """kernix_capi_forward_device on device buffers gives the bits of the host-pointer forward: on a torch stream, on
+    the model's own stream (stream=None), chunked under a small workspace limit, and interleaved with host forwards
+    of another batch (the forwards share the model's workspace; the runtime orders them on the device)."""
+    import torch
+
+    p = str(tmp_path / f"{name}.knx")
+    if name == "cnn":
+        x = configs.cnn(p, batch=24, hw=16, widths=(32, 32, 64, 64))
+    else:
+        x = configs.transformer(p, batch=6, layers=2, seq=32, d=128, heads=4, ffn=256)
+    m = Model(p)
+    want = m(x).reshape(len(x), -1)
+    other = np.asarray(x)[::-1].copy()
+    want_other = m(other).reshape(len(x), -1)
+    dx = torch.from_numpy(to_rows(m, x)).cuda()
+    s = torch.cuda.Stream()
+    outs = []
+    for stream in (s, None):
+        out = torch.full((len(x), m.out_dim), 7.0, dtype=torch.float32, device="cuda")
+        with torch.cuda.stream(s):
+            m.forward_device(dx.data_ptr(), dx.shape[0], out.data_ptr(),
+                             None if stream is None else stream.cuda_stream)
+        got_other = m(other).reshape(len(x), -1)  # a host forward right after, on the model's stream
+        assert np.array_equal(got_other, want_other)
+        torch.cuda.synchronize()
+        outs.append(out.cpu().numpy())
+    for got in outs:
+        assert np.array_equal(got, want)
+    m.close()
+    # chunked: at most 5 samples per piece
+    m = Model(p)
+    per, fixed, _ = m.ws_info()
+    m2 = Model(p, workspace_mb=((fixed + 5 * per) * 4 + 100) / (1 << 20))
+    out = torch.zeros((len(x), m.out_dim), dtype=torch.float32, device="cuda")
+    with torch.cuda.stream(s):
+        m2.forward_device(dx.data_ptr(), dx.shape[0], out.data_ptr(), s.cuda_stream)
+    s.synchronize()
+    assert m2.ws_info()[2] == 5 * m2.seq_len
+    got = out.cpu().numpy()
+    m.close()
+    m2.close()
+    assert np.array_equal(got, want)
