@@ -13,22 +13,20 @@ tests can build the same architecture at reduced width / batch.
 """
 import numpy as np
 
-from . import knx_write as kw
+from .knxfile import ModelBuilder
 
 
 def int8_mlp(path, seed=0, batch=64, dims=(784, 512, 256, 10)):
     rng = np.random.default_rng(seed)
-    m = kw.Sequential(v2=True)
+    b = ModelBuilder((dims[0],))
+    h = b.input
     for i in range(len(dims) - 1):
         fan_in = dims[i]
         w = rng.normal(0.0, 1.0 / np.sqrt(fan_in), (fan_in, dims[i + 1]))
-        b = rng.normal(0.0, 0.01, dims[i + 1])
-        m.linear(w, b, dtype="i8_col")
-        if i < len(dims) - 2:
-            m.act("relu")
-    m.write(path)
-    x = rng.random((batch, dims[0]), dtype=np.float32)
-    return x
+        bias = rng.normal(0.0, 0.01, dims[i + 1])
+        h = b.linear(h, w, bias, activation="relu" if i < len(dims) - 2 else None, fmt="i8_col")
+    b.save(path, version=2)
+    return rng.random((batch, dims[0]), dtype=np.float32)
 
 
 def i8gemm_inputs(M, N=4096, K=4096, seed=12345):
@@ -44,61 +42,59 @@ def i8gemm_inputs(M, N=4096, K=4096, seed=12345):
 
 def fp32_mlp(path, seed=0, batch=8192, dims=(4096, 4096, 4096, 1000)):
     rng = np.random.default_rng(seed)
-    m = kw.Sequential(v2=False)
+    b = ModelBuilder((dims[0],))
+    h = b.input
     for i in range(len(dims) - 1):
         fan_in = dims[i]
         w = rng.standard_normal((fan_in, dims[i + 1]), dtype=np.float32) * np.float32(np.sqrt(2.0 / fan_in))
-        b = rng.normal(0.0, 0.01, dims[i + 1])
-        m.linear(w, b)
-        if i < len(dims) - 2:
-            m.act("relu")
-    m.write(path)
-    x = rng.standard_normal((batch, dims[0]), dtype=np.float32)
-    return x
+        bias = rng.normal(0.0, 0.01, dims[i + 1])
+        h = b.linear(h, w, bias, activation="relu" if i < len(dims) - 2 else None)
+    b.save(path, version=1)
+    return rng.standard_normal((batch, dims[0]), dtype=np.float32)
 
 
 def cnn(path, seed=0, batch=256, hw=32, widths=(64, 64, 128, 256), classes=10):
     """The residual add joins conv1 and conv2 (the only same-shape pair); returns NCHW input."""
     rng = np.random.default_rng(seed)
-    g = kw.Graph((hw, hw, 3), layout=1)
+    b = ModelBuilder((hw, hw, 3), channels_first=True)
 
     def conv(x, cin, cout, stride):
         fan_in = 9 * cin
         w = rng.standard_normal((fan_in, cout), dtype=np.float32) * np.float32(np.sqrt(2.0 / fan_in))
-        b = rng.normal(0.0, 0.01, cout)
-        return g.conv(x, w, b, (3, 3), stride=(stride, stride), pads=(1, 1, 1, 1), act="relu")
+        bias = rng.normal(0.0, 0.01, cout)
+        return b.conv(x, w, bias, kernel=(3, 3), stride=(stride, stride), padding=(1, 1, 1, 1), activation="relu")
 
-    h1 = conv(0, 3, widths[0], 1)
+    h1 = conv(b.input, 3, widths[0], 1)
     h2 = conv(h1, widths[0], widths[1], 1)
-    r = g.binary(h1, h2, "add")
+    r = b.add(h1, h2)
     h3 = conv(r, widths[1], widths[2], 2)
     h4 = conv(h3, widths[2], widths[3], 2)
-    p = g.global_pool(h4, "avg")
+    p = b.global_pool(h4, "avg")
     w = rng.normal(0.0, 1.0 / np.sqrt(widths[3]), (widths[3], classes))
-    g.linear(p, w, rng.normal(0.0, 0.01, classes))
-    g.write(path)
+    b.linear(p, w, rng.normal(0.0, 0.01, classes))
+    b.save(path)
     return rng.standard_normal((batch, 3, hw, hw), dtype=np.float32)
 
 
 def transformer(path, seed=0, batch=64, seq=128, d=512, heads=8, ffn=2048, layers=4, quantize="int8"):
     rng = np.random.default_rng(seed)
-    g = kw.Graph((seq, d), quantize=quantize)
+    b = ModelBuilder((seq, d), int8=quantize == "int8")
 
     def lin(fan_in, fan_out):
         return rng.normal(0.0, 1.0 / np.sqrt(fan_in), (fan_in, fan_out)), rng.normal(0.0, 0.01, fan_out)
 
-    x = 0
+    x = b.input
     for _ in range(layers):
-        h = g.layernorm(x, 1.0 + rng.normal(0.0, 0.05, d), rng.normal(0.0, 0.05, d), 1e-5)
+        h = b.layer_norm(x, 1.0 + rng.normal(0.0, 0.05, d), rng.normal(0.0, 0.05, d), 1e-5)
         (wq, bq), (wk, bk), (wv, bv), (wo, bo) = lin(d, d), lin(d, d), lin(d, d), lin(d, d)
-        a = g.attention(h, heads, wq, bq, wk, bk, wv, bv, wo, bo)
-        x = g.binary(x, a, "add")
-        h = g.layernorm(x, 1.0 + rng.normal(0.0, 0.05, d), rng.normal(0.0, 0.05, d), 1e-5)
+        a = b.attention(h, heads, wq, wk, wv, wo, bq, bk, bv, bo)
+        x = b.add(x, a)
+        h = b.layer_norm(x, 1.0 + rng.normal(0.0, 0.05, d), rng.normal(0.0, 0.05, d), 1e-5)
         w1, b1 = lin(d, ffn)
         w2, b2 = lin(ffn, d)
-        f = g.linear(g.linear(h, w1, b1, act="gelu"), w2, b2)
-        x = g.binary(x, f, "add")
-    g.write(path)
+        f = b.linear(b.linear(h, w1, b1, activation="gelu"), w2, b2)
+        x = b.add(x, f)
+    b.save(path)
     return rng.standard_normal((batch, seq, d), dtype=np.float32)
 
 

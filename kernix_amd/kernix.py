@@ -1,15 +1,20 @@
-"""KERNIX model runtime — Python binding (ctypes + numpy only) for the MI355X build.
+"""Python binding of the KERNIX model runtime (ctypes + numpy) for the MI355X build of libkernix.so.
 
-Same API as the reference binding (reference python/kernix.py:43-115):
+API contract kept from the reference binding (reference python/kernix.py:43-115): the class `Model(path,
+workspace_mb=None, ane=False)`, the attributes `in_dim, out_dim, seq_len, in_shape, out_shape, channels_first`, calling
+a model on a batch, `trim()`, `ane_info()`, `_ane_dump()`, `close()`; ValueError for a file that does not load or an
+input of the wrong shape, RuntimeError for a failed forward.
 
-    from kernix_amd.kernix import Model
-    m = Model("model.knx")        # workspace_mb=None → library default, 0 → unlimited
-    y = m(x)                      # x: (batch, *m.in_shape) float32 → (batch, *m.out_shape)
-                                  # PyTorch conv models (layout 1): (batch, C, H, W); the legacy (rows, in_dim) too
+    m = Model("model.knx")
+    y = m(x)   # x: (batch, *m.in_shape) float32 -> (batch, *m.out_shape); also accepts (rows, in_dim)
 
-One Model may be called from several threads: calls on one model are serialized (they share its device workspace).
-The library is kernix_amd/libkernix.so, or the path in the KERNIX_LIB environment variable; importing this module
-fails with OSError when it cannot be loaded — there is no CPU fallback.
+Models whose file says layout 1 (PyTorch convolution models) take and return channels-first arrays; the runtime itself
+is channels-last, and the binding moves the axis both ways.  Calls on one Model are serialized by a lock: they share
+the model's device workspace.  Use one Model per thread to run concurrently.
+
+The shared library is kernix_amd/libkernix.so, or the file named by $KERNIX_LIB.  It is opened on first use (the first
+Model, or the first call of an extension), not at import; opening fails with OSError when the library is missing or
+was built for another target — there is no CPU fallback.
 """
 import ctypes
 import os
@@ -18,121 +23,178 @@ import warnings
 
 import numpy as np
 
-_LIB_PATH = os.environ.get("KERNIX_LIB", os.path.join(os.path.dirname(os.path.abspath(__file__)), "libkernix.so"))
-_lib = ctypes.CDLL(_LIB_PATH)
+INT8_REF, INT8_I8 = 0, 1  # kernix_capi_set_int8_mode: reference dispatch / int8 arithmetic at every batch size
 
-_P = ctypes.c_void_p
-_I = ctypes.c_int
-_IP = ctypes.POINTER(ctypes.c_int)
-for _name, _args, _res in (
-    ("kernix_capi_load", [ctypes.c_char_p], _P),
-    ("kernix_capi_free", [_P], None),
-    ("kernix_capi_dims", [_P, _IP, _IP, _IP], None),
-    ("kernix_capi_forward", [_P, _P, _I, _P], _I),
-    ("kernix_capi_trim", [_P], None),
-    ("kernix_capi_set_workspace_limit", [_P, ctypes.c_size_t], None),
-    ("kernix_capi_shapes", [_P, _IP, _IP, _IP, _IP, _IP], None),
-    ("kernix_capi_set_ane", [_P, _I], _I),
-    ("kernix_capi_ane_info", [_P, _IP], None),
-    ("kernix_capi_ane_dump", [_P, _I, _I, ctypes.c_char_p], _I),
-    ("kernix_capi_set_int8_mode", [_P, _I], _I),
-    ("kernix_capi_forward_device", [_P, _P, _I, _P, _P], _I),
-    ("kernix_capi_ws_info", [_P, ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t), _IP], None),
-):
-    _f = getattr(_lib, _name)
-    _f.argtypes = _args
-    _f.restype = _res
+_VOID, _INT, _SIZE = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
+_PINT, _PSIZE, _STR = ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_size_t), ctypes.c_char_p
 
-INT8_REF, INT8_I8 = 0, 1
+# The C ABI (include/kernix_capi.h): name -> (argument types, result type)
+_ABI = {
+    "kernix_capi_load": ((_STR,), _VOID),
+    "kernix_capi_free": ((_VOID,), None),
+    "kernix_capi_trim": ((_VOID,), None),
+    "kernix_capi_set_workspace_limit": ((_VOID, _SIZE), None),
+    "kernix_capi_dims": ((_VOID, _PINT, _PINT, _PINT), None),
+    "kernix_capi_forward": ((_VOID, _VOID, _INT, _VOID), _INT),
+    "kernix_capi_set_ane": ((_VOID, _INT), _INT),
+    "kernix_capi_ane_info": ((_VOID, _PINT), None),
+    "kernix_capi_ane_dump": ((_VOID, _INT, _INT, _STR), _INT),
+    "kernix_capi_shapes": ((_VOID, _PINT, _PINT, _PINT, _PINT, _PINT), None),
+    # extensions of this build
+    "kernix_capi_set_int8_mode": ((_VOID, _INT), _INT),
+    "kernix_capi_forward_device": ((_VOID, _VOID, _INT, _VOID, _VOID), _INT),
+    "kernix_capi_ws_info": ((_VOID, _PSIZE, _PSIZE, _PINT), None),
+}
+
+_ANE_FIELDS = ("segments", "compiles", "ane_runs", "failures")
+
+
+def library_path():
+    """the shared library the binding opens"""
+    return os.environ.get("KERNIX_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), "libkernix.so")
+
+
+class _Library:
+    """libkernix.so with its entry points typed, opened once on first attribute access."""
+
+    def __init__(self):
+        self._dll = None
+        self._opening = threading.Lock()
+
+    def _open(self):
+        with self._opening:
+            if self._dll is None:
+                dll = ctypes.CDLL(library_path())
+                for name, (args, res) in _ABI.items():
+                    fn = getattr(dll, name)
+                    fn.argtypes, fn.restype = list(args), res
+                self._dll = dll
+        return self._dll
+
+    def __getattr__(self, name):
+        if name not in _ABI:
+            raise AttributeError(name)
+        return getattr(self._dll or self._open(), name)
+
+
+_lib = _Library()
+
+
+def _channels_first_view(cl_shape):
+    """(…, C) -> (C, …): how a channels-first model shows a per-sample shape of two or more axes"""
+    return (cl_shape[-1],) + cl_shape[:-1] if len(cl_shape) >= 2 else cl_shape
 
 
 class Model:
+    """A loaded .knx model (see the module docstring)."""
+
     def __init__(self, path, workspace_mb=None, ane=False):
-        """workspace_mb: device workspace bound in MB; larger batches run in chunks.  None = library default,
-        0 = unlimited.  ane: accepted for compatibility; there is no Neural Engine here (a RuntimeWarning is issued)."""
-        self._lock = threading.Lock()  # first: close() must work even if __init__ fails below
-        self._h = _lib.kernix_capi_load(os.fsencode(path))
-        if not self._h:
+        """workspace_mb: bound of the device workspace in MB (None: the library default; 0: no bound).  A batch
+        larger than the bound allows runs in pieces.  ane: accepted for compatibility; this platform has no Neural
+        Engine, so asking for it warns and the model runs on the GPU path."""
+        self._lock = threading.Lock()  # before anything that can fail: close() takes it
+        self._h = None
+        handle = _lib.kernix_capi_load(os.fsencode(path))
+        if not handle:
             raise ValueError(f"cannot load KERNIX model: {path}")
+        self._h = handle
         if workspace_mb is not None:
             if workspace_mb < 0:
                 raise ValueError("workspace_mb must be >= 0")
-            _lib.kernix_capi_set_workspace_limit(self._h, int(workspace_mb * (1 << 20)))
-        if ane and _lib.kernix_capi_set_ane(self._h, 1) != 0:
-            warnings.warn("Neural Engine assist unavailable on this platform: running the KERNIX GPU path",
-                          RuntimeWarning, stacklevel=2)
-        dims = [ctypes.c_int() for _ in range(3)]
-        _lib.kernix_capi_dims(self._h, *dims)
-        self.in_dim, self.out_dim, self.seq_len = (d.value for d in dims)
-        in_nd, out_nd, layout = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
-        in_s, out_s = (ctypes.c_int * 4)(), (ctypes.c_int * 4)()
-        _lib.kernix_capi_shapes(self._h, ctypes.byref(in_nd), in_s, ctypes.byref(out_nd), out_s, ctypes.byref(layout))
-        self._in_cl, self._out_cl = tuple(in_s[:in_nd.value]), tuple(out_s[:out_nd.value])  # channels-last
-        self.channels_first = layout.value == 1
-        cf = (lambda s: s[-1:] + s[:-1] if self.channels_first and len(s) >= 2 else s)  # noqa: E731
-        self.in_shape, self.out_shape = cf(self._in_cl), cf(self._out_cl)
-        self._forward = _lib.kernix_capi_forward
+            _lib.kernix_capi_set_workspace_limit(handle, int(workspace_mb * (1 << 20)))
+        if ane and _lib.kernix_capi_set_ane(handle, 1) != 0:
+            warnings.warn("no Neural Engine on this platform: the model runs on the KERNIX GPU path", RuntimeWarning,
+                          stacklevel=2)
+        self._describe()
 
-    def __call__(self, x):
+    def _describe(self):
+        ints = [ctypes.c_int() for _ in range(6)]
+        in_dim, out_dim, seq_len, in_nd, out_nd, layout = ints
+        _lib.kernix_capi_dims(self._h, ctypes.byref(in_dim), ctypes.byref(out_dim), ctypes.byref(seq_len))
+        in4, out4 = (ctypes.c_int * 4)(), (ctypes.c_int * 4)()
+        _lib.kernix_capi_shapes(self._h, ctypes.byref(in_nd), in4, ctypes.byref(out_nd), out4, ctypes.byref(layout))
+        self.in_dim, self.out_dim, self.seq_len = in_dim.value, out_dim.value, seq_len.value
+        self._in_cl = tuple(in4[: in_nd.value])    # channels-last, as the runtime stores values
+        self._out_cl = tuple(out4[: out_nd.value])
+        self.channels_first = layout.value == 1
+        view = _channels_first_view if self.channels_first else tuple
+        self.in_shape, self.out_shape = view(self._in_cl), view(self._out_cl)
+
+    # ---- forward ----
+    def _rows_of(self, x):
+        """x as contiguous float32 rows of in_dim (channels-last), and the row count"""
         x = np.asarray(x)
-        if x.ndim >= 2 and tuple(x.shape[1:]) == self.in_shape:
+        batched = x.ndim >= 2 and tuple(x.shape[1:]) == self.in_shape
+        if batched:
             if self.channels_first and x.ndim >= 3:
-                x = np.moveaxis(x, 1, -1)  # (B, C, ...) → (B, ..., C)
-        elif not (x.ndim == 2 and x.shape[1] == self.in_dim):  # legacy (rows, in_dim)
-            raise ValueError(f"input shape {x.shape}: expected (batch, {', '.join(map(str, self.in_shape))}) "
-                             f"or (rows, {self.in_dim})")
+                x = np.moveaxis(x, 1, -1)
+        elif not (x.ndim == 2 and x.shape[1] == self.in_dim):
+            want = ", ".join(str(d) for d in self.in_shape)
+            raise ValueError(f"input shape {x.shape}: expected (batch, {want}) or (rows, {self.in_dim})")
         x = np.ascontiguousarray(x, dtype=np.float32)
         rows = x.size // self.in_dim
-        if rows == 0 or rows % self.seq_len:
-            raise ValueError(f"input rows {rows} must be a positive multiple of seq_len {self.seq_len}")
-        out = np.empty((rows // self.seq_len,) + self._out_cl, np.float32)
-        with self._lock:
-            status = self._forward(self._h, x.ctypes.data, rows, out.ctypes.data)
-        if status != 0:
-            raise RuntimeError("KERNIX forward failed")
-        return np.moveaxis(out, -1, 1) if self.channels_first and out.ndim >= 3 else out
+        if rows == 0 or rows % self.seq_len != 0:
+            raise ValueError(f"{rows} input rows: must be a positive multiple of seq_len {self.seq_len}")
+        return x, rows
 
-    # ---- extensions of this build ----
-    def set_int8_mode(self, mode):
-        """INT8_REF (default): int8 arithmetic only at <= 2 rows, the fp32 copy above (the reference's dispatch);
-        INT8_I8: int8 arithmetic on i8 MFMA at every batch size."""
+    def __call__(self, x):
+        x, rows = self._rows_of(x)
+        y = np.empty((rows // self.seq_len,) + self._out_cl, dtype=np.float32)
         with self._lock:
-            if _lib.kernix_capi_set_int8_mode(self._h, int(mode)) != 0:
-                raise ValueError(f"bad int8 mode {mode}")
-
-    def forward_device(self, x_ptr, rows, out_ptr, stream=None):
-        """Enqueue a forward on device buffers (e.g. torch tensors' data_ptr()); stream: hipStream_t handle or None."""
-        with self._lock:
-            if _lib.kernix_capi_forward_device(self._h, x_ptr, int(rows), out_ptr, stream) != 0:
-                raise RuntimeError("KERNIX device forward failed")
-
-    def ws_info(self):
-        """(workspace floats per sample, batch-independent floats, rows the workspace is allocated for or -1)"""
-        per, fixed, batch = ctypes.c_size_t(), ctypes.c_size_t(), ctypes.c_int()
-        with self._lock:
-            _lib.kernix_capi_ws_info(self._h, ctypes.byref(per), ctypes.byref(fixed), ctypes.byref(batch))
-        return per.value, fixed.value, batch.value
+            ok = _lib.kernix_capi_forward(self._h, x.ctypes.data, rows, y.ctypes.data) == 0
+        if not ok:
+            raise RuntimeError("KERNIX forward failed (see stderr)")
+        if self.channels_first and y.ndim >= 3:
+            y = np.moveaxis(y, -1, 1)
+        return y
 
     # ---- reference API ----
-    def ane_info(self):
-        out = (ctypes.c_int * 4)()
-        with self._lock:
-            _lib.kernix_capi_ane_info(self._h, out)
-        return dict(zip(("segments", "compiles", "ane_runs", "failures"), out))
-
-    def _ane_dump(self, seg, batch, path):
-        with self._lock:
-            return _lib.kernix_capi_ane_dump(self._h, seg, batch, os.fsencode(path))
-
     def trim(self):
-        """Release the device workspace (weights stay on the device); the next call allocates it again."""
+        """Release the device workspace; the weights stay on the device and the next call allocates it again."""
         with self._lock:
             _lib.kernix_capi_trim(self._h)
 
-    def close(self):
-        if getattr(self, "_h", None):
-            with self._lock:
-                _lib.kernix_capi_free(self._h)
-                self._h = None
+    def ane_info(self):
+        """Neural Engine counters (all zero here)."""
+        counts = (ctypes.c_int * 4)()
+        with self._lock:
+            _lib.kernix_capi_ane_info(self._h, counts)
+        return {name: counts[i] for i, name in enumerate(_ANE_FIELDS)}
 
-    __del__ = close
+    def _ane_dump(self, seg, batch, path):
+        """Core ML export of a segment: unavailable here, returns -1."""
+        with self._lock:
+            return _lib.kernix_capi_ane_dump(self._h, seg, batch, os.fsencode(path))
+
+    def close(self):
+        handle = getattr(self, "_h", None)
+        if handle:
+            with self._lock:
+                self._h = None
+                _lib.kernix_capi_free(handle)
+
+    def __del__(self):
+        self.close()
+
+    # ---- extensions of this build ----
+    def set_int8_mode(self, mode):
+        """INT8_REF (default): int8 arithmetic at <= 2 rows and the dequantized fp32 weights above, as the reference
+        dispatches; INT8_I8: int8 arithmetic (i8 MFMA) at every batch size."""
+        with self._lock:
+            if _lib.kernix_capi_set_int8_mode(self._h, int(mode)) != 0:
+                raise ValueError(f"unknown int8 mode {mode!r}")
+
+    def forward_device(self, x_ptr, rows, out_ptr, stream=None):
+        """Enqueue a forward on device buffers (e.g. torch tensors' data_ptr(); rows x in_dim in, rows/seq_len x
+        out_dim out) on a hipStream_t handle (None: the model's own stream).  Returns without waiting; forwards on
+        different streams still run in call order on the device."""
+        with self._lock:
+            if _lib.kernix_capi_forward_device(self._h, x_ptr, int(rows), out_ptr, stream) != 0:
+                raise RuntimeError("KERNIX device forward failed (see stderr)")
+
+    def ws_info(self):
+        """(workspace floats per sample, batch-independent floats, rows the workspace holds or -1)"""
+        per, fixed, rows = ctypes.c_size_t(), ctypes.c_size_t(), ctypes.c_int()
+        with self._lock:
+            _lib.kernix_capi_ws_info(self._h, ctypes.byref(per), ctypes.byref(fixed), ctypes.byref(rows))
+        return per.value, fixed.value, rows.value

@@ -83,7 +83,7 @@ def i8gemm_expected(A, W, sa, sw, bias):
 
 def write_knx2_int8_mlp(path, layers):
     """KNX2 (reference docs/int8-quantization-design.md:67-87): LINEAR with an I8_COL weight block, ACT relu between.
-    Written here byte by byte from the format description, independently of kernix_amd/knx_write.py."""
+    Written here byte by byte from the format description, independently of the package writer (kernix_amd/knxfile.py)."""
     recs = []
     for i, (q, scale, bias) in enumerate(layers):
         k, n = q.shape

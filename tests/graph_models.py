@@ -1,95 +1,113 @@
-"""Small .knx graphs that together use every op kind of the runtime, one family per graph (CNN ops, 1-D convolution
-and broadcasting, recurrent cells, embedding and attention), shared by the GPU graph parity tests and the loader fuzz
-test.  Written with the numpy .knx writer; weights N(0, 0.3) from a seed per family."""
+"""Small .knx graphs that together use every op kind, activation, binary op, broadcast, merge mode and convolution
+variant of the runtime, shared by the GPU graph parity tests and the loader fuzz test.
+
+    vision     H×W×C: plain, depthwise, grouped + dilated, strided and pointwise convolutions, both poolings with and
+               without padding counted, padding, upsampling, concat on the channel axis, global poolings, max/sub
+    sequence   T×C: 1-D convolutions (dilated, strided, grouped), 1-D pooling, layer norm without affine, row and
+               channel broadcasting (add, mul, div), select, reshape, the smooth activations
+    recurrent  T×F: LSTM, GRU and simple RNN cells, one and two directions, every merge, sequences and last states
+    tokens     token ids: embedding, constant add, causal self-attention with biases, cross attention with three
+               inputs and S ≠ Rq, layer norm, upsampling on T×C, permute, affine, softmax, min
+
+Written with kernix_amd.knxfile; weights N(0, 0.3) (activation-specific scales where a function would saturate)
+from a seed per family."""
 import numpy as np
 
-from kernix_amd import knx_write
-from kernix_amd.knx_write import FIRST, LAST
+from kernix_amd.knxfile import ModelBuilder
 
 
-def W(rng, *s, scale=0.3):
-    return rng.normal(0.0, scale, s)
+def _w(rng, *shape, scale=0.3):
+    return rng.normal(0.0, scale, shape)
 
 
-def cnn_graph(rng, quantize=None):
-    g = knx_write.Graph((9, 8, 3), quantize=quantize)
-    x = g.conv(0, W(rng, 27, 6), W(rng, 6), (3, 3), pads=(1, 1, 1, 1), act="relu")
-    y = g.conv(x, W(rng, 9, 6), None, (3, 3), pads=(1, 1, 1, 1), groups=6)                   # depthwise
-    y = g.conv(y, W(rng, 27, 6), W(rng, 6), (3, 3), pads=(1, 1, 1, 1), groups=2, act="gelu")  # grouped
-    x = g.binary(x, y, "add")
-    z = g.conv(x, W(rng, 24, 6), W(rng, 6), (2, 2), stride=(1, 1), dil=(2, 2), pads=(1, 1, 1, 1), act="silu")
-    z = g.conv(z, W(rng, 54, 5), W(rng, 5), (3, 3), stride=(2, 2), pads=(0, 1, 0, 1), act="tanh")  # 4×4×5
-    x = g.upsample(g.pad(g.pool(x, "max", (2, 2), (2, 2)), (1, 0, 0, 1)), 2, 2)                  # 10×10×6
-    x = g.pool(x, "avg", (3, 3), (1, 1), (1, 1, 1, 1), True)
-    x = g.pool(x, "avg", (3, 3), (3, 3), (1, 1, 1, 1), False)                                   # 4×4×6
-    x = g.concat([x, z], LAST)                                                                  # 4×4×11
-    m = g.global_pool(x, "max")
-    a = g.global_pool(x, "avg")
-    v = g.binary(m, a, "sub")
-    return g, g.linear(v, W(rng, 11, 4), W(rng, 4), act="softmax")
+def vision(rng, int8=False):
+    b = ModelBuilder((10, 9, 4), int8=int8)
+    x = b.conv(b.input, _w(rng, 36, 8), _w(rng, 8), kernel=(3, 3), padding=(1, 1, 1, 1), activation="relu6")
+    d = b.conv(x, _w(rng, 9, 8), None, kernel=(3, 3), padding=(1, 1, 1, 1), groups=8)                # depthwise
+    g = b.conv(x, _w(rng, 12, 8), _w(rng, 8), kernel=(1, 3), dilation=(1, 2), padding=(0, 0, 2, 2), groups=2,
+               activation="hard_sigmoid")                                                              # grouped, dilated
+    x = b.binary(d, g, "max")                                                                          # 10×9×8
+    s = b.conv(x, _w(rng, 72, 6), _w(rng, 6), kernel=(3, 3), stride=(2, 2), padding=(1, 1, 1, 1),
+               activation="mish")                                                                      # 5×5×6
+    p = b.pool(x, "max", (3, 3), (2, 2), (1, 1, 1, 1))                                                  # 5×5×8
+    p = b.upsample(b.pad(p, (0, 1, 1, 0)), (2, 1))                                                     # 12×6×8
+    p = b.pool(p, "avg", (2, 2), (2, 1), (0, 0, 1, 0), count_pad=True)                                 # 6×6×8
+    p = b.pool(p, "avg", (2, 2), (1, 1), (1, 0, 0, 0), count_pad=False)                                # 6×5×8
+    p = b.select(p, "first", 0, 5)                                                                     # 5×5×8
+    y = b.concat([p, s], "last")                                                                       # 5×5×14
+    y = b.conv(y, _w(rng, 14, 10), _w(rng, 10), activation="selu")                                     # pointwise
+    hi, lo = b.global_pool(y, "max"), b.global_pool(y, "avg")
+    return b, b.linear(b.binary(hi, lo, "sub"), _w(rng, 10, 5), _w(rng, 5), activation="softmax")
 
 
-def conv1d_graph(rng, quantize=None):
-    g = knx_write.Graph((20, 4), quantize=quantize)
-    x = g.conv(0, W(rng, 12, 8), W(rng, 8), (3, 1), dil=(2, 1), pads=(2, 2, 0, 0), act="elu", alpha=0.7)
-    x = g.pool(x, "max", (2, 1), (2, 1))                                                        # 10×8
-    x = g.conv(x, W(rng, 16, 8), W(rng, 8), (4, 1), stride=(2, 1), pads=(1, 1, 0, 0), groups=2, act="leaky_relu",
-               alpha=0.1)                                                                       # 5×8
-    x = g.layernorm(x, 1.0 + W(rng, 8, scale=0.1), W(rng, 8, scale=0.1), 1e-5)
-    r = g.global_pool(x, "avg")                                                                 # (8,)
-    x = g.binary(x, r, "mul")                                                                   # row broadcast
-    c = g.select(x, LAST, 0, 1)                                                                 # 5×1
-    x = g.binary(x, c, "div")                                                                   # channel broadcast
-    x = g.act(x, "softsign")
-    return g, g.linear(g.reshape(x, (40,)), W(rng, 40, 6), W(rng, 6), act="hard_swish")
+def sequence(rng, int8=False):
+    b = ModelBuilder((16, 6), int8=int8)
+    x = b.conv(b.input, _w(rng, 30, 9), _w(rng, 9), kernel=(5, 1), padding=(2, 2, 0, 0), activation="elu",
+               alpha=0.5)                                                                              # 16×9
+    x = b.pool(x, "avg", (3, 1), (1, 1), (1, 1, 0, 0), count_pad=True)
+    x = b.conv(x, _w(rng, 9, 9), None, kernel=(3, 1), stride=(2, 1), dilation=(2, 1), padding=(2, 1, 0, 0),
+               groups=3, activation="softplus")                                                        # 8×9
+    x = b.pool(x, "max", (2, 1), (2, 1))                                                               # 4×9
+    x = b.layer_norm(x)
+    x = b.binary(x, b.global_pool(x, "max"), "add")                                                    # row broadcast
+    c = b.select(x, "last", 4, 1)                                                                      # 4×1
+    x = b.binary(x, b.activation(c, "sigmoid"), "mul")                                                 # channel broadcast
+    x = b.binary(x, b.add_const(b.activation(c, "softsign"), np.full(4, 2.0)), "div")
+    x = b.activation(b.activation(x, "gelu_tanh"), "leaky_relu", alpha=0.2)
+    x = b.linear(b.reshape(x, (36,)), _w(rng, 36, 7), _w(rng, 7), activation="silu")
+    x = b.activation(b.linear(x, _w(rng, 7, 7, scale=0.1), None, activation="tanh"), "exp")
+    return b, b.linear(b.activation(x, "gelu"), _w(rng, 7, 3), _w(rng, 3), activation="hard_swish")
 
 
-def rnn_graph(rng, quantize=None):
-    g = knx_write.Graph((7, 5), quantize=quantize)
-    a = g.rnn(0, "GRU", 4, [(W(rng, 5, 12), W(rng, 4, 12), W(rng, 24)), (W(rng, 5, 12), W(rng, 4, 12), W(rng, 24))],
-              ret_seq=True)                                                                     # 7×8
-    b = g.rnn(0, "LSTM", 3, [(W(rng, 5, 12), W(rng, 3, 12), W(rng, 12))], act="relu", ret_seq=True)  # 7×3
-    c = g.concat([a, b], LAST)                                                                  # 7×11
-    d = g.rnn(c, "RNN", 4, [(W(rng, 11, 4), W(rng, 4, 4), W(rng, 4)), (W(rng, 11, 4), W(rng, 4, 4), W(rng, 4))],
-              ret_seq=False, merge="ave")                                                       # (4,)
-    e = g.rnn(c, "LSTM", 4, [(W(rng, 11, 16), W(rng, 4, 16), W(rng, 16)), (W(rng, 11, 16), W(rng, 4, 16), W(rng, 16))],
-              ret_seq=True, merge="sum")                                                        # 7×4
-    f = g.rnn(e, "GRU", 4, [(W(rng, 4, 12), W(rng, 4, 12), W(rng, 24)), (W(rng, 4, 12), W(rng, 4, 12), W(rng, 24))],
-              ret_seq=False, merge="mul")                                                       # (4,)
-    s = g.select(a, FIRST, 6, 1, True)                                                          # (8,)
-    return g, g.concat([d, s, f], LAST)
+def recurrent(rng, int8=False):
+    b = ModelBuilder((6, 4), int8=int8)
+
+    def cell(cell, fin, units, dirs):
+        g = {"LSTM": 4, "GRU": 3, "RNN": 1}[cell] * units
+        nb = 2 * g if cell == "GRU" else g
+        return [(_w(rng, fin, g), _w(rng, units, g), _w(rng, nb)) for _ in range(dirs)]
+
+    a = b.recurrent(b.input, "LSTM", 3, cell("LSTM", 4, 3, 2), return_sequences=True)               # 6×6 (concat)
+    g = b.recurrent(b.input, "GRU", 5, cell("GRU", 4, 5, 1), activation="relu", return_sequences=True)  # 6×5
+    s = b.concat([a, g], "last")                                                                     # 6×11
+    r = b.recurrent(s, "RNN", 4, cell("RNN", 11, 4, 2), return_sequences=True, merge="mul")           # 6×4
+    l = b.recurrent(r, "LSTM", 3, cell("LSTM", 4, 3, 2), activation="relu", merge="ave")             # (3,)
+    q = b.recurrent(s, "GRU", 3, cell("GRU", 11, 3, 2), merge="sum")                                 # (3,)
+    t = b.select(g, "first", 5, 1, squeeze=True)                                                     # (5,)
+    u = b.recurrent(b.select(s, "first", 2, 3), "RNN", 2, cell("RNN", 11, 2, 1), activation="sigmoid")  # (2,)
+    return b, b.concat([l, q, t, u], "last")
 
 
-def attn_graph(rng, quantize=None):
-    g = knx_write.Graph((6,), quantize=quantize)
-    e = g.add_const(g.embedding(0, W(rng, 10, 8)), W(rng, 48))                                 # 6×8
-    h = g.attention(e, 2, W(rng, 8, 6), W(rng, 6), W(rng, 8, 6), W(rng, 6), W(rng, 8, 4), W(rng, 4), W(rng, 4, 8),
-                    W(rng, 8), causal=True)
-    h = g.layernorm(g.binary(e, h, "add"), W(rng, 8), W(rng, 8), 1e-5)
-    u = g.upsample(h, 2)                                                                        # 12×8
-    k = g.act(u, "tanh")
-    h = g.attention(h, 4, W(rng, 8, 16), None, W(rng, 8, 16), None, W(rng, 8, 8), None, W(rng, 8, 8), None,
-                    v=u, k=k)                                                                   # cross, S = 12
-    h = g.permute(g.reshape(h, (6, 2, 4)), (1, 0, 2))
-    h = g.affine(g.reshape(h, (2, 24)), W(rng, 24), W(rng, 24))
-    h = g.softmax(g.binary(h, g.select(h, FIRST, 1, 1), "max"))
-    return g, g.binary(h, g.select(h, LAST, 3, 1), "min")
+def tokens(rng, int8=False):
+    b = ModelBuilder((5,), int8=int8)
+    e = b.add_const(b.embedding(b.input, _w(rng, 12, 6)), _w(rng, 30))                               # 5×6
+    a = b.attention(e, 3, _w(rng, 6, 6), _w(rng, 6, 6), _w(rng, 6, 9), _w(rng, 9, 6), _w(rng, 6), _w(rng, 6),
+                    _w(rng, 9), _w(rng, 6), causal=True)                                             # dk 2, dv 3
+    h = b.layer_norm(b.add(e, a), 1.0 + _w(rng, 6, scale=0.1), _w(rng, 6, scale=0.1))
+    u = b.upsample(h, (2, 1))                                                                        # 10×6
+    k = b.activation(u, "relu")
+    c = b.attention(h, 2, _w(rng, 6, 8), _w(rng, 6, 8), _w(rng, 6, 4), _w(rng, 4, 6), v=u, k=k)     # S = 10, Rq = 5
+    c = b.permute(b.reshape(c, (5, 3, 2)), (2, 0, 1))                                                # 2×5×3
+    c = b.affine(b.reshape(c, (10, 3)), _w(rng, 3), _w(rng, 3))
+    c = b.softmax(b.binary(c, b.select(c, "first", 4, 1), "min"))
+    return b, b.binary(c, b.concat([b.select(c, "first", 0, 5), b.select(c, "first", 5, 5)], "first"), "add")
 
 
-FAMILIES = {"cnn": cnn_graph, "conv1d": conv1d_graph, "rnn": rnn_graph, "attn": attn_graph}
+FAMILIES = {"vision": vision, "sequence": sequence, "recurrent": recurrent, "tokens": tokens}
 
 
 def make(tmp_path, family, quantize=None):
+    """(path of the written .knx, its builder); quantize="int8" writes int8 weight blocks"""
     rng = np.random.default_rng(sum(map(ord, family)))
-    g, _ = FAMILIES[family](rng, quantize)
-    p = str(tmp_path / f"{family}.knx")
-    g.write(p)
-    return p, g
+    b, _ = FAMILIES[family](rng, int8=quantize == "int8")
+    p = str(tmp_path / f"{family}{'_i8' if quantize else ''}.knx")
+    b.save(p)
+    return p, b
 
 
-def inputs(g, batch, seed=0):
+def inputs(b, batch, seed=0):
     rng = np.random.default_rng(seed + batch)
-    shape = g.shapes[0]
-    if shape == (6,):  # token ids of the embedding model
-        return rng.integers(0, 10, (batch,) + shape).astype(np.float32)
+    shape = b.input.shape
+    if shape == (5,):  # token ids of the embedding model
+        return rng.integers(0, 12, (batch,) + shape).astype(np.float32)
     return rng.standard_normal((batch,) + shape).astype(np.float32)

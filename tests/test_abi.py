@@ -54,7 +54,8 @@ def test_reference_capi_signatures_bind(tmp_path):
 
 
 def test_missing_library_fails_loudly():
-    code = "import sys; sys.path.insert(0, %r); import kernix_amd.kernix" % ROOT
+    """the binding opens the library on first use: a missing library is an OSError there, not a fallback"""
+    code = "import sys; sys.path.insert(0, %r); import kernix_amd.kernix as k; k.Model('any.knx')" % ROOT
     r = subprocess.run([sys.executable, "-c", code], env=dict(os.environ, KERNIX_LIB="/nonexistent/libkernix.so"),
                        capture_output=True, text=True)
     assert r.returncode != 0 and "OSError" in r.stderr

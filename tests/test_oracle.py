@@ -11,7 +11,9 @@ import math
 import numpy as np
 import pytest
 
-from kernix_amd import knx_write
+import struct
+
+from kernix_amd import knxfile
 from oracle import knx_ref
 
 
@@ -138,7 +140,7 @@ def test_qweight_unpack_exact():
     rng = LCG()
     q, scale, _, _ = qcase(rng, 37, 19, 1)
     w = q.astype(np.float32) * scale[None, :]
-    blob = knx_write.u32(1) + knx_write.f32(scale) + q.tobytes()
+    blob = struct.pack("<I", 1) + scale.astype("<f4").tobytes() + q.tobytes()
     r = knx_ref._R(blob)
     kind, w2 = knx_ref._weight(r, 2, 37, 19, False)
     assert kind == "f32" and np.array_equal(w2, w)
@@ -152,7 +154,7 @@ def test_quantize_cols_invariants():
     w[:, 3] = 0.0
     w[:, 5] = np.array([127.0, 63.5, -0.5, 1.5] + [0.0] * 66)  # scale exactly 1 → ties
     scale, q = knx_ref.quantize_cols(w)
-    s2, q2 = knx_write.quantize(w, "col")
+    s2, q2 = knxfile.quantize(w, "column")
     assert np.array_equal(scale, s2) and np.array_equal(q, q2)
     assert scale[3] == 1.0 and not q[:, 3].any()
     assert list(q[:4, 5]) == [127, 64, 0, 2]
@@ -162,7 +164,7 @@ def test_quantize_cols_invariants():
         assert np.abs(q[:, c]).max() == 127
         assert np.all(np.abs(w[:, c] / np.float64(scale[c]) - q[:, c]) <= 0.5)
     # per-row axis
-    sr, qr = knx_write.quantize(w.T, "row")
+    sr, qr = knxfile.quantize(w.T, "row")
     assert np.array_equal(sr, scale) and np.array_equal(qr, q.T)
 
 
@@ -298,7 +300,7 @@ def test_v2_zero_column_gives_bias(tmp_path):
     zq = np.array([10, 0, 20, 0, 30, 0, 40, 0], np.int8).reshape(4, 2)
     zs = np.array([0.02, 1.0], np.float32)
     zb = np.array([0.25, -0.75], np.float32)
-    blob = (b"KNX2" + knx_write.u32(1, 0, 4, 2, 1, 1) + knx_write.f32(zs) + zq.tobytes() + knx_write.f32(zb))
+    blob = b"KNX2" + struct.pack("<6I", 1, 0, 4, 2, 1, 1) + zs.astype("<f4").tobytes() + zq.tobytes() + zb.astype("<f4").tobytes()
     p = tmp_path / "v2.knx"
     p.write_bytes(blob)
     m = knx_ref.parse(str(p))
