@@ -1,16 +1,23 @@
 #!/usr/bin/env python3
 """Benchmark of the KERNIX forward hot path on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--no-cpu] [--no-forward]
+    python bench.py [--steps K] [--warmup W] [--no-cpu] [--no-forward] [--no-small]
 
 Headline (`value`): int8 GEMM Y = relu(((float)(A·Wᵀ)·sa[m])·sw[n] + bias[n]) at M = K = N = 4096 with int32
-accumulation, inputs resident in HBM, through the C ABI (knx_hip_i8gemm), in TOPS (1 MAC = 2 ops): K launches back to
-back after W warm-up launches, bracketed by device synchronization and timed by HIP events on the launch stream.
-`roofline` relates the same figure to the int8 MFMA peak and carries the HBM traffic per launch measured with
-rocprofv3 counters (read from profiles/i8gemm_4096_traffic.json).
-Also reported: the same GEMM at M ∈ {1, 16, 256} (HBM-bound) and the .knx forward samples/sec of the int8 MLP,
-fp32 MLP, CNN and int8-weight Transformer workloads (device-resident and end to end through kernix_capi_forward),
-and the CPU oracle (plain C, the reference's int8 arithmetic) timed on this machine's host cores.
+accumulation, inputs resident in HBM, through the C ABI (knx_hip_i8gemm), in TOPS (1 MAC = 2 ops), sustained: W
+untimed warm-up launches and at least 200 ms more of back-to-back launches (past the first milliseconds, in which
+the clocks are still above their loaded level), then exactly K launches back to back, bracketed by device
+synchronizations and timed by HIP events on the launch stream.  Windows of 50 launches after them give the median
+and spread, and the burst figure (K launches right after the W warm-up launches, no further warm-up) is reported
+beside it.  `roofline` relates the
+sustained figure to the int8 MFMA peak and carries the HBM traffic per launch measured with rocprofv3 counters
+(read from profiles/i8gemm_4096_traffic.json).
+Also reported: the GEMM at M ∈ {1, 16, 256} (HBM-bound), with the same operands every launch (the last-level cache
+then holds the weights) and rotating over enough operand copies (> 256 MB) that every launch reads them from HBM; the
+bandwidth-bound row kernels the same two ways; the convolution layers and the attention core; the .knx forward
+samples/sec of the int8 MLP, fp32 MLP, CNN and int8-weight Transformer workloads (device-resident and end to end
+through kernix_capi_forward), each beside the reference's CPU path (oracle/cpu_forward.py: the plain-C kernels of
+the oracle) timed on this machine's host cores on a sample of the same batch; and the CPU oracle's int8 GEMM.
 One JSON line is printed on stdout.
 """
 import argparse
@@ -54,7 +61,35 @@ def time_launches(fn, steps, warmup):
     return start.elapsed_time(end) / steps, wall
 
 
-def i8gemm_bench(M, steps, warmup, N=4096, K=4096):
+def time_sustained(fn, steps, warm_ms=200.0, windows=20, per_window=50):
+    """After at least warm_ms of back-to-back launches (untimed, past the clock ramp of the first milliseconds):
+    exactly `steps` launches timed between two HIP events on torch's current stream with a device synchronization
+    on both sides (ms per launch), then `windows` windows of `per_window` back-to-back launches each bracketed by
+    events (median, p10, p90 ms per launch)."""
+    import statistics
+
+    import torch
+
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < warm_ms:
+        for _ in range(per_window):
+            fn()
+        torch.cuda.synchronize()
+    ms, _ = time_launches(fn, steps, 0)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(windows + 1)]
+    ev[0].record()
+    for w in range(windows):
+        for _ in range(per_window):
+            fn()
+        ev[w + 1].record()
+    torch.cuda.synchronize()
+    per = sorted(ev[w].elapsed_time(ev[w + 1]) / per_window for w in range(windows))
+    return ms, statistics.median(per), per[len(per) // 10], per[(9 * len(per)) // 10]
+
+
+def i8gemm_bench(M, steps, warmup, N=4096, K=4096, sustained=True, rotate_bytes=0):
+    """The int8 GEMM at M×N×K.  rotate_bytes > 0: launches cycle over copies of A and W (and of the output) that
+    together exceed rotate_bytes, so no launch finds its operands in the 256 MB last-level cache."""
     import numpy as np
     import torch
 
@@ -64,18 +99,29 @@ def i8gemm_bench(M, steps, warmup, N=4096, K=4096):
     hipabi.check(L.knx_hip_init())
     A, W, sa, sw, bias = configs.i8gemm_inputs(M, N, K)
     dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
-    dA, dW, dsa, dsw, db = dev(A), dev(W), dev(sa), dev(sw), dev(bias)
-    Y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    dsa, dsw, db = dev(sa), dev(sw), dev(bias)
     P = hipabi.ptr
-    args = (M, N, K, P(dA), K, P(dsa), P(dW), K, P(dsw), P(db), 0, 0.0, 0, P(Y), N, None, 0, hipabi.stream())
+    per_copy = M * K + N * K + 4 * M * N
+    copies = max(1, -(-rotate_bytes // per_copy)) if rotate_bytes else 1
+    dA, dW = dev(A), dev(W)
+    sets = [(dA, dW, torch.empty((M, N), dtype=torch.float32, device="cuda"))]
+    for _ in range(copies - 1):
+        sets.append((dA.clone(), dW.clone(), torch.empty((M, N), dtype=torch.float32, device="cuda")))
+    args = [(M, N, K, P(a), K, P(dsa), P(w), K, P(dsw), P(db), 0, 0.0, 0, P(y), N, None, 0, hipabi.stream())
+            for a, w, y in sets]
+    turn = [0]
 
     def run():
-        hipabi.check(L.knx_hip_i8gemm(*args))
+        hipabi.check(L.knx_hip_i8gemm(*args[turn[0]]))
+        turn[0] = (turn[0] + 1) % len(args)
 
     ms, wall = time_launches(run, steps, warmup)
+    sus = time_sustained(run, steps) if sustained else (ms, ms, ms, ms)
     ops, algo_bytes = configs.i8gemm_work(M, N, K)
-    return dict(M=M, N=N, K=K, ms=ms, wall_ms=wall, tops=ops / (ms * 1e-3) / 1e12, gbs=algo_bytes / (ms * 1e-3) / 1e9,
-                algo_bytes=algo_bytes, ops=ops, A=A, W=W, sa=sa, sw=sw, bias=bias, Y=Y)
+    return dict(M=M, N=N, K=K, ms=sus[0], ms_median=sus[1], ms_p10=sus[2], ms_p90=sus[3], burst_ms=ms, wall_ms=wall,
+                tops=ops / (sus[0] * 1e-3) / 1e12, burst_tops=ops / (ms * 1e-3) / 1e12,
+                gbs=algo_bytes / (sus[0] * 1e-3) / 1e9, algo_bytes=algo_bytes, ops=ops, copies=copies,
+                A=A, W=W, sa=sa, sw=sw, bias=bias, Y=sets[0][2])
 
 
 def cpu_baseline(g, threads, target_s=10.0):
@@ -104,10 +150,15 @@ def cpu_baseline(g, threads, target_s=10.0):
     return dict(tops=ops / sec / 1e12, seconds=sec, rows=rows, reps=reps, bit_exact=bool(np.array_equal(got, y)))
 
 
+ROTATE_BYTES = 320 << 20  # more than the 256 MB last-level cache: a rotating working set comes from HBM
+
+
 def rows_bench(steps, warmup):
     """The bandwidth-bound kernels at the Transformer / CNN workload shapes: algorithmic bytes (every fp32 input read
-    once, every output written once) per launch ÷ time, against HBM peak.  Working sets of 16–80 MB stay in the
-    256 MB last-level cache across back-to-back launches, so these rates can exceed what HBM alone delivers."""
+    once, every output written once) per launch ÷ time, against HBM peak.  Two figures each: `cached`, the same
+    buffers every launch (16-134 MB working sets stay in the 256 MB last-level cache, so this can exceed what HBM
+    delivers; it is what a forward sees when a step's input was just written), and `hbm`, launches rotating over
+    copies whose total exceeds the cache, so every byte comes from HBM."""
     import torch
 
     from kernix_amd import hipabi
@@ -115,33 +166,48 @@ def rows_bench(steps, warmup):
     L = hipabi.lib()
     hipabi.check(L.knx_hip_init())
     P, S = hipabi.ptr, hipabi.stream()
-    dev = lambda *shape: torch.randn(*shape, device="cuda", dtype=torch.float32)  # noqa: E731
+    rnd = lambda *shape: torch.randn(*shape, device="cuda", dtype=torch.float32)  # noqa: E731
     out = {}
 
-    def run(name, fn, nbytes):
-        ms, _ = time_launches(lambda: hipabi.check(fn()), steps, warmup)
-        gbs = nbytes / (ms * 1e-3) / 1e9
-        out[name] = dict(us=round(ms * 1e3, 2), gbs=round(gbs, 1), hbm_frac=round(gbs / PEAK_HBM_GBS, 4),
-                         bytes=int(nbytes))
-        log(f"{name}: {ms * 1e3:.2f} us  {gbs:.0f} GB/s")
+    def run(name, make, call, nbytes):
+        """make(): one set of buffers; call(set): the launch on it"""
+        copies = max(2, -(-ROTATE_BYTES // nbytes))
+        sets = [make() for _ in range(copies)]
+        res = {"bytes": int(nbytes)}
+        for mode in ("cached", "hbm"):
+            turn = [0]
 
-    x, y, g, b = dev(8192, 512), dev(8192, 512), dev(512), dev(512)
-    run("layernorm_8192x512", lambda: L.knx_hip_layernorm(P(x), P(y), 8192, 512, P(g), P(b), 1e-5, S),
-        2 * 8192 * 512 * 4 + 2 * 512 * 4)
-    sc = dev(65536, 128)
-    run("softmax_65536x128_inplace", lambda: L.knx_hip_softmax(P(sc), P(sc), 65536, 128, S), 2 * 65536 * 128 * 4)
-    h, hb = dev(8192, 2048), dev(2048)
-    run("bias_gelu_8192x2048_inplace", lambda: L.knx_hip_bias_act(P(h), P(h), 8192, 2048, P(hb), 1, 0.0, S),
-        2 * 8192 * 2048 * 4 + 2048 * 4)
-    r = dev(8192, 512)
-    run("binary_add_8192x512", lambda: L.knx_hip_binary(0, P(x), 512, 512, P(y), 512, 512, P(r), 16, 512, 512, S),
+            def one():
+                hipabi.check(call(sets[turn[0]]))
+                if mode == "hbm":
+                    turn[0] = (turn[0] + 1) % copies
+
+            ms, _ = time_launches(one, steps, warmup)
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            res[mode] = dict(us=round(ms * 1e3, 2), gbs=round(gbs, 1), hbm_frac=round(gbs / PEAK_HBM_GBS, 4))
+        res["rotating_copies"] = copies
+        out[name] = res
+        log(f"{name}: cached {res['cached']['us']} us {res['cached']['gbs']:.0f} GB/s, "
+            f"from HBM {res['hbm']['us']} us {res['hbm']['gbs']:.0f} GB/s")
+        del sets
+        torch.cuda.empty_cache()
+
+    g, b = rnd(512), rnd(512)
+    run("layernorm_8192x512", lambda: (rnd(8192, 512), torch.empty(8192, 512, device="cuda")),
+        lambda t: L.knx_hip_layernorm(P(t[0]), P(t[1]), 8192, 512, P(g), P(b), 1e-5, S), 2 * 8192 * 512 * 4 + 2 * 512 * 4)
+    run("softmax_65536x128_inplace", lambda: (rnd(65536, 128),),
+        lambda t: L.knx_hip_softmax(P(t[0]), P(t[0]), 65536, 128, S), 2 * 65536 * 128 * 4)
+    hb = rnd(2048)
+    run("bias_gelu_8192x2048_inplace", lambda: (rnd(8192, 2048),),
+        lambda t: L.knx_hip_bias_act(P(t[0]), P(t[0]), 8192, 2048, P(hb), 1, 0.0, S), 2 * 8192 * 2048 * 4 + 2048 * 4)
+    run("binary_add_8192x512", lambda: (rnd(8192, 512), rnd(8192, 512), torch.empty(8192, 512, device="cuda")),
+        lambda t: L.knx_hip_binary(0, P(t[0]), 512, 512, P(t[1]), 512, 512, P(t[2]), 16, 512, 512, S),
         3 * 8192 * 512 * 4)
-    c, gp = dev(256 * 64, 256), torch.empty(256, 256, device="cuda")
-    run("global_avg_pool_256x64x256", lambda: L.knx_hip_global_pool(1, P(c), 256, 64, 256, P(gp), S),
-        256 * 64 * 256 * 4 + 256 * 256 * 4)
-    xq = torch.empty(8192, 2048, dtype=torch.int8, device="cuda")
-    sx = torch.empty(8192, device="cuda")
-    run("quantize_rows_8192x2048", lambda: L.knx_hip_quantize_rows(P(h), 2048, 8192, 2048, 2048, P(xq), 2048, P(sx), S),
+    run("global_avg_pool_256x64x256", lambda: (rnd(256 * 64, 256), torch.empty(256, 256, device="cuda")),
+        lambda t: L.knx_hip_global_pool(1, P(t[0]), 256, 64, 256, P(t[1]), S), 256 * 64 * 256 * 4 + 256 * 256 * 4)
+    run("quantize_rows_8192x2048",
+        lambda: (rnd(8192, 2048), torch.empty(8192, 2048, dtype=torch.int8, device="cuda"), torch.empty(8192, device="cuda")),
+        lambda t: L.knx_hip_quantize_rows(P(t[0]), 2048, 8192, 2048, 2048, P(t[1]), 2048, P(t[2]), S),
         8192 * 2048 * 5 + 8192 * 4)
     return out
 
@@ -223,9 +289,42 @@ def measured_traffic():
         return None
 
 
-def forward_bench(name, make, flops, steps, warmup, mode="ref", i8_ops=0.0):
+def cpu_model_name():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_forward_baseline(path, xr, seq_len, threads, target_s):
+    """The reference's CPU forward path (oracle/cpu_forward.py, plain C) on `threads` host threads, on the first
+    samples of the same batch: samples/s, timed over about target_s seconds (at least one sample, whole forwards)."""
+    from oracle import knx_ref
+    from oracle.cpu_forward import CpuModel
+
+    cm = CpuModel(knx_ref.parse(path))
+    B = xr.shape[0] // seq_len
+    n = 1
+    t0 = time.perf_counter()
+    cm.forward(xr[: n * seq_len], threads)
+    per = max(time.perf_counter() - t0, 1e-6)
+    n = int(min(B, max(1, target_s / per)))
+    if n > 1:  # the batch the reference would run at once, within the time budget
+        t0 = time.perf_counter()
+        cm.forward(xr[: n * seq_len], threads)
+        per = (time.perf_counter() - t0) / n
+    return dict(value=round(1.0 / per, 1), unit="samples/s", cores=threads, kind="port",
+                sample=f"first {n} of the {B} samples, one forward")
+
+
+def forward_bench(name, make, flops, steps, warmup, mode="ref", i8_ops=0.0, cpu=None):
     """`flops` of one forward, `i8_ops` of them on the int8 MFMA (`i8` mode): the roofline time is the fp32 part at
-    the fp32 MFMA peak plus the int8 part at the int8 peak, and roofline_frac that time over the measured one."""
+    the fp32 MFMA peak plus the int8 part at the int8 peak, and roofline_frac that time over the measured one.
+    cpu: None, or (list of thread counts, seconds per measurement) for the CPU baseline of the same workload."""
     import numpy as np
     import torch
 
@@ -260,23 +359,31 @@ def forward_bench(name, make, flops, steps, warmup, mode="ref", i8_ops=0.0):
         for _ in range(n_e2e):
             m(x)
         e2e = (time.perf_counter() - t0) * 1e3 / n_e2e
+        seq = m.seq_len
         m.close()
+        base = {}
+        if cpu is not None:
+            threads, secs = cpu
+            for t in threads:
+                base[str(t)] = cpu_forward_baseline(path, xr, seq, t, secs)
     tf = flops / (ms * 1e-3) / 1e12
     ideal_ms = ((flops - i8_ops) / (PEAK_F32_TFLOPS * 1e12) + i8_ops / (PEAK_I8_TOPS * 1e12)) * 1e3
-    return dict(batch=B, ms=round(ms, 4), samples_per_s=round(B / (ms * 1e-3), 1),
-                e2e_ms=round(e2e, 3), e2e_samples_per_s=round(B / (e2e * 1e-3), 1),
-                tflops=round(tf, 2), roofline_frac=round(ideal_ms / ms, 4), mode=mode)
+    res = dict(batch=B, ms=round(ms, 4), samples_per_s=round(B / (ms * 1e-3), 1),
+               e2e_ms=round(e2e, 3), e2e_samples_per_s=round(B / (e2e * 1e-3), 1),
+               tflops=round(tf, 2), roofline_frac=round(ideal_ms / ms, 4), mode=mode)
+    if base:
+        res["cpu_baseline"] = base
+    return res
 
 
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    # the defaults give the clocks time to settle (a GEMM timed right after 5 warm-up launches reads ≈5% slower)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-forward", action="store_true")
-    ap.add_argument("--no-small", action="store_true", help="skip the small-M GEMM lines")
+    ap.add_argument("--no-small", action="store_true", help="skip the small-M GEMM, row, convolution, attention lines")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run a 256 MiB read (sum) and a 256 MiB copy: reference kernels of known HBM traffic for "
                          "scaling the FETCH_SIZE / WRITE_SIZE counters")
@@ -293,7 +400,10 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs the MI355X"
     log(f"device: {torch.cuda.get_device_name(0)}")
     g = i8gemm_bench(4096, args.steps, args.warmup)
-    log(f"i8gemm M=4096: {g['ms'] * 1e3:.1f} us  {g['tops']:.1f} TOPS")
+    log(f"i8gemm M=4096: sustained {g['ms'] * 1e3:.1f} us ({g['tops']:.1f} TOPS; windows median "
+        f"{g['ms_median'] * 1e3:.1f}, p10-p90 {g['ms_p10'] * 1e3:.1f}-{g['ms_p90'] * 1e3:.1f} us), burst "
+        f"{g['burst_ms'] * 1e3:.1f} us "
+        f"({g['burst_tops']:.1f} TOPS)")
     if args.calibrate:
         n = 256 << 20
         src = torch.ones(n // 4, dtype=torch.float32, device="cuda")
@@ -305,10 +415,15 @@ def main():
         log(f"calibration: {n} byte read (sum) and {n} byte copy issued 3 times")
     small = {}
     for M in (() if args.no_small else (1, 16, 256)):
-        r = i8gemm_bench(M, max(args.steps, 20), args.warmup)
-        small[str(M)] = dict(us=round(r["ms"] * 1e3, 2), tops=round(r["tops"], 2), gbs=round(r["gbs"], 1),
-                             hbm_frac=round(r["gbs"] / PEAK_HBM_GBS, 4))
-        log(f"i8gemm M={M}: {r['ms'] * 1e3:.2f} us  {r['gbs']:.0f} GB/s algorithmic")
+        entry = {}
+        for mode, rot in (("cached", 0), ("hbm", ROTATE_BYTES)):
+            r = i8gemm_bench(M, max(args.steps, 50), max(args.warmup, 20), sustained=False, rotate_bytes=rot)
+            entry[mode] = dict(us=round(r["burst_ms"] * 1e3, 2), tops=round(r["burst_tops"], 2),
+                               gbs=round(r["algo_bytes"] / (r["burst_ms"] * 1e-3) / 1e9, 1),
+                               hbm_frac=round(r["algo_bytes"] / (r["burst_ms"] * 1e-3) / 1e9 / PEAK_HBM_GBS, 4))
+            log(f"i8gemm M={M} {mode}: {r['burst_ms'] * 1e3:.2f} us  {entry[mode]['gbs']:.0f} GB/s algorithmic")
+        entry["bytes"] = int(configs.i8gemm_work(M)[1])
+        small[str(M)] = entry
 
     out = {
         "metric": METRIC,
@@ -327,30 +442,38 @@ def main():
                    "M": 4096, "N": 4096, "K": 4096},
         "roofline": {"bound": "mfma", "achieved": round(g["tops"], 2), "peak": PEAK_I8_TOPS, "unit": "TOP/s",
                      "frac": round(g["tops"] / PEAK_I8_TOPS, 4), "traffic": measured_traffic(),
-                     "kernel_us": round(g["ms"] * 1e3, 2)},
+                     "kernel_us": round(g["ms"] * 1e3, 2),
+                     "timing": "sustained: the K timed launches follow at least 200 ms of back-to-back launches",
+                     "windows_us": {"median": round(g["ms_median"] * 1e3, 2), "p10": round(g["ms_p10"] * 1e3, 2),
+                                    "p90": round(g["ms_p90"] * 1e3, 2), "windows": 20, "launches_per_window": 50}},
+        "burst": {"steps": args.steps, "warmup": args.warmup, "kernel_us": round(g["burst_ms"] * 1e3, 2),
+                  "tops": round(g["burst_tops"], 2), "frac": round(g["burst_tops"] / PEAK_I8_TOPS, 4)},
     }
+    ncpu = len(os.sched_getaffinity(0))
+    threads = [8] + ([ncpu] if ncpu != 8 else [])
     if not args.no_cpu:
         c8 = cpu_baseline(g, 8)
         out["cpu_baseline"] = {"value": round(c8["tops"], 4), "unit": "TOPS", "cores": 8, "kind": "port",
                                "sample": f"oracle int8 GEMM (plain C, -O3), rows 0..{c8['rows'] - 1} of the "
                                          f"M=4096 workload ({c8['rows']}x4096x4096), mean of {c8['reps']}",
-                               "gpu_rows_bit_exact": c8["bit_exact"]}
+                               "gpu_rows_bit_exact": c8["bit_exact"], "cpu": cpu_model_name()}
         log(f"cpu 8 threads: {c8['tops'] * 1e3:.1f} GOPS, GPU rows bit-exact: {c8['bit_exact']}")
-        ncpu = len(os.sched_getaffinity(0))
         if ncpu != 8:
             cn = cpu_baseline(g, ncpu, target_s=5.0)
             out["cpu_baseline_all_cores"] = {"value": round(cn["tops"], 4), "unit": "TOPS", "cores": ncpu}
     out["i8gemm_small_m"] = small
     if not args.no_small:
-        out["row_kernels"] = rows_bench(max(args.steps, 20), args.warmup)
-        out["conv_layers"] = conv_bench(max(args.steps // 4, 10), max(args.warmup // 10, 3))
-        out["attention_core"] = attention_bench(max(args.steps // 4, 10), max(args.warmup // 10, 3))
+        out["row_kernels"] = rows_bench(max(args.steps, 50), max(args.warmup, 20))
+        out["conv_layers"] = conv_bench(max(args.steps, 20), max(args.warmup, 3))
+        out["attention_core"] = attention_bench(max(args.steps, 20), max(args.warmup, 3))
     if not args.no_forward:
         fw = {}
-        st = max(5, args.steps // 5)
-        fwarm = max(3, args.warmup // 10)
+        st = max(10, args.steps)
+        fwarm = max(3, args.warmup)
+        cpu = None if args.no_cpu else (threads, 2.0)
         fw["int8_mlp_784_512_256_10_b64"] = forward_bench(
-            "mlp", lambda p: configs.int8_mlp(p, batch=64), configs.mlp_flops(64, (784, 512, 256, 10)), st, fwarm)
+            "mlp", lambda p: configs.int8_mlp(p, batch=64), configs.mlp_flops(64, (784, 512, 256, 10)), st, fwarm,
+            cpu=cpu)
         # batch 1: the reference's int8 latency path (int8 arithmetic at ≤ 2 rows), quantize fused into the GEMM
         fw["int8_mlp_784_512_256_10_b1"] = forward_bench(
             "mlp", lambda p: configs.int8_mlp(p, batch=1), configs.mlp_flops(1, (784, 512, 256, 10)), st, fwarm,
@@ -359,16 +482,24 @@ def main():
             "mlp", lambda p: configs.int8_mlp(p, batch=64), configs.mlp_flops(64, (784, 512, 256, 10)), st, fwarm,
             mode="i8", i8_ops=configs.mlp_flops(64, (784, 512, 256, 10)))
         fw["fp32_mlp_4096_4096_4096_1000_b8192"] = forward_bench(
-            "f32", lambda p: configs.fp32_mlp(p), configs.mlp_flops(8192, (4096, 4096, 4096, 1000)), st, fwarm)
-        fw["cnn_b256"] = forward_bench("cnn", lambda p: configs.cnn(p), configs.cnn_flops(), st, fwarm)
+            "f32", lambda p: configs.fp32_mlp(p), configs.mlp_flops(8192, (4096, 4096, 4096, 1000)), st, fwarm,
+            cpu=cpu)
+        fw["cnn_b256"] = forward_bench("cnn", lambda p: configs.cnn(p), configs.cnn_flops(), st, fwarm, cpu=cpu)
         fw["transformer_4l_d512_b64"] = forward_bench(
-            "tr", lambda p: configs.transformer(p), configs.transformer_flops(), st, fwarm)
+            "tr", lambda p: configs.transformer(p), configs.transformer_flops(), st, fwarm, cpu=cpu)
         fw["transformer_4l_d512_b64_i8"] = forward_bench(
             "tr", lambda p: configs.transformer(p), configs.transformer_flops(), st, fwarm, mode="i8",
             i8_ops=configs.transformer_ffn_flops())
         for k, v in fw.items():
-            log(f"forward {k}: {v['ms']:.3f} ms  {v['samples_per_s']:.0f} samples/s  {v['tflops']:.1f} TFLOP/s")
+            cpu_txt = ""
+            if "cpu_baseline" in v:
+                cpu_txt = "  cpu " + ", ".join(f"{c['value']:.0f}/s on {t}" for t, c in v["cpu_baseline"].items())
+            log(f"forward {k}: {v['ms']:.3f} ms  {v['samples_per_s']:.0f} samples/s  {v['tflops']:.1f} TFLOP/s{cpu_txt}")
         out["forward"] = fw
+        if not args.no_cpu:
+            out["forward_cpu"] = {"cpu": cpu_model_name(), "threads": threads,
+                                  "path": "oracle/cpu_forward.py: fp32 native GEMM, im2col convolution, row ops, "
+                                          "int8 kernel at <= 2 rows (the reference's CPU dispatch), plain C"}
     print(json.dumps(out), flush=True)
 
 
