@@ -376,6 +376,70 @@ def forward_bench(name, make, flops, steps, warmup, mode="ref", i8_ops=0.0, cpu=
     return res
 
 
+def run_parts(args, out, want, configs):
+    """the lines beside the headline: small-M GEMMs, row kernels, convolutions, attention, .knx forwards"""
+    ncpu = len(os.sched_getaffinity(0))
+    threads = [8] + ([ncpu] if ncpu != 8 else [])
+    # profiling runs (--no-sustained) take the launch counts as given; otherwise enough launches for stable figures
+    few = args.no_sustained
+    n_small = (args.steps, args.warmup) if few else (max(args.steps, 50), max(args.warmup, 20))
+    n_layer = (args.steps, args.warmup) if few else (max(args.steps, 20), max(args.warmup, 3))
+    small = {}
+    for M in (() if args.no_small or not want("gemm_small") else (1, 16, 256)):
+        entry = {}
+        for mode, rot in (("cached", 0), ("hbm", ROTATE_BYTES)):
+            r = i8gemm_bench(M, n_small[0], n_small[1], sustained=False, rotate_bytes=rot)
+            entry[mode] = dict(us=round(r["burst_ms"] * 1e3, 2), tops=round(r["burst_tops"], 2),
+                               gbs=round(r["algo_bytes"] / (r["burst_ms"] * 1e-3) / 1e9, 1),
+                               hbm_frac=round(r["algo_bytes"] / (r["burst_ms"] * 1e-3) / 1e9 / PEAK_HBM_GBS, 4))
+            log(f"i8gemm M={M} {mode}: {r['burst_ms'] * 1e3:.2f} us  {entry[mode]['gbs']:.0f} GB/s algorithmic")
+        entry["bytes"] = int(configs.i8gemm_work(M)[1])
+        small[str(M)] = entry
+
+    if small:
+        out["i8gemm_small_m"] = small
+    if not args.no_small and want("rows"):
+        out["row_kernels"] = rows_bench(*n_small)
+    if not args.no_small and want("conv"):
+        out["conv_layers"] = conv_bench(*n_layer)
+    if not args.no_small and want("attention"):
+        out["attention_core"] = attention_bench(*n_layer)
+    if not args.no_forward and want("forward"):
+        fw = {}
+        st = max(10, args.steps)
+        fwarm = max(3, args.warmup)
+        cpu = None if args.no_cpu else (threads, 2.0)
+        fw["int8_mlp_784_512_256_10_b64"] = forward_bench(
+            "mlp", lambda p: configs.int8_mlp(p, batch=64), configs.mlp_flops(64, (784, 512, 256, 10)), st, fwarm,
+            cpu=cpu)
+        # batch 1: the reference's int8 latency path (int8 arithmetic at ≤ 2 rows), quantize fused into the GEMM
+        fw["int8_mlp_784_512_256_10_b1"] = forward_bench(
+            "mlp", lambda p: configs.int8_mlp(p, batch=1), configs.mlp_flops(1, (784, 512, 256, 10)), st, fwarm,
+            i8_ops=configs.mlp_flops(1, (784, 512, 256, 10)))
+        fw["int8_mlp_784_512_256_10_b64_i8"] = forward_bench(
+            "mlp", lambda p: configs.int8_mlp(p, batch=64), configs.mlp_flops(64, (784, 512, 256, 10)), st, fwarm,
+            mode="i8", i8_ops=configs.mlp_flops(64, (784, 512, 256, 10)))
+        fw["fp32_mlp_4096_4096_4096_1000_b8192"] = forward_bench(
+            "f32", lambda p: configs.fp32_mlp(p), configs.mlp_flops(8192, (4096, 4096, 4096, 1000)), st, fwarm,
+            cpu=cpu)
+        fw["cnn_b256"] = forward_bench("cnn", lambda p: configs.cnn(p), configs.cnn_flops(), st, fwarm, cpu=cpu)
+        fw["transformer_4l_d512_b64"] = forward_bench(
+            "tr", lambda p: configs.transformer(p), configs.transformer_flops(), st, fwarm, cpu=cpu)
+        fw["transformer_4l_d512_b64_i8"] = forward_bench(
+            "tr", lambda p: configs.transformer(p), configs.transformer_flops(), st, fwarm, mode="i8",
+            i8_ops=configs.transformer_ffn_flops())
+        for k, v in fw.items():
+            cpu_txt = ""
+            if "cpu_baseline" in v:
+                cpu_txt = "  cpu " + ", ".join(f"{c['value']:.0f}/s on {t}" for t, c in v["cpu_baseline"].items())
+            log(f"forward {k}: {v['ms']:.3f} ms  {v['samples_per_s']:.0f} samples/s  {v['tflops']:.1f} TFLOP/s{cpu_txt}")
+        out["forward"] = fw
+        if not args.no_cpu:
+            out["forward_cpu"] = {"cpu": cpu_model_name(), "threads": threads,
+                                  "path": "oracle/cpu_forward.py: fp32 native GEMM, im2col convolution, row ops, "
+                                          "int8 kernel at <= 2 rows (the reference's CPU dispatch), plain C"}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -384,6 +448,11 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-forward", action="store_true")
     ap.add_argument("--no-small", action="store_true", help="skip the small-M GEMM, row, convolution, attention lines")
+    ap.add_argument("--only", default="",
+                    help="comma-separated subset for profiling runs: gemm4096, gemm_small, rows, conv, attention, "
+                         "forward (the JSON line then lacks the parts not run)")
+    ap.add_argument("--no-sustained", action="store_true",
+                    help="time the headline GEMM only in the burst form (profiling runs with few launches)")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run a 256 MiB read (sum) and a 256 MiB copy: reference kernels of known HBM traffic for "
                          "scaling the FETCH_SIZE / WRITE_SIZE counters")
@@ -399,12 +468,11 @@ def main():
 
     assert torch.cuda.is_available(), "bench.py needs the MI355X"
     log(f"device: {torch.cuda.get_device_name(0)}")
-    g = i8gemm_bench(4096, args.steps, args.warmup)
-    log(f"i8gemm M=4096: sustained {g['ms'] * 1e3:.1f} us ({g['tops']:.1f} TOPS; windows median "
-        f"{g['ms_median'] * 1e3:.1f}, p10-p90 {g['ms_p10'] * 1e3:.1f}-{g['ms_p90'] * 1e3:.1f} us), burst "
-        f"{g['burst_ms'] * 1e3:.1f} us "
-        f"({g['burst_tops']:.1f} TOPS)")
-    if args.calibrate:
+    only = set(filter(None, args.only.split(",")))
+    want = lambda part: not only or part in only  # noqa: E731
+    if only and "gemm4096" not in only:
+        args.no_cpu = True
+    if args.calibrate:  # kernels of known traffic, in the same process as the kernels profiled
         n = 256 << 20
         src = torch.ones(n // 4, dtype=torch.float32, device="cuda")
         dst = torch.empty_like(src)
@@ -413,18 +481,16 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         log(f"calibration: {n} byte read (sum) and {n} byte copy issued 3 times")
-    small = {}
-    for M in (() if args.no_small else (1, 16, 256)):
-        entry = {}
-        for mode, rot in (("cached", 0), ("hbm", ROTATE_BYTES)):
-            r = i8gemm_bench(M, max(args.steps, 50), max(args.warmup, 20), sustained=False, rotate_bytes=rot)
-            entry[mode] = dict(us=round(r["burst_ms"] * 1e3, 2), tops=round(r["burst_tops"], 2),
-                               gbs=round(r["algo_bytes"] / (r["burst_ms"] * 1e-3) / 1e9, 1),
-                               hbm_frac=round(r["algo_bytes"] / (r["burst_ms"] * 1e-3) / 1e9 / PEAK_HBM_GBS, 4))
-            log(f"i8gemm M={M} {mode}: {r['burst_ms'] * 1e3:.2f} us  {entry[mode]['gbs']:.0f} GB/s algorithmic")
-        entry["bytes"] = int(configs.i8gemm_work(M)[1])
-        small[str(M)] = entry
-
+    g = i8gemm_bench(4096, args.steps, args.warmup, sustained=not args.no_sustained) if want("gemm4096") else None
+    if g is None:
+        out = {"metric": METRIC, "only": sorted(only)}
+        run_parts(args, out, want, configs)
+        print(json.dumps(out), flush=True)
+        return
+    log(f"i8gemm M=4096: sustained {g['ms'] * 1e3:.1f} us ({g['tops']:.1f} TOPS; windows median "
+        f"{g['ms_median'] * 1e3:.1f}, p10-p90 {g['ms_p10'] * 1e3:.1f}-{g['ms_p90'] * 1e3:.1f} us), burst "
+        f"{g['burst_ms'] * 1e3:.1f} us "
+        f"({g['burst_tops']:.1f} TOPS)")
     out = {
         "metric": METRIC,
         "value": round(g["tops"], 2),
@@ -461,45 +527,7 @@ def main():
         if ncpu != 8:
             cn = cpu_baseline(g, ncpu, target_s=5.0)
             out["cpu_baseline_all_cores"] = {"value": round(cn["tops"], 4), "unit": "TOPS", "cores": ncpu}
-    out["i8gemm_small_m"] = small
-    if not args.no_small:
-        out["row_kernels"] = rows_bench(max(args.steps, 50), max(args.warmup, 20))
-        out["conv_layers"] = conv_bench(max(args.steps, 20), max(args.warmup, 3))
-        out["attention_core"] = attention_bench(max(args.steps, 20), max(args.warmup, 3))
-    if not args.no_forward:
-        fw = {}
-        st = max(10, args.steps)
-        fwarm = max(3, args.warmup)
-        cpu = None if args.no_cpu else (threads, 2.0)
-        fw["int8_mlp_784_512_256_10_b64"] = forward_bench(
-            "mlp", lambda p: configs.int8_mlp(p, batch=64), configs.mlp_flops(64, (784, 512, 256, 10)), st, fwarm,
-            cpu=cpu)
-        # batch 1: the reference's int8 latency path (int8 arithmetic at ≤ 2 rows), quantize fused into the GEMM
-        fw["int8_mlp_784_512_256_10_b1"] = forward_bench(
-            "mlp", lambda p: configs.int8_mlp(p, batch=1), configs.mlp_flops(1, (784, 512, 256, 10)), st, fwarm,
-            i8_ops=configs.mlp_flops(1, (784, 512, 256, 10)))
-        fw["int8_mlp_784_512_256_10_b64_i8"] = forward_bench(
-            "mlp", lambda p: configs.int8_mlp(p, batch=64), configs.mlp_flops(64, (784, 512, 256, 10)), st, fwarm,
-            mode="i8", i8_ops=configs.mlp_flops(64, (784, 512, 256, 10)))
-        fw["fp32_mlp_4096_4096_4096_1000_b8192"] = forward_bench(
-            "f32", lambda p: configs.fp32_mlp(p), configs.mlp_flops(8192, (4096, 4096, 4096, 1000)), st, fwarm,
-            cpu=cpu)
-        fw["cnn_b256"] = forward_bench("cnn", lambda p: configs.cnn(p), configs.cnn_flops(), st, fwarm, cpu=cpu)
-        fw["transformer_4l_d512_b64"] = forward_bench(
-            "tr", lambda p: configs.transformer(p), configs.transformer_flops(), st, fwarm, cpu=cpu)
-        fw["transformer_4l_d512_b64_i8"] = forward_bench(
-            "tr", lambda p: configs.transformer(p), configs.transformer_flops(), st, fwarm, mode="i8",
-            i8_ops=configs.transformer_ffn_flops())
-        for k, v in fw.items():
-            cpu_txt = ""
-            if "cpu_baseline" in v:
-                cpu_txt = "  cpu " + ", ".join(f"{c['value']:.0f}/s on {t}" for t, c in v["cpu_baseline"].items())
-            log(f"forward {k}: {v['ms']:.3f} ms  {v['samples_per_s']:.0f} samples/s  {v['tflops']:.1f} TFLOP/s{cpu_txt}")
-        out["forward"] = fw
-        if not args.no_cpu:
-            out["forward_cpu"] = {"cpu": cpu_model_name(), "threads": threads,
-                                  "path": "oracle/cpu_forward.py: fp32 native GEMM, im2col convolution, row ops, "
-                                          "int8 kernel at <= 2 rows (the reference's CPU dispatch), plain C"}
+    run_parts(args, out, want, configs)
     print(json.dumps(out), flush=True)
 
 
