@@ -274,35 +274,64 @@ __global__ void __launch_bounds__(WM * WN * 64) sgemm_k32(SgArgs p)
     const int lda4 = p.lda * 4, ldb4 = p.ldb * 4;  // row strides in bytes
     const int cl = (lane & 7) ^ (lane >> 3), rs = lane >> 3;
     const int nk = p.K / 32;
-    // convolution: the output pixel of this lane's row in every A slot (fixed over K) as (b, oy·sh − pt, ox·sw − pl)
+    // Convolution: k-tile kt is 32 consecutive channels of one tap (the group's channel count cg is a multiple of 32),
+    // taps in (ky, kx) order.  Per A slot, fixed over K: the byte address of this lane's 16-byte chunk at tap (0, 0),
+    // channel 0 of the group (an integer: it lies outside x when the pixel's window starts in the padding), and the
+    // taps whose input pixel is inside the image as a mask, bit ky·kw + kx (at most 64 taps).  The k-tiles are issued
+    // in order, so a cursor (tap, k-tile within the tap, byte offset of the k-tile from tap (0, 0), channel 0) moves
+    // one k-tile per issue round: no divisions in the loop, and per slot one 64-bit add, a mask test and a select.
     constexpr int SAC = CONV ? SA : 1;
-    int pb[SAC], piy[SAC], pix[SAC];
+    unsigned long long at0[SAC], inside[SAC];
+    int ctap = 0, ckt = 0, ckx = 0;
+    long long coff = 0;
+    // the zero line's address, read once: an opaque register value, so that the compiler does not load it again from
+    // the global offset table in every k-tile (that load would sit in front of the k-tile's wait)
+    unsigned long long zero_at;
+    asm volatile("" : "=s"(zero_at) : "0"((unsigned long long)(uintptr_t)knx_zero_line));
     if (CONV) {
         const knx_conv_geom& g = p.cv;
 #pragma unroll
         for (int i = 0; i < SAC; ++i) {
-            const int m = m0 + (i * NW + wave) * 8 + rs;
-            const int ox = m % g.Wo, oy = (m / g.Wo) % g.Ho;
-            pb[i] = m / (g.Wo * g.Ho);
-            piy[i] = oy * g.sh - g.pt;
-            pix[i] = ox * g.sw - g.pl;
+            const int slot = i * NW + wave;
+            const int m = m0 + slot * 8 + rs;
+            const int ox = m % g.Wo, oy = (m / g.Wo) % g.Ho, b = m / (g.Wo * g.Ho);
+            const int iy = oy * g.sh - g.pt, ix = ox * g.sw - g.pl;
+            const long long e = (((long long)b * g.H + iy) * g.W + ix) * g.C + cbase;
+            at0[i] = (unsigned long long)(uintptr_t)A + (unsigned long long)(e * 4) + (unsigned)((cl ^ (slot & 7)) * 16);
+            unsigned long long bits = 0;
+            for (int ky = 0; ky < g.kh; ++ky) {
+                const int y = iy + ky * g.dh;
+                if (y < 0 || y >= g.H) continue;
+                for (int kx = 0; kx < g.kw; ++kx) {
+                    const int x = ix + kx * g.dw;
+                    if (x >= 0 && x < g.W) bits |= 1ull << (ky * g.kw + kx);
+                }
+            }
+            inside[i] = bits;
         }
     }
+    auto conv_next = [&]() {  // cursor to the next k-tile
+        const knx_conv_geom& g = p.cv;
+        coff += 128;
+        if (++ckt == p.cgc / 32) {
+            ckt = 0;
+            ++ctap;
+            coff += (long long)g.dw * g.C * 4 - p.cgc * 4;
+            if (++ckx == g.kw) {
+                ckx = 0;
+                coff += ((long long)g.dh * g.W - (long long)g.kw * g.dw) * g.C * 4;
+            }
+        }
+    };
     auto issue1 = [&](int kt, int i) {
         const int slot = i * NW + wave;
         const bool a = i < SA;
         const int chunk = cl ^ (slot & 7);
         int8_t* dst = lds + (kt % STG) * STAGE + slot * 1024;
         if (CONV && a) {
-            // k-tile kt is 32 consecutive channels of one tap (the group's channel count is a multiple of 32)
-            const knx_conv_geom& g = p.cv;
-            const int k0 = kt * 32, seg = k0 / p.cgc, ci0 = k0 - seg * p.cgc;
-            const int ky = seg / g.kw, kx = seg - ky * g.kw;
-            const int iy = piy[i] + ky * g.dh, ix = pix[i] + kx * g.dw;
-            const bool in = iy >= 0 && iy < g.H && ix >= 0 && ix < g.W;
-            const int8_t* src = in ? reinterpret_cast<const int8_t*>(A + (((size_t)pb[i] * g.H + iy) * g.W + ix) * g.C + cbase + ci0) + chunk * 16
-                                   : knx_zero_line + chunk * 16;
-            dma16_at(src, dst);
+            const bool in = (inside[i] >> ctap) & 1;
+            const unsigned long long src = in ? at0[i] + (unsigned long long)coff : zero_at;
+            dma16_at(reinterpret_cast<const void*>(src), dst);
             return;
         }
         const int ld = a ? lda4 : ldb4;
@@ -388,18 +417,22 @@ __global__ void __launch_bounds__(WM * WN * 64) sgemm_k32(SgArgs p)
             }
             __builtin_amdgcn_sched_barrier(0);
         }
+        if (CONV && iss) conv_next();
     };
     using yes = std::integral_constant<bool, true>;
     using no = std::integral_constant<bool, false>;
 #pragma unroll
     for (int i = 0; i < SLOTS; ++i) issue1(0, i);
+    if (CONV) conv_next();
     int kt = 0;
     if (STG == 2) {
         KNX_WAIT_VM_LDS(0);
         knx_barrier_nofence();
-        if (nk > 1)
+        if (nk > 1) {
 #pragma unroll
             for (int i = 0; i < SLOTS; ++i) issue1(1, i);
+            if (CONV) conv_next();
+        }
 #pragma unroll
         for (int j = 0; j < NR; ++j) read1(0, 0, j);
         for (; kt < nk - 2; ++kt) ktile(kt, yes{}, yes{}, no{});
@@ -409,14 +442,17 @@ __global__ void __launch_bounds__(WM * WN * 64) sgemm_k32(SgArgs p)
         if (nk > 1) {
 #pragma unroll
             for (int i = 0; i < SLOTS; ++i) issue1(1, i);
+            if (CONV) conv_next();
             KNX_WAIT_VM_LDS(SLOTS);
         } else {
             KNX_WAIT_VM_LDS(0);
         }
         knx_barrier_nofence();
-        if (nk > 2)
+        if (nk > 2) {
 #pragma unroll
             for (int i = 0; i < SLOTS; ++i) issue1(2, i);
+            if (CONV) conv_next();
+        }
 #pragma unroll
         for (int j = 0; j < NR; ++j) read1(0, 0, j);
         for (; kt < nk - 3; ++kt) ktile(kt, yes{}, yes{}, yes{});
@@ -681,13 +717,13 @@ int dispatch_nt(SgArgs p, int batch, hipStream_t s, const char* name)
     return dispatch<true>(p, batch, s, name);
 }
 
-template <int BM, int BN, int WM, int WN>
+template <int BM, int BN, int WM, int WN, int STG = 2>
 int launch_conv_k32(SgArgs p, hipStream_t s, const char* name)
 {
     p.tiles_m = (p.M + BM - 1) / BM;
     p.tiles_n = (p.N + BN - 1) / BN;
     const unsigned tiles = (unsigned)p.tiles_m * (unsigned)p.tiles_n;
-    hipLaunchKernelGGL((sgemm_k32<BM, BN, WM, WN, true>), dim3(tiles, p.cv.groups), dim3(WM * WN * 64), 0, s, p);
+    hipLaunchKernelGGL((sgemm_k32<BM, BN, WM, WN, true, STG>), dim3(tiles, p.cv.groups), dim3(WM * WN * 64), 0, s, p);
     return knx::check_launch(name);
 }
 
@@ -701,7 +737,8 @@ int knx_conv_k32(const knx_conv_geom* g, const float* x, const float* wt, const 
 {
     const int cg = g->C / g->groups, N = g->Co / g->groups;
     const long M = (long)g->B * g->Ho * g->Wo;
-    if (cg % 32 != 0 || ((uintptr_t)x & 15) != 0 || ((uintptr_t)wt & 15) != 0 || M > 0x7fffffffL) return 1;
+    if (cg % 32 != 0 || ((uintptr_t)x & 15) != 0 || ((uintptr_t)wt & 15) != 0 || M > 0x7fffffffL || g->kh * g->kw > 64)
+        return 1;
     const char* force = getenv("KNX_SGEMM_KERNEL");
     if (force != nullptr && strcmp(force, "general") == 0) return 1;
     SgArgs p{};
@@ -718,15 +755,19 @@ int knx_conv_k32(const knx_conv_geom* g, const float* x, const float* wt, const 
         if (strcmp(tile, "256x256") == 0 && N >= 256 && M >= 256) return launch_conv_k32<256, 256, 4, 2>(p, s, name);
         if (strcmp(tile, "256x128") == 0 && N >= 128 && M >= 256) return launch_conv_k32<256, 128, 4, 2>(p, s, name);
         if (strcmp(tile, "128x128") == 0 && N >= 128 && M >= 128) return launch_conv_k32<128, 128, 2, 2>(p, s, name);
+        if (strcmp(tile, "64x128") == 0 && N >= 128 && M >= 64) return launch_conv_k32<64, 128, 2, 2>(p, s, name);
         if (strcmp(tile, "256x64") == 0 && N >= 64 && M >= 256) return launch_conv_k32<256, 64, 4, 1>(p, s, name);
-        if (strcmp(tile, "128x64") == 0 && N >= 64 && M >= 128) return launch_conv_k32<128, 64, 4, 1>(p, s, name);
-        if (strcmp(tile, "128x64w2") == 0 && N >= 64 && M >= 128) return launch_conv_k32<128, 64, 2, 2>(p, s, name);
+        if (strcmp(tile, "128x64") == 0 && N >= 64 && M >= 128) return launch_conv_k32<128, 64, 2, 2>(p, s, name);
     }
     if (N >= 256 && M >= 256 && tiles(256, 256) >= cus) return launch_conv_k32<256, 256, 4, 2>(p, s, name);
+    // 128 or more output channels: 64×128 tiles when that gives every CU two or more workgroups, so that one's
+    // prologue and epilogue overlap another's multiplies (CNN conv3, 256×32×32×64 → 128 stride 2: 84 µs as against 84
+    // for 256×128; conv4, 256×16×16×128 → 256 stride 2: 80 µs against 84 for 128×128)
+    if (N >= 128 && M >= 64 && tiles(64, 128) >= 2 * cus) return launch_conv_k32<64, 128, 2, 2>(p, s, name);
     if (N >= 128 && M >= 256 && tiles(256, 128) >= cus) return launch_conv_k32<256, 128, 4, 2>(p, s, name);
     if (N >= 128 && M >= 128 && tiles(128, 128) >= cus) return launch_conv_k32<128, 128, 2, 2>(p, s, name);
-    // 64 output channels: 128×64 tiles on 2×2 waves (CNN conv2, 256×32×32×64 → 64: 189 µs against 209-225 for
-    // 256×64), several workgroups per CU
+    // 64 output channels: 128×64 tiles on 2×2 waves, several workgroups per CU (CNN conv2, 256×32×32×64 → 64:
+    // 169 µs, the same as 64×64 and 128×64 on 4×1 waves, against 174 for 256×64)
     if (N >= 64 && M >= 128 && tiles(128, 64) >= 2 * cus) return launch_conv_k32<128, 64, 2, 2>(p, s, name);
     if (N >= 64 && M >= 256 && tiles(256, 64) >= cus) return launch_conv_k32<256, 64, 4, 1>(p, s, name);
     return 1;

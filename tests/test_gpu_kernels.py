@@ -513,9 +513,14 @@ def test_conv_residual(L, case):
     assert np.array_equal(host(dR), host(y))
 
 
-CONV_TILES = ["256x256", "256x128", "128x128", "256x64", "128x64", "128x64w2"]
+CONV_TILES = ["256x256", "256x128", "128x128", "64x128", "256x64", "128x64"]
+# the tap mask of the pipelined gather: 1 tap, 25 taps, 49 (bits past 32), and 81 taps (more than the mask holds:
+# the general kernel); output pixels not a multiple of the tile
 CONV_TILE_CASES = [(64, 32, 32, 64, 64, 3, 1, 1, 1, 1), (128, 16, 16, 64, 128, 3, 1, 1, 1, 1),
-                   (256, 16, 16, 128, 256, 3, 2, 1, 1, 1), (128, 16, 16, 128, 128, 3, 1, 1, 2, 1)]
+                   (256, 16, 16, 128, 256, 3, 2, 1, 1, 1), (128, 16, 16, 128, 128, 3, 1, 1, 2, 1),
+                   (4, 15, 13, 64, 128, 1, 1, 0, 1, 1), (4, 12, 12, 64, 64, 5, 1, 2, 1, 1),
+                   (4, 14, 14, 32, 64, 7, 1, 3, 1, 1), (3, 11, 12, 32, 128, 7, 2, 2, 1, 1),
+                   (2, 12, 12, 32, 64, 9, 1, 4, 1, 1)]
 
 
 @pytest.mark.parametrize("tile", CONV_TILES)
