@@ -4,7 +4,7 @@
 // the loop body of kernix_attention_run (reference include/kernix_model.h:1021-1046).  The Q/K/V/O projections
 // are ordinary Linear GEMMs run by the host (knx_hip_sgemm_ep).
 //
-// Paths: for dk = dv ∈ {32, 64, 128} and S ≤ 256 (S ≤ 128 at 128) one fused kernel keeps each head's K and Vᵀ in
+// Paths: for dk = dv ∈ {32, 64, 128} and S ≤ 256 (S ≤ 128 at 128) one fused kernel keeps each head's K and V in
 // LDS and the scores in registers, so nothing but Q, K, V and the context touches HBM.  Otherwise one batched NT
 // MFMA GEMM writes all B·H score matrices (alpha = scale and the causal mask fused in its epilogue), the wavefront
 // softmax normalizes each row in place, and one batched GEMM multiplies by V and writes the context directly in the
@@ -13,7 +13,9 @@
 #include <stdlib.h>
 #include <string.h>
 
-#include "knx_common.hpp"
+#include <utility>
+
+#include "knx_pipe.hpp"
 
 int knx_sgemm_batched(int M, int N, int K, const float* A, int lda, long long sAb, long long sAh, const float* B, int ldb,
                       long long sBb, long long sBh, bool transB, float* C, int ldc, long long sCb, long long sCh, int nb,
@@ -43,62 +45,99 @@ __global__ void __launch_bounds__(256) transpose_kernel(const float* __restrict_
 
 typedef float v16f __attribute__((ext_vector_type(16)));
 
-// Fused attention for sequences of at most 32·NS keys, dk = DK, dv = DV.  One block per (b·h, 128 queries): K_h
-// (row pitch DK + 4) and V_hᵀ (row pitch 32·NS + 4) of the whole sequence are staged in LDS, zero beyond S; each
-// wave owns 32 queries.  It computes Sᵀ = K_h·Q_hᵀ on 32×32×2 fp32 MFMA, so its accumulators hold, per lane, one
-// query (lane & 31) and 16 keys of each 32-key tile: the row max and sum of the softmax need one exchange between
-// the two half-waves, and the normalized probabilities are already the B operand of ctxᵀ = V_hᵀ·Pᵀ.  Keys beyond S
+// f(integral_constant<int, t>) for t = 0, 1, …: a loop whose index is a compile-time constant in the body
+template <typename F, int... T>
+__device__ __forceinline__ void unrolled(F&& f, std::integer_sequence<int, T...>)
+{
+    (f(std::integral_constant<int, T>{}), ...);
+}
+
+// 16 zero bytes: the source of the staged chunks of keys beyond S
+__device__ __attribute__((aligned(16))) float knx_attn_zero[4];
+
+// Fused attention for sequences of at most 32·NS keys, dk = dv = D ∈ {32, 64, 128}.  One block per (b·h, 128
+// queries), each wave owns 32 queries.  K_h and V_h of the whole sequence (zero beyond S) are staged in LDS by
+// LDS-DMA (global_load_lds, 16 bytes per lane), both row-major in 16-byte chunks with a per-row chunk swizzle, one
+// 32-key tile after another: the K tiles first, then the V tiles.  The wave computes Sᵀ = K_h·Q_hᵀ on 32×32×2 fp32
+// MFMA tile by tile, each tile as soon as its keys have arrived, while the later K tiles and all of V are still in
+// flight; its accumulators hold, per lane, one query (lane & 31) and 16 keys of each 32-key tile, so the row max and
+// sum of the softmax need one exchange between the two half-waves, and the normalized probabilities are already the
+// B operand of ctxᵀ = V_hᵀ·Pᵀ, whose A operand is read from the row-major V one float at a time.  Keys beyond S
 // count as −inf, which leaves max, sum and probabilities as they are over the S keys alone.
+//
+// LDS layout (16-byte chunk c of key row r), conflict-free for both products:
+//   K: chunk position r·CPR + (c ^ sk(r)), sk(r) = r mod 16 (CPR = D/4 ≥ 16) or (r/2) mod 8 (CPR = 8): the 16 rows
+//      one quarter-wave reads at one logical chunk fall on 16 distinct 16-byte bank groups;
+//   V: chunk position vrow(r)·CPR + (c ^ sv(r)), sv(r) = 8·((r/4) mod 2) (CPR ≥ 16) or 0, vrow(r) = r ^ ((r/4) mod
+//      2) (CPR = 8) or r: the two half-waves read rows 4 apart, which then occupy disjoint halves of the banks.
 template <int NS, int DK, int DV>
 __global__ void __launch_bounds__(256) attention_fused(const float* __restrict__ Q, int ldq, const float* __restrict__ K,
                                                        int ldk, const float* __restrict__ V, int ldv,
                                                        float* __restrict__ ctx, int H, int Rq, int S, float scale,
                                                        int causal)
 {
-    constexpr int SK = 32 * NS, KP = DK + 4, VP = SK + 4;  // pitches put rows 4 banks apart
-    __shared__ __attribute__((aligned(16))) float ks[SK * KP];
-    __shared__ __attribute__((aligned(16))) float vts[DV * VP];
+    static_assert(DK == DV && (DK == 32 || DK == 64 || DK == 128), "head sizes");
+    constexpr int D = DK, SK = 32 * NS, CPR = D / 4, TILE = 32 * CPR, PW = TILE / 256;  // PW: DMA ops per wave per tile
+    __shared__ __attribute__((aligned(16))) float ks[SK * D];
+    __shared__ __attribute__((aligned(16))) float vs[SK * D];
     const int z = blockIdx.y, b = z / H, h = z % H;
     const int tid = threadIdx.x, lane = tid & 63, col = lane & 31, hf = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const float* Kh = K + (size_t)b * S * ldk + (size_t)h * DK;
     const float* Vh = V + (size_t)b * S * ldv + (size_t)h * DV;
-    for (int i = tid; i < SK * (DK / 4); i += 256) {
-        const int r = i / (DK / 4), c = i % (DK / 4);
-        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (r < S) v = *reinterpret_cast<const float4*>(Kh + (size_t)r * ldk + 4 * c);
-        *reinterpret_cast<float4*>(&ks[r * KP + 4 * c]) = v;
-    }
-    for (int i = tid; i < SK * (DV / 4); i += 256) {
-        const int r = i / (DV / 4), c = i % (DV / 4);
-        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (r < S) v = *reinterpret_cast<const float4*>(Vh + (size_t)r * ldv + 4 * c);
-        vts[(4 * c + 0) * VP + r] = v.x;
-        vts[(4 * c + 1) * VP + r] = v.y;
-        vts[(4 * c + 2) * VP + r] = v.z;
-        vts[(4 * c + 3) * VP + r] = v.w;
-    }
-    // Q fragments: at step c of group g, half-wave hf contracts over d = 8g + 4hf + c (K fragments likewise)
-    const int qi = blockIdx.x * 128 + (tid >> 6) * 32 + col;
+    auto sk = [](int r) { return CPR >= 16 ? (r & 15) : ((r >> 1) & 7); };
+    auto sv = [](int r) { return CPR >= 16 ? ((r >> 2) & 1) << 3 : 0; };
+    auto vrow = [](int r) { return CPR == 8 ? (r ^ ((r >> 2) & 1)) : r; };
+
+    // this lane's 32 Q values of query qi (rows beyond Rq read row Rq − 1 and store nothing): at step c of group g,
+    // half-wave hf contracts over d = 8g + 4hf + c (K fragments likewise)
+    const int qi = blockIdx.x * 128 + wave * 32 + col;
     const float* Qr = Q + ((size_t)b * Rq + (qi < Rq ? qi : Rq - 1)) * ldq + (size_t)h * DK;
     float4 qf[DK / 8];
 #pragma unroll
     for (int g = 0; g < DK / 8; ++g) qf[g] = *reinterpret_cast<const float4*>(Qr + 8 * g + 4 * hf);
-    __syncthreads();
-
-    v16f sc[NS];
+    // The staging loads are inline assembly the compiler does not count: have it wait for Q here, before any of them
+    // is issued, so that its own wait before the first product does not also wait for the staging.
 #pragma unroll
-    for (int t = 0; t < NS; ++t)
+    for (int g = 0; g < DK / 8; ++g) asm volatile("" ::"v"(qf[g].x), "v"(qf[g].y), "v"(qf[g].z), "v"(qf[g].w));
+
+    // staging: LDS-DMA op k of this wave in tile t fills chunk positions p0 .. p0 + 63, lane l position p0 + l
+    auto stage = [&](bool isv, int t) {
+#pragma unroll
+        for (int k = 0; k < PW; ++k) {
+            const int p0 = t * TILE + (k * 4 + wave) * 64, p = p0 + lane;
+            const int rl = p / CPR, cp = p % CPR;
+            const int r = isv ? vrow(rl) : rl, c = cp ^ (isv ? sv(r) : sk(r));
+            const float* src = r < S ? (isv ? Vh + (size_t)r * ldv : Kh + (size_t)r * ldk) + 4 * c : knx_attn_zero;
+            dma16_at(src, (isv ? vs : ks) + (size_t)p0 * 4);
+        }
+    };
+#pragma unroll
+    for (int t = 0; t < NS; ++t) stage(false, t);
+#pragma unroll
+    for (int t = 0; t < NS; ++t) stage(true, t);
+
+    // K fragment of group g: row 32t + col, logical chunk 2g + hf (byte offset within the tile)
+    int kb[DK / 8];
+#pragma unroll
+    for (int g = 0; g < DK / 8; ++g) kb[g] = (col * CPR + ((2 * g + hf) ^ sk(col))) * 16;
+    v16f sc[NS];
+    unrolled([&](auto tc) {
+        constexpr int t = decltype(tc)::value;
 #pragma unroll
         for (int e = 0; e < 16; ++e) sc[t][e] = 0.0f;
+        // tiles t + 1 .. NS − 1 of K and all of V may stay in flight
+        KNX_WAIT_VM_LDS((NS - 1 - t) * PW + NS * PW);
+        knx_barrier_nofence();
+        const int8_t* kt = reinterpret_cast<const int8_t*>(ks) + t * TILE * 16;
 #pragma unroll
-    for (int g = 0; g < DK / 8; ++g)
-#pragma unroll
-        for (int t = 0; t < NS; ++t) {
-            const float4 kf = *reinterpret_cast<const float4*>(&ks[(32 * t + col) * KP + 8 * g + 4 * hf]);
+        for (int g = 0; g < DK / 8; ++g) {
+            const float4 kf = *reinterpret_cast<const float4*>(kt + kb[g]);
 #pragma unroll
             for (int c = 0; c < 4; ++c)
                 sc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32((&kf.x)[c], (&qf[g].x)[c], sc[t], 0, 0, 0);
         }
+    }, std::make_integer_sequence<int, NS>{});
 
     // element e of tile t is key 32t + 8(e/4) + 4hf + e%4 of query qi
     float m = -INFINITY;
@@ -133,22 +172,36 @@ __global__ void __launch_bounds__(256) attention_fused(const float* __restrict__
 #pragma unroll
         for (int e = 0; e < 16; ++e) sc[t][e] = sc[t][e] * inv;
 
+    // V value of key j = J + 4hf (J = 32t + 8e4 + c, bit 2 of J clear) and column 32u + col: byte offset
+    // J·CPR·16 + vb[J & 1][u]
+    int vb[2][DV / 32];
+#pragma unroll
+    for (int par = 0; par < 2; ++par)
+#pragma unroll
+        for (int u = 0; u < DV / 32; ++u) {
+            const int j = par + 4 * hf;  // the row's low bits; vrow and sv depend on bits 0-2 only
+            vb[par][u] = ((vrow(j) - par) * CPR + ((8 * u + (col >> 2)) ^ sv(j))) * 16 + (col & 3) * 4;
+        }
+    KNX_WAIT_VM_LDS(0);
+    knx_barrier_nofence();
     v16f o[DV / 32];
 #pragma unroll
     for (int u = 0; u < DV / 32; ++u)
 #pragma unroll
         for (int e = 0; e < 16; ++e) o[u][e] = 0.0f;
+    const int8_t* vbase = reinterpret_cast<const int8_t*>(vs);
 #pragma unroll
     for (int t = 0; t < NS; ++t)
 #pragma unroll
         for (int e4 = 0; e4 < 4; ++e4)
 #pragma unroll
-            for (int u = 0; u < DV / 32; ++u) {
-                const float4 vf = *reinterpret_cast<const float4*>(&vts[(32 * u + col) * VP + 32 * t + 8 * e4 + 4 * hf]);
+            for (int u = 0; u < DV / 32; ++u)
 #pragma unroll
-                for (int c = 0; c < 4; ++c)
-                    o[u] = __builtin_amdgcn_mfma_f32_32x32x2f32((&vf.x)[c], sc[t][4 * e4 + c], o[u], 0, 0, 0);
-            }
+                for (int c = 0; c < 4; ++c) {
+                    const int J = 32 * t + 8 * e4 + c;
+                    const float vv = *reinterpret_cast<const float*>(vbase + J * CPR * 16 + vb[c & 1][u]);
+                    o[u] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv, sc[t][4 * e4 + c], o[u], 0, 0, 0);
+                }
     if (qi >= Rq) return;
     // element e of o[u] is ctx column 32u + 8(e/4) + 4hf + e%4 of query qi
     float* y = ctx + ((size_t)b * Rq + qi) * ((size_t)H * DV) + (size_t)h * DV + 4 * hf;
