@@ -21,6 +21,7 @@
 #include <string>
 #include <mutex>
 #include <type_traits>
+#include <utility>
 
 #include "knx_pipe.hpp"
 
@@ -925,16 +926,28 @@ bool k128_fits(const I8Args& p)
     return p.M >= BM && p.N >= BN && (long)8 * p.lda < 0x7fffffffL && (long)8 * p.ldw < 0x7fffffffL;
 }
 
+// f(integral_constant<int, d>) for d = 0, 1, …: a loop whose index is a compile-time constant in the body
+template <typename F, int... T>
+__device__ __forceinline__ void ring_unrolled(F&& f, std::integer_sequence<int, T...>)
+{
+    (f(std::integral_constant<int, T>{}), ...);
+}
+
 // ---------------------------------------------------------------- deep-ring kernel (mid-size M)
 // Shapes whose 256×256 and 128×128 tiles would leave CUs idle (e.g. M = 256, N = K = 4096: 64×64 tiles give every CU
 // one) move little MFMA work per k-tile (a 64×64×128 k-tile is 128 MFMA cycles per SIMD) against 16 KB of loads, so
 // latency decides: S LDS stages of 128-byte k-tiles (whole lines, the same swizzled layout and LDS-DMA loads as
-// i8gemm_k128) keep S−KPI k-tiles in flight per workgroup.  Per iteration of KPI k-tiles: wait until their loads have
+// i8gemm_k128) keep S−KPI k-tiles in flight per ring.  Per iteration of KPI k-tiles: wait until their loads have
 // landed (vmcnt counts the younger ones still in flight), one workgroup barrier (every wave is done with the previous
 // KPI k-tiles, whose stages are free), issue the loads of the k-tiles S−KPI ahead into those stages, read every
 // fragment of the KPI k-tiles at once (one LDS round trip instead of one per k-step), multiply.
-template <int BM, int BN, int WM, int WN, int S, int KPI>
-__global__ void __launch_bounds__(WM * WN * 64) i8gemm_ring(I8Args p)
+//
+// KG > 1 splits K inside the workgroup: KG groups of WM×WN waves, group g streams k-tiles [g·nk/KG, (g+1)·nk/KG)
+// through a ring of its own, so a CU keeps KG times the bytes in flight for the same tile.  Every group runs the
+// same number of iterations (nk % KG == 0), so the workgroup barriers match.  At the end the groups g ≥ 1 hand their
+// int32 partial tiles to group 0 through LDS (exact adds), and group 0 runs the epilogue.
+template <int BM, int BN, int WM, int WN, int S, int KPI, int KG = 1>
+__global__ void __launch_bounds__(KG * WM * WN * 64) i8gemm_ring(I8Args p)
 {
     constexpr int NW = WM * WN;
     constexpr int TM = BM / WM, TN = BN / WN;
@@ -948,12 +961,15 @@ __global__ void __launch_bounds__(WM * WN * 64) i8gemm_ring(I8Args p)
     static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile");
     static_assert(S >= 2 * KPI && SLOTS * 6 <= 63, "ring depth and vmcnt range");
     static_assert(NW * 16 * (TN + 4) * 4 <= S * STAGE, "staging fits in the ring");
+    static_assert(NW * FM * FN * 16 * 64 * 4 <= S * STAGE, "a partial tile fits in a ring");
     static_assert(BM <= NW * 64, "one row scale per thread");
-    __shared__ __attribute__((aligned(16))) int8_t lds[S * STAGE];
+    __shared__ __attribute__((aligned(16))) int8_t lds_all[KG * S * STAGE];
     __shared__ float row_scale[BM];
 
     const int t = threadIdx.x, lane = t & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int wave_all = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int kg = wave_all / NW, wave = wave_all % NW;  // K group, wave within the group
+    int8_t* const lds = lds_all + kg * S * STAGE;
     const int wm = wave / WN, wn = wave % WN;
     int tm, tn;
     tile_of_best(blockIdx.x, p.tiles_m, p.tiles_n, BM, BN, tm, tn);
@@ -969,10 +985,11 @@ __global__ void __launch_bounds__(WM * WN * 64) i8gemm_ring(I8Args p)
     }
     const float my_sa = (t < BM && p.Y) ? p.sa[m0 + t] : 0.0f;
 
-    const int8_t* tile_a = p.A + (size_t)m0 * p.lda;
-    const int8_t* tile_w = p.W + (size_t)n0 * p.ldw;
+    const int nk_all = (p.K + 127) / 128;
+    const int nk = nk_all / KG;  // this group's k-tiles (KG > 1: nk_all % KG == 0 and no half k-tile)
+    const int8_t* tile_a = p.A + (size_t)m0 * p.lda + (size_t)kg * nk * 128;
+    const int8_t* tile_w = p.W + (size_t)n0 * p.ldw + (size_t)kg * nk * 128;
     const int cl = (lane & 7) ^ (lane >> 3), rs = lane >> 3;
-    const int nk = (p.K + 127) / 128;
     const bool half = (p.K & 127) != 0;
     auto issue = [&](int kt) {  // this wave's loads of k-tile kt into stage kt % S
         int8_t* stage = lds + (kt % S) * STAGE;
@@ -1078,17 +1095,56 @@ __global__ void __launch_bounds__(WM * WN * 64) i8gemm_ring(I8Args p)
         for (int fi = 0; fi < FM; ++fi)
 #pragma unroll
             for (int fj = 0; fj < FN; ++fj) accs[0][fi][fj] += accs[c][fi][fj];
+    if (KG > 1) {
+        // partial tiles of groups 1.. through their own rings (every group is past its last fragment read), lane by
+        // lane: element e of block f of wave w at ((w·FM·FN + f)·16 + e)·64 + lane
+        int* part = reinterpret_cast<int*>(lds);
+        KNX_WAIT_LDS();
+        knx_barrier_nofence();
+        if (kg > 0) {
+#pragma unroll
+            for (int fi = 0; fi < FM; ++fi)
+#pragma unroll
+                for (int fj = 0; fj < FN; ++fj)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) part[((wave * FM * FN + fi * FN + fj) * 16 + e) * 64 + lane] = accs[0][fi][fj][e];
+        }
+        KNX_WAIT_LDS();
+        knx_barrier_nofence();
+        if (kg > 0) {
+            knx_barrier_nofence();  // the one barrier of group 0's epilogue
+            return;
+        }
+#pragma unroll
+        for (int g2 = 1; g2 < KG; ++g2) {
+            const int* src = reinterpret_cast<const int*>(lds_all + g2 * S * STAGE);
+#pragma unroll
+            for (int fi = 0; fi < FM; ++fi)
+#pragma unroll
+                for (int fj = 0; fj < FN; ++fj)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) accs[0][fi][fj][e] += src[((wave * FM * FN + fi * FN + fj) * 16 + e) * 64 + lane];
+        }
+    }
     tile_epilogue<BM, BN, WM, WN>(p, accs[0], lds, row_scale, my_sa, m0, nb, swv, bv, mlo, nlo);
 }
 
-template <int BM, int BN, int WM, int WN, int S, int KPI>
+template <int BM, int BN, int WM, int WN, int S, int KPI, int KG = 1>
 int launch_ring(I8Args p, hipStream_t s, const char* name)
 {
     p.tiles_m = (p.M + BM - 1) / BM;
     p.tiles_n = (p.N + BN - 1) / BN;
     const unsigned grid = (unsigned)p.tiles_m * (unsigned)p.tiles_n;
-    hipLaunchKernelGGL((i8gemm_ring<BM, BN, WM, WN, S, KPI>), dim3(grid), dim3(WM * WN * 64), 0, s, p);
+    hipLaunchKernelGGL((i8gemm_ring<BM, BN, WM, WN, S, KPI, KG>), dim3(grid), dim3(KG * WM * WN * 64), 0, s, p);
     return knx::check_launch(name);
+}
+
+// the in-workgroup K split needs whole 128-byte k-tiles, as many per group, and a full ring's worth per group
+template <int KG, int S>
+bool ring_split_fits(const I8Args& p)
+{
+    const int nk = p.K / 128;
+    return p.K % 128 == 0 && nk % KG == 0 && nk / KG >= S;
 }
 
 // ---------------------------------------------------------------- skinny kernel (M ≤ 64)
@@ -1121,15 +1177,20 @@ __global__ void __launch_bounds__(KS * 64) i8gemm_skinny(I8Args p)
 #pragma unroll
     for (int b = 0; b < MB; ++b) acc[b] = v4i{0, 0, 0, 0};
     const int nk = p.K / 64;
-    // wave w takes k-steps w, w+KS, w+2·KS, … ; KT of them per pass, loads issued before the multiplies
+    // wave w takes k-steps w, w+KS, w+2·KS, … ; KT of them per pass, loads issued before the multiplies.  Workgroup
+    // b starts its K order rot(b) k-steps in (a multiple of KS, so every wave keeps its share; int32 sums are exact
+    // in any order): at a power-of-two row stride the workgroups would otherwise all read the same offsets within
+    // their rows at the same time, and so the same memory channels.
+    const int rot = nk >= 2 * KS ? (int)(blockIdx.x % (unsigned)(nk / KS)) * KS : 0;
     for (int k0 = wave; k0 < nk; k0 += KS * KT) {
         v4i wf[KT], af[KT][MB];
 #pragma unroll
         for (int j = 0; j < KT; ++j) {
             const int kk = k0 + j * KS;
-            wf[j] = kk < nk ? *(const v4i*)(wrow + (size_t)kk * 64) : v4i{0, 0, 0, 0};
+            const int kr = kk + rot < nk ? kk + rot : kk + rot - nk;
+            wf[j] = kk < nk ? *(const v4i*)(wrow + (size_t)kr * 64) : v4i{0, 0, 0, 0};
 #pragma unroll
-            for (int b = 0; b < MB; ++b) af[j][b] = (kk < nk && aok[b]) ? *(const v4i*)(arow[b] + (size_t)kk * 64) : v4i{0, 0, 0, 0};
+            for (int b = 0; b < MB; ++b) af[j][b] = (kk < nk && aok[b]) ? *(const v4i*)(arow[b] + (size_t)kr * 64) : v4i{0, 0, 0, 0};
         }
 #pragma unroll
         for (int j = 0; j < KT; ++j)
@@ -1249,13 +1310,15 @@ __global__ void __launch_bounds__(KS * 64) i8gemm_skinny_q(I8Args p, const float
     v4i acc = v4i{0, 0, 0, 0};
     const v4i z = v4i{0, 0, 0, 0};
     const int nk = p.K / 64;
+    const int rot = nk >= 2 * KS ? (int)(blockIdx.x % (unsigned)(nk / KS)) * KS : 0;  // as in i8gemm_skinny
     for (int k0 = wave; k0 < nk; k0 += KS * KT) {
         v4i wf[KT], af[KT];
 #pragma unroll
         for (int j = 0; j < KT; ++j) {
             const int kk = k0 + j * KS;
-            wf[j] = kk < nk ? *(const v4i*)(wrow + (size_t)kk * 64) : z;
-            af[j] = (kk < nk && rok) ? quant16(kk) : z;
+            const int kr = kk + rot < nk ? kk + rot : kk + rot - nk;
+            wf[j] = kk < nk ? *(const v4i*)(wrow + (size_t)kr * 64) : z;
+            af[j] = (kk < nk && rok) ? quant16(kr) : z;
         }
 #pragma unroll
         for (int j = 0; j < KT; ++j) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[j], wf[j], acc, 0, 0, 0);
@@ -1503,6 +1566,8 @@ static int i8gemm_run(I8Args p, hipStream_t s, const char* name)
         if (f == "pp" && k128_fits<256, 256>(p)) return launch_pp<256, 256>(p, s, name);
         if (f == "ring64s4" && k128_fits<64, 64>(p)) return launch_ring<64, 64, 2, 2, 4, 1>(p, s, name);
         if (f == "ring64s8k2" && k128_fits<64, 64>(p)) return launch_ring<64, 64, 2, 2, 8, 2>(p, s, name);
+        if (f == "ring64g2" && k128_fits<64, 64>(p) && ring_split_fits<2, 4>(p)) return launch_ring<64, 64, 2, 2, 4, 1, 2>(p, s, name);
+        if (f == "ring64s8" && k128_fits<64, 64>(p)) return launch_ring<64, 64, 2, 2, 8, 1>(p, s, name);
         if (f == "skinny" && M <= 64) return M <= 16 ? launch_skinny<1>(p, s, name) : M <= 32 ? launch_skinny<2>(p, s, name) : launch_skinny<4>(p, s, name);
     }
     if (M <= 16) return launch_skinny<1>(p, s, name);
@@ -1523,7 +1588,11 @@ static int i8gemm_run(I8Args p, hipStream_t s, const char* name)
         return launch_k128<128, 128, 2, 2, 2>(p, s, name);
     }
     // fewer tiles than CUs even at 128×128 (e.g. M = 256, N = 4096): one 64×64 tile per workgroup on the deep LDS
-    // ring (M = 256: 13.2 µs against 16.8 for the 64-byte k-tile pipeline)
+    // ring (M = 256: 13.2 µs against 16.8 for the 64-byte k-tile pipeline), K split over two rings in the workgroup
+    // when the 64×64 tiles leave CUs without a second workgroup
+    const long tiles64 = (long)((M + 63) / 64) * ((N + 63) / 64);
+    if (tiles64 <= knx::num_cus() && k128_fits<64, 64>(p) && ring_split_fits<2, 4>(p))
+        return launch_ring<64, 64, 2, 2, 4, 1, 2>(p, s, name);
     if (k128_fits<64, 64>(p)) return launch_ring<64, 64, 2, 2, 4, 1>(p, s, name);
     return launch_pipe<64, 64, 2, 2, 4>(p, s, name);
 }

@@ -90,11 +90,13 @@ def test_i8gemm_standalone_config(L, M):
 
 
 I8_VARIANTS = ["default", "pp", "k128", "k128w8", "k128w8t", "k128m", "k128w8ta3", "k128ma3", "k128w8ta3e", "k128w16", "ring64s4", "ring64s8k2",
-               "pipe256", "pipe256w8", "pipe128", "pipe64", "tile64"]
+               "ring64g2", "ring64s8", "pipe256", "pipe256w8", "pipe128", "pipe64", "tile64"]
 # tiles moved back at the M/N edges, half k-tiles (K % 128 == 64), N % 4 != 0, one whole 256x256 tile, 2..4 k-tiles
-# (every branch of the three-stage A ring's prologue and tail), and an 8 x 8 tile grid split into XCD blocks
+# (every branch of the three-stage A ring's prologue and tail), an 8 x 8 tile grid split into XCD blocks, and for the
+# K split between two rings: 6 k-tiles per ring, ragged tiles with 8 per ring, 13 k-tiles (no split)
 I8_EDGE_SHAPES = [(300, 300, 1024), (520, 700, 320), (257, 259, 192), (256, 256, 64), (640, 384, 4096),
-                  (512, 256, 256), (256, 512, 384), (384, 384, 448), (2048, 2048, 512)]
+                  (512, 256, 256), (256, 512, 384), (384, 384, 448), (2048, 2048, 512), (192, 320, 1536),
+                  (200, 260, 2048), (130, 200, 1664)]
 
 
 @pytest.mark.parametrize("variant", I8_VARIANTS)
@@ -150,8 +152,8 @@ def test_i8gemm_skinny_variants(L, monkeypatch, variant, M, N, K):
     assert np.array_equal(host(Y), want_y)
 
 
-@pytest.mark.parametrize("variant", ["default", "k128w8t", "k128w8ta3e", "k128m", "ring64s4", "pipe64", "tile64", "pp",
-                                     "skinny"])
+@pytest.mark.parametrize("variant", ["default", "k128w8t", "k128w8ta3e", "k128m", "ring64s4", "ring64g2", "pipe64", "tile64",
+                                     "pp", "skinny"])
 @pytest.mark.parametrize("M,N,K,inplace", [(300, 300, 1024, False), (520, 700, 320, True), (2048, 2048, 2048, False),
                                            (48, 520, 192, True)])
 def test_i8gemm_residual(L, monkeypatch, variant, M, N, K, inplace):
