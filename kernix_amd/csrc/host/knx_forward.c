@@ -757,16 +757,23 @@ static int run_ln_quant(kernix_model* m, int i, int fuse, void* st)
     return 2;
 }
 
-/* Enqueues every step for one chunk whose input starts at `in` (device). */
-static int run_chunk(kernix_model* m, const float* in, int B, void* st)
+static int fuse_enabled(void)
+{
+    const char* nf = getenv("KNX_NO_FUSE");
+    return nf == NULL || *nf == '\0' || *nf == '0';
+}
+
+/* Enqueues every step for one chunk whose input starts at `in` (device); the output value goes to `out` instead of
+ * its storage buffer when out is not NULL (see direct_output). */
+static int run_chunk(kernix_model* m, const float* in, int B, float* out, void* st)
 {
     for (int v = 0; v < m->n_vals; v++) {
         const kernix_val* val = &m->vals[v];
         m->views[v] = (float_tensor){ B * val->r, val->c, val->st < 0 ? (float*)in : m->st[val->st]->tensor };
     }
+    if (out != NULL) m->views[m->out_v].tensor = out;
     if (B == 0) return 0;
-    const char* nf = getenv("KNX_NO_FUSE");
-    const int fuse = nf == NULL || *nf == '\0' || *nf == '0';
+    const int fuse = fuse_enabled();
     for (int i = 0; i < m->n_steps; i++) {
         if (fuse && ln_quant_fusable(m, i)) {
             const int c = run_ln_quant(m, i, fuse, st);
@@ -841,16 +848,35 @@ static int prepare(kernix_model* m, int per)
     return mark_done(m, m->dev->stream);
 }
 
-/* One piece: samples [s0, s0 + n) of the batch, whose input rows start at x (device memory); the output is copied
- * to dst (device or pinned host memory, `to_host` says which, holding the whole batch's output) at the piece's rows. */
+/* The forward's output value can be written by its producing step straight into the caller's device buffer `out`
+ * (no copy afterwards): it is not the input or a view of another value (RESHAPE), no RESHAPE makes a view of it, and
+ * out does not overlap the input rows x.  Every other step reads and writes the workspace as planned; the producing
+ * step then runs out of place where the plan had it in place. */
+static int direct_output(const kernix_model* m, const float* x, size_t x_bytes, const float* out, size_t out_bytes)
+{
+    const int ov = m->out_v;
+    if (ov < 1 || m->vals[ov].st < 0 || m->steps[ov - 1].kind == KERNIX_OP_RESHAPE) return 0;
+    for (int i = ov; i < m->n_steps; i++)
+        if (m->steps[i].kind == KERNIX_OP_RESHAPE && m->steps[i].inp[0] == ov) return 0;
+    const char* a = (const char*)x;
+    const char* b = (const char*)out;
+    return b + out_bytes <= a || a + x_bytes <= b;
+}
+
+/* One piece: samples [s0, s0 + n) of the batch, whose input rows start at x (device memory); the output goes to dst
+ * (device or pinned host memory, `to_host` says which, holding the whole batch's output) at the piece's rows:
+ * written there directly by the last step when direct_output allows, else copied from the workspace. */
 static int run_piece(kernix_model* m, const float* x, int s0, int n, float* dst, int to_host, void* st)
 {
     const size_t out_row = (size_t)m->out_dim;
-    ws_view(m, n * m->seq_len);
-    if (run_chunk(m, x, n, st) != 0) return -1;
-    const float* y = m->views[m->out_v].tensor;
     const size_t bytes = (size_t)n * out_row * sizeof(float);
     float* at = dst + (size_t)s0 * out_row;
+    const size_t x_bytes = (size_t)n * (size_t)m->seq_len * (size_t)m->in_dim * sizeof(float);
+    const int direct = !to_host && direct_output(m, x, x_bytes, at, bytes);
+    ws_view(m, n * m->seq_len);
+    if (run_chunk(m, x, n, direct ? at : NULL, st) != 0) return -1;
+    if (direct) return 0;
+    const float* y = m->views[m->out_v].tensor;
     return hip_ok(to_host ? knx_hip_memcpy_d2h(at, y, bytes, st) : knx_hip_memcpy_d2d(at, y, bytes, st), "output copy");
 }
 

@@ -230,3 +230,34 @@ def test_forward_device_matches_host_forward(tmp_path, name):
     m.close()
     m2.close()
     assert np.array_equal(got, want)
+
+
+
+@pytest.mark.parametrize("case", ["direct", "reshape_out", "in_place"])
+def test_forward_device_output_paths(tmp_path, case):
+    """The device forward's output: written by the last step straight into the caller's buffer (direct), or copied
+    from the workspace when the output value is a reshape view or when the output buffer is the input buffer
+    (in_place): all give the host forward's bits."""
+    import torch
+
+    from kernix_amd.knxfile import ModelBuilder
+
+    rng = np.random.default_rng(5)
+    b = ModelBuilder((16,))
+    h = b.linear(b.input, rng.normal(0, 0.3, (16, 32)), rng.normal(0, 0.1, 32), activation="relu")
+    y = b.linear(h, rng.normal(0, 0.3, (32, 16)), rng.normal(0, 0.1, 16))
+    if case == "reshape_out":
+        b.reshape(y, (4, 4))
+    p = b.save(str(tmp_path / "m.knx"))
+    x = rng.normal(0, 1, (40, 16)).astype(np.float32)
+    m = Model(p)
+    want = m(x).reshape(40, -1).copy()
+    s = torch.cuda.Stream()
+    for _ in range(3):
+        dx = torch.from_numpy(x).cuda()
+        out = dx if case == "in_place" else torch.full((40, m.out_dim), 7.0, dtype=torch.float32, device="cuda")
+        with torch.cuda.stream(s):
+            m.forward_device(dx.data_ptr(), 40, out.data_ptr(), s.cuda_stream)
+        s.synchronize()
+        assert np.array_equal(out.cpu().numpy().reshape(40, -1), want)
+    m.close()
