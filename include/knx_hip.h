@@ -104,9 +104,9 @@ KNX_API int knx_hip_i8gemm_res(int M, int N, int K, const int8_t* A, int lda, co
 
 /* kernix_qmatmul and the activation of its LINEAR step in one call (reference include/kernix_model.h:99-182 then
  * :1854-1856): x (rows × k fp32, stride ldx) quantized per row, multiplied by W (n × kp int8), then the epilogue of
- * knx_hip_i8gemm (accumulate adds into Y; R, if not NULL, is added after the activation; not both).  At ≤ 4 rows one
- * kernel quantizes on the fly (xq and sx may be NULL); above, knx_hip_quantize_rows into xq (rows × kp) and sx (rows)
- * and then the GEMM.  Results are the same bits either way. */
+ * knx_hip_i8gemm (accumulate adds into Y; R, if not NULL, is added after the activation; not both).  At ≤ 16 rows
+ * with rows·k·n ≤ 2^23 one kernel quantizes on the fly (xq and sx are not touched and may then be NULL); otherwise
+ * knx_hip_quantize_rows into xq (rows × kp) and sx (rows) and then the GEMM.  Results are the same bits either way. */
 KNX_API int knx_hip_qlinear(const float* x, int ldx, int rows, int k, int kp, int8_t* xq, float* sx, const int8_t* W,
                             int ldw, int n, const float* sw, const float* bias, int act, float alpha, int accumulate,
                             const float* R, int ldr, float* Y, int ldy, void* stream);

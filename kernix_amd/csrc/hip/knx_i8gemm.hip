@@ -1214,125 +1214,169 @@ __global__ void __launch_bounds__(KS * 64) i8gemm_skinny(I8Args p)
     }
 }
 
-// ---------------------------------------------------------------- fused quantize + skinny GEMM (≤ 4 rows)
-// kernix_qmatmul at the few rows the reference runs int8 arithmetic on (≤ 2, its batch-1 latency path) as one kernel
-// instead of the row quantizer followed by the skinny GEMM.  Every workgroup (16 output channels) first finds the
-// absolute maxima of its ≤ 4 fp32 input rows (each row split over the waves, the partial maxima combined through LDS:
-// a maximum is exact in any order), then runs the skinny K loop with each lane quantizing its 16 inputs of a k-step
-// on the fly with the operations of knx_hip_quantize_rows (s = m/127 or 1 for an all-zero row, inv = 1/s, rint,
-// clamp ±127; a row holding NaN or ±inf gets s = NaN and q = 0, so its whole output row is NaN).  The int32 sums and
-// outputs are therefore bit-exact against the two-kernel path.  The fp32 rows are read once per workgroup (16 KB
-// per row at K = 4096, from L2), which is why the fused form stops at 4 rows.
-template <int KS, int KT>
+// ---------------------------------------------------------------- fused quantize + skinny GEMM (≤ 64 rows)
+// kernix_qmatmul at small row counts and small weights (the reference's int8 arithmetic at ≤ 2 rows, its batch-1
+// latency path, and the int8 mode at small batches) as one kernel instead of the row quantizer followed by the skinny
+// GEMM.  Every
+// workgroup (16 output channels, MB blocks of 16 rows) first finds the absolute maximum of each fp32 input row (all
+// threads take part at every row count; partial maxima meet by exchanges and in LDS: a maximum is exact in any
+// order), then runs the skinny K loop with
+// each lane quantizing its 16 inputs of a k-step on the fly with the operations of knx_hip_quantize_rows (s = m/127
+// or 1 for an all-zero row, inv = 1/s, rint, clamp ±127; a row holding NaN or ±inf gets s = NaN and q = 0, so its
+// whole output row is NaN).  The int32 sums and outputs are therefore bit-exact against the two-kernel path.  The
+// fp32 rows are read twice per workgroup from L2, which is why the fused form serves small row counts and weights
+// only (see knx_hip_qlinear).
+template <int KS, int KT, int MB>
 __global__ void __launch_bounds__(KS * 64) i8gemm_skinny_q(I8Args p, const float* __restrict__ X, int ldx, int kx)
 {
-    constexpr int MR = 4;
-    __shared__ int part[KS][16][17];
-    __shared__ float pmax[MR][KS];
-    __shared__ int pbad[MR][KS];
+    constexpr int MR = 16 * MB;
+    static_assert(MR <= 64, "at most 64 rows (one exchange group of eight or more threads per row)");
+    __shared__ int part[KS][MB][16][17];
+    __shared__ float pmax[1][64];  // one partial maximum per exchange group (at most 64 groups)
+    __shared__ int pbad[1][64];
     __shared__ float row_s[MR], row_inv[MR];
     __shared__ int row_bad[MR];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int M = p.M;
-    // row maxima: row m, wave w covers elements [w·seg, (w+1)·seg)
-    const int seg = (kx + KS - 1) / KS;
-    for (int m = 0; m < M; ++m) {
-        const float* xr = X + (size_t)m * ldx;
+    const bool xvec = (ldx & 3) == 0 && ((uintptr_t)X & 15) == 0;
+    // row maxima: the KS·64 threads split into groups of G = KS·64 / Mp (Mp = M rounded up to a power of two), group
+    // r scanning row r with G threads side by side (coalesced, four loads in flight per thread); the threads of a
+    // group reduce by exchanges within at most one wave, then the ≤ KS waves of a row through LDS
+    const int t = threadIdx.x;
+    int mp = 1;
+    while (mp < M) mp <<= 1;
+    const int G = KS * 64 / mp, GW = G < 64 ? G : 64;  // threads per row, per exchange group
+    {
+        const int row = t / G, sub = t % G;
         float mx = 0.0f;
         int bad = 0;
-        const int j1 = min(kx, (wave + 1) * seg);
-        for (int j = wave * seg + lane; j < j1; j += 64) {
-            const float a = fabsf(xr[j]);
+        auto take = [&](float v) {
+            const float a = fabsf(v);
             if (!(a <= 3.402823466e38f)) bad = 1;  // NaN or ±inf
             else mx = a > mx ? a : mx;
+        };
+        if (row < M) {
+            const float* xr = X + (size_t)row * ldx;
+            int j = 0;
+            if (xvec) {
+                const int n4 = kx / 4;
+                for (int i = sub; i < n4; i += 4 * G) {
+                    float4 f[4];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u)
+                        f[u] = i + u * G < n4 ? *reinterpret_cast<const float4*>(xr + 4 * (i + u * G)) : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        take(f[u].x); take(f[u].y); take(f[u].z); take(f[u].w);
+                    }
+                }
+                j = 4 * n4;
+            }
+            for (j += sub; j < kx; j += G) take(xr[j]);
         }
-        mx = knx_wave_max(mx);
-        bad = __any(bad);
-        if (lane == 0) {
-            pmax[m][wave] = mx;
-            pbad[m][wave] = bad;
+        for (int off = GW / 2; off > 0; off >>= 1) {
+            const float o = __shfl_xor(mx, off, 64);
+            mx = o > mx ? o : mx;
+            bad |= __shfl_xor(bad, off, 64);
+        }
+        if (t % GW == 0) {
+            pmax[0][t / GW] = mx;
+            pbad[0][t / GW] = bad;
         }
     }
     __syncthreads();
-    if ((int)threadIdx.x < M) {
-        const int m = threadIdx.x;
+    if (t < M) {
+        const int m = t, gpr = G / GW;  // exchange groups per row
         float mx = 0.0f;
         int bad = 0;
-        for (int w = 0; w < KS; ++w) {
-            mx = pmax[m][w] > mx ? pmax[m][w] : mx;
-            bad |= pbad[m][w];
+        for (int w = 0; w < gpr; ++w) {
+            mx = pmax[0][m * gpr + w] > mx ? pmax[0][m * gpr + w] : mx;
+            bad |= pbad[0][m * gpr + w];
         }
-        const float s = mx > 0.0f ? __fdiv_rn(mx, 127.0f) : 1.0f;
-        row_s[m] = bad ? __int_as_float(0x7fc00000) : s;
-        row_inv[m] = __fdiv_rn(1.0f, s);
+        const float sc = mx > 0.0f ? __fdiv_rn(mx, 127.0f) : 1.0f;
+        row_s[m] = bad ? __int_as_float(0x7fc00000) : sc;
+        row_inv[m] = __fdiv_rn(1.0f, sc);
         row_bad[m] = bad;
     }
     __syncthreads();
 
-    // K loop of the skinny kernel (one block of 16 rows, rows ≥ M are zero); lane (r, c) holds row r, bytes
+    // K loop of the skinny kernel over MB blocks of 16 rows (rows ≥ M are zero); lane (r, c) holds row 16b + r, bytes
     // [64·kk + 16c, +16) of k-step kk
     const int r = lane & 15, c = lane >> 4;
     const int n0 = blockIdx.x * 16;
     const int gn = min(n0 + r, p.N - 1);
     const int8_t* wrow = p.W + (size_t)gn * p.ldw + c * 16;
-    const bool rok = r < M && !row_bad[r < M ? r : 0];
-    const float* xrow = X + (size_t)(r < M ? r : 0) * ldx;
-    const float inv = r < M ? row_inv[r] : 0.0f;
-    const bool xvec = (ldx & 3) == 0 && ((uintptr_t)X & 15) == 0;
-    // the 16 inputs of k-step kk of this lane, quantized and packed four per int
-    auto quant16 = [&](int kk) -> v4i {
+    bool rok[MB];
+    const float* xrow[MB];
+    float inv[MB];
+#pragma unroll
+    for (int b = 0; b < MB; ++b) {
+        const int m = 16 * b + r;
+        rok[b] = m < M && !row_bad[m < M ? m : 0];
+        xrow[b] = X + (size_t)(m < M ? m : 0) * ldx;
+        inv[b] = m < M ? row_inv[m] : 0.0f;
+    }
+    // the 16 inputs of k-step kk of this lane in row block b, quantized and packed four per int
+    auto quant16 = [&](int b, int kk) -> v4i {
         const int j0 = kk * 64 + c * 16;
         float v[16];
         if (xvec && j0 + 16 <= kx) {
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                const float4 f = *reinterpret_cast<const float4*>(xrow + j0 + 4 * u);
+                const float4 f = *reinterpret_cast<const float4*>(xrow[b] + j0 + 4 * u);
                 v[4 * u] = f.x; v[4 * u + 1] = f.y; v[4 * u + 2] = f.z; v[4 * u + 3] = f.w;
             }
         } else {
 #pragma unroll
-            for (int e = 0; e < 16; ++e) v[e] = j0 + e < kx ? xrow[j0 + e] : 0.0f;
+            for (int e = 0; e < 16; ++e) v[e] = j0 + e < kx ? xrow[b][j0 + e] : 0.0f;
         }
         v4i out;
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             int packed = 0;
 #pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                const float q = rintf(v[4 * u + b] * inv);
+            for (int e = 0; e < 4; ++e) {
+                const float q = rintf(v[4 * u + e] * inv[b]);
                 const int qi = (int)(q > 127.0f ? 127.0f : q < -127.0f ? -127.0f : q);
-                packed |= (qi & 0xff) << (8 * b);
+                packed |= (qi & 0xff) << (8 * e);
             }
             out[u] = packed;
         }
         return out;
     };
-    v4i acc = v4i{0, 0, 0, 0};
+    v4i acc[MB];
+#pragma unroll
+    for (int b = 0; b < MB; ++b) acc[b] = v4i{0, 0, 0, 0};
     const v4i z = v4i{0, 0, 0, 0};
     const int nk = p.K / 64;
     const int rot = nk >= 2 * KS ? (int)(blockIdx.x % (unsigned)(nk / KS)) * KS : 0;  // as in i8gemm_skinny
     for (int k0 = wave; k0 < nk; k0 += KS * KT) {
-        v4i wf[KT], af[KT];
+        v4i wf[KT], af[KT][MB];
 #pragma unroll
         for (int j = 0; j < KT; ++j) {
             const int kk = k0 + j * KS;
             const int kr = kk + rot < nk ? kk + rot : kk + rot - nk;
             wf[j] = kk < nk ? *(const v4i*)(wrow + (size_t)kr * 64) : z;
-            af[j] = (kk < nk && rok) ? quant16(kr) : z;
+#pragma unroll
+            for (int b = 0; b < MB; ++b) af[j][b] = (kk < nk && rok[b]) ? quant16(b, kr) : z;
         }
 #pragma unroll
-        for (int j = 0; j < KT; ++j) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[j], wf[j], acc, 0, 0, 0);
+        for (int j = 0; j < KT; ++j)
+#pragma unroll
+            for (int b = 0; b < MB; ++b) acc[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[j][b], wf[j], acc[b], 0, 0, 0);
     }
 #pragma unroll
-    for (int e = 0; e < 4; ++e) part[wave][4 * c + e][r] = acc[e];
+    for (int b = 0; b < MB; ++b)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) part[wave][b][4 * c + e][r] = acc[b][e];
     __syncthreads();
     // rows < M × 16 columns: the exact int32 sum of the waves' partial tiles, then the epilogue with the row scale
-    for (int i = threadIdx.x; i < 16 * 16; i += KS * 64) {
-        const int row = i >> 4, col = i & 15, n = n0 + col;
+    for (int i = threadIdx.x; i < MB * 256; i += KS * 64) {
+        const int b = i >> 8, row = 16 * b + ((i >> 4) & 15), col = i & 15, n = n0 + col;
         if (row >= M || n >= p.N) continue;
         int a = 0;
 #pragma unroll
-        for (int w = 0; w < KS; ++w) a += part[w][row][col];
+        for (int w = 0; w < KS; ++w) a += part[w][b][row & 15][col];
         float v = (float)a * row_s[row];  // ((float)acc · sx) · scale + bias, each step rounded
         v = v * p.sw[n];
         if (p.bias) v = v + p.bias[n];
@@ -1637,9 +1681,12 @@ extern "C" int knx_hip_qlinear(const float* x, int ldx, int rows, int k, int kp,
     // KNX_QLINEAR=split: always the quantizer followed by the GEMM (tests)
     const char* mode = getenv("KNX_QLINEAR");
     const bool split = mode != nullptr && strcmp(mode, "split") == 0;
-    if (rows <= 4 && !split) {
+    // One kernel while every workgroup's own pass over the fp32 rows stays cheap: each of the n/16 workgroups reads
+    // all rows twice, so the fused form loses once rows·k·n passes 2^23 (784×512 layer: 6.0 against 7.5 µs at 8 rows,
+    // 9.6 against 7.4 at 32; 4096×4096: 11.6 against 10.5 µs already at 1 row)
+    if (rows <= 16 && (long long)rows * k * n <= (1LL << 23) && !split) {
         I8Args p{rows, n, kp, nullptr, 0, nullptr, W, ldw, sw, bias, act, alpha, accumulate, Y, ldy, nullptr, 0, 0, 0, R, ldr};
-        hipLaunchKernelGGL((i8gemm_skinny_q<8, 4>), dim3((unsigned)((n + 15) / 16)), dim3(8 * 64), 0, s, p, x, ldx, k);
+        hipLaunchKernelGGL((i8gemm_skinny_q<8, 4, 1>), dim3((unsigned)((n + 15) / 16)), dim3(8 * 64), 0, s, p, x, ldx, k);
         return knx::check_launch(name);
     }
     KNX_REQUIRE(xq != nullptr && sx != nullptr, name);
@@ -1745,7 +1792,7 @@ extern "C" int knx_hip_qlinear_noalloc(const float* x, int ldx, int rows, int k,
         sx = reinterpret_cast<float*>(base);
         xq = reinterpret_cast<int8_t*>(base + ((size_t)rows * sizeof(float) + 255) / 256 * 256);
     }
-    // the same kernels and arguments as knx_hip_qlinear (rows <= 4 quantize inside the GEMM and use no scratch)
+    // the same kernels and arguments as knx_hip_qlinear (its one-kernel form writes no scratch)
     return knx_hip_qlinear(x, ldx, rows, k, kp, xq, sx, W, ldw, n, sw, bias, act, alpha, accumulate, R, ldr, Y, ldy,
                            stream);
 }

@@ -176,12 +176,13 @@ def test_i8gemm_residual(L, monkeypatch, variant, M, N, K, inplace):
     assert np.array_equal(host(Y), want)
 
 
-@pytest.mark.parametrize("rows", [1, 2, 3, 4, 5, 9])
+@pytest.mark.parametrize("rows", [1, 2, 3, 4, 5, 9, 16, 17, 33, 64, 65])
 @pytest.mark.parametrize("k,n", [(784, 512), (4096, 4096), (64, 10), (200, 33)])
 @pytest.mark.parametrize("path", ["fused", "split"])
 def test_qlinear(L, monkeypatch, rows, k, n, path):
     """knx_hip_qlinear (kernix_qmatmul + act) against the oracle's kernix_qmatmul, bit-exact: one-kernel quantize-on-
-    the-fly path at ≤ 4 rows, quantizer + GEMM above and when forced; a zero row and (from 3 rows) a row with inf"""
+    the-fly path at ≤ 16 rows for the small weights, quantizer + GEMM above and when forced; a zero row and (from 3
+    rows) a row with inf"""
     if path == "split":
         monkeypatch.setenv("KNX_QLINEAR", "split")
     rng = np.random.default_rng(rows * 131 + k + n)
