@@ -30,6 +30,9 @@ HIP_FLAGS = [
     "-mllvm", "-pragma-unroll-threshold=1000000",
     "-Wall", "-Wno-unused-function",
 ]
+# KNX_TUNING=1: also build the kernel variants that only the forcing switches (KNX_I8_KERNEL, KNX_SGEMM_KERNEL) reach
+if os.environ.get("KNX_TUNING", "") not in ("", "0"):
+    HIP_FLAGS.append("-DKNX_TUNING")
 C_FLAGS = ["-O2", "-std=c11", "-fPIC", "-fvisibility=hidden", "-D_GNU_SOURCE", "-ffp-contract=off",
            "-Wall", "-Wextra", "-Wno-unused-parameter"]
 

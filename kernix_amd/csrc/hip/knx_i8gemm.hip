@@ -1592,26 +1592,29 @@ static int i8gemm_run(I8Args p, hipStream_t s, const char* name)
     const char* force = getenv("KNX_I8_KERNEL");
     if (force != nullptr && *force) {
         const std::string f(force);
-        if (f == "tile256") return launch_tile<256, 256, 2, 2>(p, s, name);
         if (f == "tile64") return launch_tile<64, 64, 1, 1>(p, s, name);
+        if (f == "pipe64") return launch_pipe<64, 64, 2, 2, 4>(p, s, name);
+        if (f == "k128w8t" && k128_fits<256, 256>(p)) return launch_k128<256, 256, 4, 2, 2>(p, s, name);
+        if (f == "k128w8ta3e" && k128_fits<256, 256>(p)) return launch_k128<256, 256, 4, 2, 3, true>(p, s, name);
+        if (f == "k128m" && k128_fits<128, 128>(p)) return launch_k128<128, 128, 2, 2, 2>(p, s, name);
+        if (f == "k128ma3" && k128_fits<128, 128>(p)) return launch_k128<128, 128, 2, 2, 3>(p, s, name);
+        if (f == "ring64s4" && k128_fits<64, 64>(p)) return launch_ring<64, 64, 2, 2, 4, 1>(p, s, name);
+        if (f == "ring64g2" && k128_fits<64, 64>(p) && ring_split_fits<2, 4>(p)) return launch_ring<64, 64, 2, 2, 4, 1, 2>(p, s, name);
+#ifdef KNX_TUNING
+        // variants no shape selects (measured slower where they fit), built only for tuning (-DKNX_TUNING)
+        if (f == "tile256") return launch_tile<256, 256, 2, 2>(p, s, name);
         if (f == "pipe256") return launch_pipe<256, 256, 2, 2, 4>(p, s, name);
         if (f == "pipe256w8") return launch_pipe<256, 256, 2, 4, 4>(p, s, name);
         if (f == "pipe256s3") return launch_pipe<256, 256, 2, 2, 3>(p, s, name);
         if (f == "pipe128") return launch_pipe<128, 128, 2, 2, 4>(p, s, name);
-        if (f == "pipe64") return launch_pipe<64, 64, 2, 2, 4>(p, s, name);
         if (f == "k128" && k128_fits<256, 256>(p)) return launch_k128<256, 256, 2, 2, 2>(p, s, name);
         if (f == "k128w8" && k128_fits<256, 256>(p)) return launch_k128<256, 256, 2, 4, 2>(p, s, name);
-        if (f == "k128w8t" && k128_fits<256, 256>(p)) return launch_k128<256, 256, 4, 2, 2>(p, s, name);
         if (f == "k128w8ta3" && k128_fits<256, 256>(p)) return launch_k128<256, 256, 4, 2, 3>(p, s, name);
-        if (f == "k128w8ta3e" && k128_fits<256, 256>(p)) return launch_k128<256, 256, 4, 2, 3, true>(p, s, name);
         if (f == "k128w16" && k128_fits<256, 256>(p)) return launch_k128<256, 256, 4, 4, 2>(p, s, name);
-        if (f == "k128m" && k128_fits<128, 128>(p)) return launch_k128<128, 128, 2, 2, 2>(p, s, name);
-        if (f == "k128ma3" && k128_fits<128, 128>(p)) return launch_k128<128, 128, 2, 2, 3>(p, s, name);
         if (f == "pp" && k128_fits<256, 256>(p)) return launch_pp<256, 256>(p, s, name);
-        if (f == "ring64s4" && k128_fits<64, 64>(p)) return launch_ring<64, 64, 2, 2, 4, 1>(p, s, name);
         if (f == "ring64s8k2" && k128_fits<64, 64>(p)) return launch_ring<64, 64, 2, 2, 8, 2>(p, s, name);
-        if (f == "ring64g2" && k128_fits<64, 64>(p) && ring_split_fits<2, 4>(p)) return launch_ring<64, 64, 2, 2, 4, 1, 2>(p, s, name);
         if (f == "ring64s8" && k128_fits<64, 64>(p)) return launch_ring<64, 64, 2, 2, 8, 1>(p, s, name);
+#endif
         if (f == "skinny" && M <= 64) return M <= 16 ? launch_skinny<1>(p, s, name) : M <= 32 ? launch_skinny<2>(p, s, name) : launch_skinny<4>(p, s, name);
     }
     if (M <= 16) return launch_skinny<1>(p, s, name);

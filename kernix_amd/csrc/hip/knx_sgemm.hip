@@ -693,12 +693,15 @@ int dispatch_nt(SgArgs p, int batch, hipStream_t s, const char* name)
         if (strcmp(force, "t256") == 0 && k32_ok(p, 256, 256)) return launch_k32<256, 256, 4, 2>(p, batch, s, name);
         if (strcmp(force, "t128") == 0 && k32_ok(p, 128, 128)) return launch_k32<128, 128, 2, 2>(p, batch, s, name);
         if (strcmp(force, "t64") == 0 && k32_ok(p, 128, 64)) return launch_k32<128, 64, 4, 1>(p, batch, s, name);
+#ifdef KNX_TUNING
+        // variants no shape selects (measured slower where they fit), built only for tuning (-DKNX_TUNING)
         if (strcmp(force, "t128s3") == 0 && k32_ok(p, 128, 128)) return launch_k32<128, 128, 2, 2, 3>(p, batch, s, name);
         if (strcmp(force, "t64s3") == 0 && k32_ok(p, 128, 64)) return launch_k32<128, 64, 4, 1, 3>(p, batch, s, name);
         if (strcmp(force, "t64w2") == 0 && k32_ok(p, 128, 64)) return launch_k32<128, 64, 2, 2>(p, batch, s, name);
         if (strcmp(force, "t256x128") == 0 && k32_ok(p, 256, 128)) return launch_k32<256, 128, 4, 2>(p, batch, s, name);
         if (strcmp(force, "t256x192") == 0 && k32_ok(p, 256, 192)) return launch_k32<256, 192, 4, 2>(p, batch, s, name);
         if (strcmp(force, "t128x256") == 0 && k32_ok(p, 128, 256)) return launch_k32<128, 256, 2, 4>(p, batch, s, name);
+#endif
         if (strcmp(force, "skinny") == 0 && skinny_ok(p, batch)) return launch_skinny(p, s, name);
         return dispatch<true>(p, batch, s, name);
     }
