@@ -321,7 +321,15 @@ __global__ void __launch_bounds__(256) global_pool_kernel(int type, const float*
         const float* xp = x + b * (size_t)R * C + c;
         float o = xp[0];
         int r = 1;
-        // eight loads in flight, combined in row order (the reference's sequential order)
+        // 32 loads in flight (there is one thread per output, too few to cover the memory latency with less),
+        // combined in row order (the reference's sequential order)
+        for (; r + 32 <= R; r += 32) {
+            float v[32];
+#pragma unroll
+            for (int u = 0; u < 32; ++u) v[u] = xp[(size_t)(r + u) * C];
+#pragma unroll
+            for (int u = 0; u < 32; ++u) o = type == 0 ? (o > v[u] ? o : v[u]) : o + v[u];
+        }
         for (; r + 8 <= R; r += 8) {
             float v[8];
 #pragma unroll

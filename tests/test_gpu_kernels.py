@@ -447,15 +447,16 @@ def test_binary_broadcast_and_pool(L):
             da, db = dev(a), dev(b)
             hipabi.check(L.knx_hip_binary(op, ptr(da), ra, ca, ptr(db), rb, cb, ptr(y), B, R, C, hipabi.stream()))
             assert np.array_equal(host(y), want)
-    for R in (64, 13, 1):  # whole groups of eight rows, a remainder, a single row
-        x = rng.normal(0, 1, (4 * R, 256)).astype(np.float32)
+    # whole groups of 32 and of eight rows, remainders, a single row; channel counts a multiple of 64 and not
+    for R, C in ((64, 256), (13, 256), (1, 256), (130, 128), (64, 72), (13, 72)):
+        x = rng.normal(0, 1, (4 * R, C)).astype(np.float32)
         for t in (0, 1):
-            want = np.zeros((4, 256), np.float32)
-            knx_ref.lib().ko_global_pool(t, knx_ref._p(x), 4, R, 256, knx_ref._p(want))
-            y = torch.empty((4, 256), dtype=torch.float32, device="cuda")
+            want = np.zeros((4, C), np.float32)
+            knx_ref.lib().ko_global_pool(t, knx_ref._p(x), 4, R, C, knx_ref._p(want))
+            y = torch.empty((4, C), dtype=torch.float32, device="cuda")
             dx = dev(x)
-            hipabi.check(L.knx_hip_global_pool(t, ptr(dx), 4, R, 256, ptr(y), hipabi.stream()))
-            assert np.array_equal(host(y), want)
+            hipabi.check(L.knx_hip_global_pool(t, ptr(dx), 4, R, C, ptr(y), hipabi.stream()))
+            assert np.array_equal(host(y), want), (R, C, t)
 
 
 # ---------------------------------------------------------------- convolution
