@@ -409,25 +409,31 @@ def run_parts(args, out, want, configs):
         st = max(10, args.steps)
         fwarm = max(3, args.warmup)
         cpu = None if args.no_cpu else (threads, 2.0)
-        fw["int8_mlp_784_512_256_10_b64"] = forward_bench(
-            "mlp", lambda p: configs.int8_mlp(p, batch=64), configs.mlp_flops(64, (784, 512, 256, 10)), st, fwarm,
-            cpu=cpu)
-        # batch 1: the reference's int8 latency path (int8 arithmetic at ≤ 2 rows), quantize fused into the GEMM
-        fw["int8_mlp_784_512_256_10_b1"] = forward_bench(
-            "mlp", lambda p: configs.int8_mlp(p, batch=1), configs.mlp_flops(1, (784, 512, 256, 10)), st, fwarm,
-            i8_ops=configs.mlp_flops(1, (784, 512, 256, 10)))
-        fw["int8_mlp_784_512_256_10_b64_i8"] = forward_bench(
-            "mlp", lambda p: configs.int8_mlp(p, batch=64), configs.mlp_flops(64, (784, 512, 256, 10)), st, fwarm,
-            mode="i8", i8_ops=configs.mlp_flops(64, (784, 512, 256, 10)))
-        fw["fp32_mlp_4096_4096_4096_1000_b8192"] = forward_bench(
-            "f32", lambda p: configs.fp32_mlp(p), configs.mlp_flops(8192, (4096, 4096, 4096, 1000)), st, fwarm,
-            cpu=cpu)
-        fw["cnn_b256"] = forward_bench("cnn", lambda p: configs.cnn(p), configs.cnn_flops(), st, fwarm, cpu=cpu)
-        fw["transformer_4l_d512_b64"] = forward_bench(
-            "tr", lambda p: configs.transformer(p), configs.transformer_flops(), st, fwarm, cpu=cpu)
-        fw["transformer_4l_d512_b64_i8"] = forward_bench(
-            "tr", lambda p: configs.transformer(p), configs.transformer_flops(), st, fwarm, mode="i8",
-            i8_ops=configs.transformer_ffn_flops())
+        mlp = (784, 512, 256, 10)
+        lines = {
+            "int8_mlp_784_512_256_10_b64": lambda: forward_bench(
+                "mlp", lambda p: configs.int8_mlp(p, batch=64), configs.mlp_flops(64, mlp), st, fwarm, cpu=cpu),
+            # batch 1: the reference's int8 latency path (int8 arithmetic at ≤ 2 rows), quantize fused into the GEMM
+            "int8_mlp_784_512_256_10_b1": lambda: forward_bench(
+                "mlp", lambda p: configs.int8_mlp(p, batch=1), configs.mlp_flops(1, mlp), st, fwarm,
+                i8_ops=configs.mlp_flops(1, mlp)),
+            "int8_mlp_784_512_256_10_b64_i8": lambda: forward_bench(
+                "mlp", lambda p: configs.int8_mlp(p, batch=64), configs.mlp_flops(64, mlp), st, fwarm, mode="i8",
+                i8_ops=configs.mlp_flops(64, mlp)),
+            "fp32_mlp_4096_4096_4096_1000_b8192": lambda: forward_bench(
+                "f32", lambda p: configs.fp32_mlp(p), configs.mlp_flops(8192, (4096, 4096, 4096, 1000)), st, fwarm,
+                cpu=cpu),
+            "cnn_b256": lambda: forward_bench("cnn", lambda p: configs.cnn(p), configs.cnn_flops(), st, fwarm, cpu=cpu),
+            "transformer_4l_d512_b64": lambda: forward_bench(
+                "tr", lambda p: configs.transformer(p), configs.transformer_flops(), st, fwarm, cpu=cpu),
+            "transformer_4l_d512_b64_i8": lambda: forward_bench(
+                "tr", lambda p: configs.transformer(p), configs.transformer_flops(), st, fwarm, mode="i8",
+                i8_ops=configs.transformer_ffn_flops()),
+        }
+        only = {k for k in args.forward_only.split(",") if k}
+        for k, run in lines.items():
+            if not only or k in only:
+                fw[k] = run()
         for k, v in fw.items():
             cpu_txt = ""
             if "cpu_baseline" in v:
@@ -451,6 +457,8 @@ def main():
     ap.add_argument("--only", default="",
                     help="comma-separated subset for profiling runs: gemm4096, gemm_small, rows, conv, attention, "
                          "forward (the JSON line then lacks the parts not run)")
+    ap.add_argument("--forward-only", default="",
+                    help="comma-separated subset of the .knx forward lines (their keys, e.g. cnn_b256), for profiling runs")
     ap.add_argument("--no-sustained", action="store_true",
                     help="time the headline GEMM only in the burst form (profiling runs with few launches)")
     ap.add_argument("--calibrate", action="store_true",
