@@ -38,6 +38,9 @@
  *   knx_hip_upsample        kernix_upsample_run                                 include/kernix_model.h:970-984
  *   knx_hip_embedding       kernix_embedding_run                                include/kernix_model.h:987-1000
  *   knx_hip_rnn_gates       per-timestep gate update of kernix_rnn_dir          include/kernix_model.h:580-631
+ *   knx_hip_linear_chain    consecutive LINEAR steps of a small batch           include/kernix_model.h:1843-1860,
+ *                           (kernix_step_run layer after layer, int8 ones       :99-182
+ *                           through kernix_qmatmul)
  */
 #ifndef KNX_HIP_H
 #define KNX_HIP_H
@@ -121,6 +124,37 @@ KNX_API int knx_hip_qlinear(const float* x, int ldx, int rows, int k, int kp, in
 KNX_API int knx_hip_qlinear_noalloc(const float* x, int ldx, int rows, int k, int kp, const int8_t* W, int ldw, int n,
                                     const float* sw, const float* bias, int act, float alpha, int accumulate,
                                     const float* R, int ldr, float* Y, int ldy, void* stream);
+
+/* ---- a chain of Linear layers over a few rows, one launch ----
+ * Layer 0 reads x (rows × k fp32, stride ldx), layer l > 0 reads the output of layer l − 1 (k of layer l = n of layer
+ * l − 1); every layer writes y = act(x·Wᵀ + bias) (rows × n, stride ldy).  An int8 layer (i8 = 1; w: n rows of kp
+ * int8, stride ldw bytes, zero past k, kp ≤ 2048; sw: n scales) quantizes its input rows as knx_hip_quantize_rows
+ * and computes the epilogue of knx_hip_i8gemm, the same bits as knx_hip_qlinear; an fp32 layer (w: n rows of k
+ * floats, stride ldw) sums in its own order.  1 ≤ rows ≤ 64, at most KNX_CHAIN_MAX_LAYERS layers, every k a multiple
+ * of 4, x and every y but the last 16-byte aligned with strides multiple of 4 floats; a layer's output must not
+ * overlap its input.  The layers are separated by barriers across the launch's workgroups (at most one per CU, all
+ * resident at once).  scratch (knx_hip_linear_chain_scratch bytes, 256-byte aligned) holds the barrier words: zero
+ * before the first call (each call leaves them ready for the next); calls that share a scratch must not overlap.  A barrier that
+ * waits ≈ 1 s without the other workgroups arriving (they could not be resident) stops waiting and raises a flag
+ * that knx_hip_chain_status reports (the outputs are then wrong). */
+#define KNX_CHAIN_MAX_LAYERS 8
+typedef struct {
+    const void* w;
+    const float* sw;
+    const float* bias;  /* n values or NULL */
+    float* y;
+    int k, kp, n, ldw, ldy;
+    int act;            /* KERNIX_ACT_* id, −1 none */
+    int i8;
+    float alpha;        /* activation parameter */
+} knx_chain_layer;
+KNX_API size_t knx_hip_linear_chain_scratch(const knx_chain_layer* layers, int n_layers, int rows); /* 0: bad shape */
+KNX_API int knx_hip_linear_chain(const float* x, int ldx, int rows, const knx_chain_layer* layers, int n_layers,
+                                 void* scratch, size_t scratch_bytes, void* stream);
+/* 1 if a chain launch stopped waiting at a barrier since the previous call (read after synchronizing), else 0 */
+KNX_API int knx_hip_chain_status(void);
+/* Fills bytes of device memory with a byte value, ordered on stream. */
+KNX_API int knx_hip_memset(void* p, int value, size_t bytes, void* stream);
 
 /* dst (K×N row-major fp32) = (float)q[n][k] · scale[n]; q is N×K int8 with row stride ldq bytes. */
 KNX_API int knx_hip_dequant(const int8_t* q, int ldq, const float* scale, int K, int N, float* dst, void* stream);

@@ -152,6 +152,15 @@ extern "C" int knx_hip_memcpy_d2d(void* dst, const void* src, size_t bytes, void
     return copy(dst, src, bytes, hipMemcpyDeviceToDevice, stream, "knx_hip_memcpy_d2d");
 }
 
+extern "C" int knx_hip_memset(void* p, int value, size_t bytes, void* stream)
+{
+    KNX_ENTRY("knx_hip_memset");
+    if (bytes == 0) return KNX_OK;
+    KNX_REQUIRE(p != nullptr, "knx_hip_memset");
+    const hipError_t e = hipMemsetAsync(p, value, bytes, knx::as_stream(stream));
+    return e == hipSuccess ? KNX_OK : knx::fail(KNX_EHIP, "knx_hip_memset(%zu): %s", bytes, hipGetErrorString(e));
+}
+
 extern "C" int knx_hip_stream_create(void** stream)
 {
     KNX_ENTRY("knx_hip_stream_create");

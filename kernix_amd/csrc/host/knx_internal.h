@@ -46,6 +46,8 @@ struct knx_dmodel {
     void* arena;      /* workspace: storage buffers, step scratch, dequantized copies, input staging */
     size_t arena_bytes;
     float* d_in;      /* device copy of the current chunk's input */
+    void* chain;      /* scratch of knx_hip_linear_chain (barrier words, zero between launches; partial maxima) */
+    size_t chain_bytes;
     float* h_out;     /* pinned host output of an unchunked forward (batch × out_dim) */
     size_t h_out_floats;
     int out_all_pinned; /* out_all->tensor was allocated pinned */

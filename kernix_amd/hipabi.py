@@ -18,6 +18,12 @@ class ConvGeom(ctypes.Structure):
                 ("B", "H", "W", "C", "Ho", "Wo", "Co", "kh", "kw", "sh", "sw", "dh", "dw", "pt", "pl", "groups")]
 
 
+class ChainLayer(ctypes.Structure):
+    """knx_chain_layer (include/knx_hip.h)"""
+    _fields_ = [("w", P), ("sw", P), ("bias", P), ("y", P), ("k", I), ("kp", I), ("n", I), ("ldw", I), ("ldy", I),
+                ("act", I), ("i8", I), ("alpha", F)]
+
+
 SIGS = {
     "knx_hip_init": ([], I),
     "knx_hip_last_error": ([], ctypes.c_char_p),
@@ -44,6 +50,10 @@ SIGS = {
     "knx_hip_add_const": ([P, P, I, I, P, P], I),
     "knx_hip_attention_core": ([P, P, P, P, P, I, I, I, I, I, I, F, I, P], I),
     "knx_hip_attention_core_ex": ([P, I, P, I, P, I, P, P, P, I, I, I, I, I, I, F, I, P], I),
+    "knx_hip_linear_chain_scratch": ([ctypes.POINTER(ChainLayer), I, I], Z),
+    "knx_hip_linear_chain": ([P, I, I, ctypes.POINTER(ChainLayer), I, P, Z, P], I),
+    "knx_hip_chain_status": ([], I),
+    "knx_hip_memset": ([P, I, Z, P], I),
 }
 
 _lib = None

@@ -261,3 +261,57 @@ def test_forward_device_output_paths(tmp_path, case):
         s.synchronize()
         assert np.array_equal(out.cpu().numpy().reshape(40, -1), want)
     m.close()
+
+
+# ---------------------------------------------------------------- Linear chains (one launch for consecutive Linears)
+@pytest.mark.parametrize("mode", ["ref", "i8"])
+@pytest.mark.parametrize("batch", [1, 2, 17, 64])
+def test_linear_chain_matches_separate_steps(tmp_path, monkeypatch, mode, batch):
+    """The int8 MLP's three Linear steps as one chain launch (≤ 64 rows) against the same steps launched one by one
+    (KNX_CHAIN=0): the same bits wherever the layers run int8 arithmetic (i8 mode, or ≤ 2 rows), within 1e-5 where
+    they run fp32 on the dequantized weights (another summation order)."""
+    p = str(tmp_path / "mlp.knx")
+    x = configs.int8_mlp(p, batch=batch)
+    got = {}
+    for chain in ("1", "0"):
+        monkeypatch.setenv("KNX_CHAIN", chain)
+        m = Model(p)
+        if mode == "i8":
+            m.set_int8_mode(INT8_I8)
+        got[chain] = m(x).copy()
+        got[chain + "again"] = m(x).copy()
+        m.close()
+    assert np.array_equal(got["1"], got["1again"])
+    if mode == "i8" or batch <= 2:
+        assert np.array_equal(got["1"], got["0"])
+    else:
+        assert rel_err(got["1"], got["0"]) <= 1e-5
+
+
+def test_linear_chain_graph_boundaries(tmp_path):
+    """Chains inside a graph: a run broken by a value that two steps read, a Linear whose output feeds a fused add,
+    a layer_norm between Linears, int8 and fp32 weights mixed, pieces of ≤ 64 rows through the workspace limit;
+    against the oracle in both modes."""
+    from kernix_amd.knxfile import ModelBuilder
+
+    rng = np.random.default_rng(21)
+
+    def w(i, o):
+        return rng.normal(0, 1.0 / np.sqrt(i), (i, o))
+
+    b = ModelBuilder((48,))
+    h1 = b.linear(b.input, w(48, 64), rng.normal(0, 0.1, 64), activation="relu", fmt="i8_col")
+    h2 = b.linear(h1, w(64, 64), rng.normal(0, 0.1, 64), activation="gelu")
+    h3 = b.linear(h2, w(64, 32), None, activation="relu", fmt="i8_col")
+    h4 = b.linear(h3, w(32, 64), rng.normal(0, 0.1, 64), fmt="i8_col")
+    r = b.add(h4, h1)  # h1 read twice: the run h1 → h2 stops there; h4 feeds a fused add
+    n = b.layer_norm(r, np.ones(64), np.zeros(64))
+    h5 = b.linear(n, w(64, 40), rng.normal(0, 0.1, 40), activation="leaky_relu", alpha=0.2, fmt="i8_col")
+    h6 = b.linear(h5, w(40, 24), rng.normal(0, 0.1, 24), activation="tanh")
+    b.linear(h6, w(24, 8), rng.normal(0, 0.1, 8), fmt="i8_col")
+    p = b.save(str(tmp_path / "g.knx"))
+    x = rng.normal(0, 1, (100, 48)).astype(np.float32)
+    for mode in ("ref", "i8"):
+        check(p, x[:2], mode=mode, tol=1e-4 if mode == "ref" else 1e-2)
+        check(p, x[:40], mode=mode, tol=1e-4 if mode == "ref" else 1e-2)
+        check(p, x, mode=mode, tol=1e-4 if mode == "ref" else 1e-2, workspace_mb=0.05)
