@@ -55,6 +55,15 @@ struct knx_dmodel {
     int done_recorded;  /* `done` has been recorded after the last forward */
     int have_last;      /* a forward (or workspace set-up) has been enqueued */
     void* last_stream;  /* the stream it was enqueued on */
+    /* host-buffer forwards of large batches: input copies on their own stream, overlapped with the compute of the
+     * previous piece (created on first use) */
+    void* copy_stream;
+    void* ev_in[2];     /* piece's input copied into half h of d_in */
+    void* ev_used[2];   /* the compute that reads half h of d_in has been enqueued before this point */
+    /* pinned staging ring for input copies from pageable host memory (created on first use) */
+    void* ring[4];
+    void* ring_ev[4];   /* the copy out of slot k has completed after this event */
+    int ring_next;
 };
 
 /* A decoded .knx file: its header and op records in file order (inputs, arguments, host weights). */

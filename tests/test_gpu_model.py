@@ -315,3 +315,43 @@ def test_linear_chain_graph_boundaries(tmp_path):
         check(p, x[:2], mode=mode, tol=1e-4 if mode == "ref" else 1e-2)
         check(p, x[:40], mode=mode, tol=1e-4 if mode == "ref" else 1e-2)
         check(p, x, mode=mode, tol=1e-4 if mode == "ref" else 1e-2, workspace_mb=0.05)
+
+
+# ---------------------------------------------------------------- host-buffer forward with overlapped copies
+@pytest.mark.parametrize("case", ["fp32", "int8_i8", "int8_i8_chunked", "transformer"])
+def test_overlapped_host_forward(tmp_path, monkeypatch, case):
+    """Batches with ≥ 32 MB of input run as sub-pieces whose input copies (through the pinned staging ring) overlap
+    the previous piece's compute (two halves of the staged input, ordered by events): against the same forward without
+    overlap (KNX_OVERLAP=0), the same bits where the rows are independent of the piece size (int8 arithmetic), within
+    1e-5 for fp32 GEMMs of other row counts; inside workspace chunking too; twice in a row (the halves' events carried
+    over)."""
+    p = str(tmp_path / "m.knx")
+    mode, ws = "ref", None
+    if case == "fp32":
+        x = configs.fp32_mlp(p, batch=8400, dims=(1024, 512, 256, 100))
+    elif case == "transformer":
+        x = configs.transformer(p, batch=132, seq=128, d=512, heads=8, ffn=1024, layers=1)
+    else:
+        x = configs.int8_mlp(p, batch=11000)
+        mode = "i8"
+        if case == "int8_i8_chunked":
+            ws = 24.0
+    assert np.asarray(x, np.float32).nbytes >= 32 << 20
+    got = {}
+    for ov in ("1", "0"):
+        monkeypatch.setenv("KNX_OVERLAP", ov)
+        m = Model(p, workspace_mb=ws)
+        if mode == "i8":
+            m.set_int8_mode(INT8_I8)
+        got[ov] = m(x).copy()
+        got[ov + "b"] = m(x).copy()
+        m.close()
+    assert np.array_equal(got["1"], got["1b"])
+    if case.startswith("int8"):
+        assert np.array_equal(got["1"], got["0"])
+    else:
+        assert rel_err(got["1"], got["0"]) <= 1e-5
+    ref = knx_ref.parse(p)
+    xs = to_rows(Model(p), np.asarray(x)[:4])
+    want, _ = knx_ref.forward(ref, xs, mode=mode)
+    assert rel_err(got["1"][:4].reshape(4, -1), want) <= (1e-4 if mode == "ref" else 0.0)
