@@ -140,11 +140,11 @@ __device__ void item_i8(const LayerDev& L, int rows, __amdgpu_buffer_rsrc_t xr, 
     const __amdgpu_buffer_rsrc_t wr = rsrc(L.w, (long long)L.n * L.ldw);
     const int n = 16 * ct + r;
     const bool nok = n < L.n;
-    const int wbase = n * L.ldw + c * 16;
+    const int wbase = (nok ? n : 0) * L.ldw + c * 16;  // offsets of rows / channels that exist only (no overflow)
     const int nk = L.kp / 64;
     const int i = t >> 5, s0 = t & 31, m = 16 * rb + i;  // the row this thread quantizes
     const bool mok = m < rows;
-    const int K4 = L.k / 4, xbase = m * L.ldx * 4;
+    const int K4 = L.k / 4, xbase = (mok ? m : 0) * L.ldx * 4;
     // every load of the item at once
     float4 xv[kXS];
 #pragma unroll
@@ -219,7 +219,7 @@ __device__ void item_f32(const LayerDev& L, int rows, __amdgpu_buffer_rsrc_t xr,
     const __amdgpu_buffer_rsrc_t wr = rsrc(L.w, (long long)L.n * L.ldw * 4);
     const int n = 16 * ct + r, m = 16 * rb + r;
     const bool nok = n < L.n, mok = m < rows;
-    const int wbase = n * L.ldw * 4 + 16 * q, xbase = m * L.ldx * 4 + 16 * q;
+    const int wbase = (nok ? n : 0) * L.ldw * 4 + 16 * q, xbase = (mok ? m : 0) * L.ldx * 4 + 16 * q;
     const int nkc = (L.k + 15) / 16;
     const int ne = min(16 * ct + (t & 15), L.n - 1);
     const __amdgpu_buffer_rsrc_t br = rsrc(L.bias, L.bias ? (long long)L.n * 4 : 0);
