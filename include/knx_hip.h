@@ -151,7 +151,8 @@ typedef struct {
 KNX_API size_t knx_hip_linear_chain_scratch(const knx_chain_layer* layers, int n_layers, int rows); /* 0: bad shape */
 KNX_API int knx_hip_linear_chain(const float* x, int ldx, int rows, const knx_chain_layer* layers, int n_layers,
                                  void* scratch, size_t scratch_bytes, void* stream);
-/* 1 if a chain launch stopped waiting at a barrier since the previous call (read after synchronizing), else 0 */
+/* 1 if a launch with a grid barrier (knx_hip_linear_chain) stopped waiting since the previous call (read after
+ * synchronizing), else 0 */
 KNX_API int knx_hip_chain_status(void);
 /* Fills bytes of device memory with a byte value, ordered on stream. */
 KNX_API int knx_hip_memset(void* p, int value, size_t bytes, void* stream);

@@ -273,21 +273,6 @@ bool overlaps(const void* a, size_t na, const void* b, size_t nb)
     return x < y + nb && y < x + na;
 }
 
-int* g_err = nullptr;  // pinned host word raised by a barrier that stopped waiting
-std::mutex g_err_mu;
-
-int* err_word()
-{
-    std::lock_guard<std::mutex> lk(g_err_mu);
-    if (g_err == nullptr) {
-        void* p = nullptr;
-        if (hipHostMalloc(&p, sizeof(int), hipHostMallocDefault) != hipSuccess) return nullptr;
-        g_err = static_cast<int*>(p);
-        *g_err = 0;
-    }
-    return g_err;
-}
-
 constexpr size_t kScratchBytes = 256;  // the barrier words (one 64-bit word per barrier, layers − 1 of them)
 
 }  // namespace
@@ -330,7 +315,7 @@ extern "C" int knx_hip_linear_chain(const float* x, int ldx, int rows, const knx
         items_max = items > items_max ? items : items_max;
     }
     KNX_REQUIRE(scratch != nullptr && ((uintptr_t)scratch & 255) == 0 && scratch_bytes >= kScratchBytes, name);
-    int* err = err_word();
+    int* err = knx::grid_error_word();
     if (err == nullptr) return knx::fail(KNX_EHIP, "%s: cannot allocate the error word", name);
 
     ChainArgs a{};
@@ -357,12 +342,4 @@ extern "C" int knx_hip_linear_chain(const float* x, int ldx, int rows, const knx
     }
     hipLaunchKernelGGL(linear_chain, dim3((unsigned)G), dim3(kThreads), 0, knx::as_stream(stream), a);
     return knx::check_launch(name);
-}
-
-extern "C" int knx_hip_chain_status(void)
-{
-    std::lock_guard<std::mutex> lk(g_err_mu);
-    if (g_err == nullptr) return 0;
-    const int v = __atomic_exchange_n(g_err, 0, __ATOMIC_SEQ_CST);
-    return v != 0;
 }

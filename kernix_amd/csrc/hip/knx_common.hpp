@@ -18,6 +18,8 @@ bool injected(const char* name);
 int check_launch(const char* what);
 // Number of compute units of the current device (cached).
 int num_cus();
+// Pinned host word that a grid barrier (knx_grid.hpp) raises when it stops waiting; null if it cannot be allocated.
+int* grid_error_word();
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 

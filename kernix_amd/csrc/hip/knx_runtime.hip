@@ -57,7 +57,29 @@ int num_cus()
     return g_cus;
 }
 
+static int* g_grid_err = nullptr;  // pinned host word raised by a grid barrier that stopped waiting
+static std::mutex g_grid_err_mu;
+
+int* grid_error_word()
+{
+    std::lock_guard<std::mutex> lk(g_grid_err_mu);
+    if (g_grid_err == nullptr) {
+        void* p = nullptr;
+        if (hipHostMalloc(&p, sizeof(int), hipHostMallocDefault) != hipSuccess) return nullptr;
+        g_grid_err = static_cast<int*>(p);
+        *g_grid_err = 0;
+    }
+    return g_grid_err;
+}
+
 }  // namespace knx
+
+extern "C" int knx_hip_chain_status(void)
+{
+    std::lock_guard<std::mutex> lk(knx::g_grid_err_mu);
+    if (knx::g_grid_err == nullptr) return 0;
+    return __atomic_exchange_n(knx::g_grid_err, 0, __ATOMIC_SEQ_CST) != 0;
+}
 
 static std::once_flag g_init_once;
 static int g_init_rc = KNX_ENODEV;

@@ -355,3 +355,19 @@ def test_overlapped_host_forward(tmp_path, monkeypatch, case):
     xs = to_rows(Model(p), np.asarray(x)[:4])
     want, _ = knx_ref.forward(ref, xs, mode=mode)
     assert rel_err(got["1"][:4].reshape(4, -1), want) <= (1e-4 if mode == "ref" else 0.0)
+
+
+def test_ffn_fusions_full_size(tmp_path, monkeypatch):
+    """The Transformer at full size in i8 mode (8192 rows, d 512, FFN 2048, one layer): the fused steps (layer_norm +
+    quantize, GEMM + residual add) give the same bits as every step on its own (KNX_NO_FUSE=1), forward after forward."""
+    p = str(tmp_path / "t.knx")
+    x = configs.transformer(p, batch=64, layers=1)
+    outs = []
+    for no_fuse in ("0", "1"):
+        monkeypatch.setenv("KNX_NO_FUSE", no_fuse)
+        m = Model(p)
+        m.set_int8_mode(INT8_I8)
+        outs.append(np.array(m(x)))
+        outs.append(np.array(m(x)))
+        m.close()
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
