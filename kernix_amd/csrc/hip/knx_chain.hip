@@ -4,9 +4,11 @@
 // MFMAs, outputs written) and a launch costs about as much again, so a chain of layers (the int8 MLP at batch 1 to
 // 64: reference kernix_step_run, include/kernix_model.h:1843-1860, layer after layer) runs here as one grid: the
 // layers one after the other, separated by barriers across the grid (knx_grid.hpp: one workgroup per CU at most,
-// all resident at once).  Inside a layer the work is split into items of 16 rows × 16 output channels; an item's
-// K range is split over the 8 waves of its workgroup (16×16×64 int8 or 16×16×4 fp32 MFMA, the partial tiles summed
-// through LDS in wave order), and its epilogue applies bias and activation.
+// all resident at once).  Inside a layer the work is split into items of 16 rows × 16 output channels (int8 layers:
+// × 1, 2 or 4 adjacent blocks of 16 channels, so that at more rows the grid, and with it the cost of each barrier,
+// stays small while an item's input rows are loaded and quantized once for all of its channels); an item's K range
+// is split over the 8 waves of its workgroup (16×16×64 int8 or 16×16×4 fp32 MFMA, the partial tiles summed through
+// LDS in wave order), and its epilogue applies bias and activation.
 //
 // Latency is the whole cost here (one memory round trip ≈ 1.2–1.8 µs on MI355X), so each item issues all of its
 // loads at once — weight fragments, input rows, per-channel scales and bias — and waits once.
@@ -21,6 +23,7 @@
 // XCDs share), and after each barrier the workgroup drops its cached copies of other agents' data (knx_grid.hpp),
 // so every input row is read with ordinary loads: each line once per XCD from memory, then from the XCD's L2.
 #include <float.h>
+#include <algorithm>
 #include <math.h>
 #include <mutex>
 #include <string.h>
@@ -36,6 +39,8 @@ namespace {
 
 constexpr int kThreads = 512, kWaves = 8;
 constexpr int kMaxRows = 64;
+constexpr int kMaxBlocks = 8;                   // 16-channel blocks per int8 item (at most 2 when kp > 1024)
+constexpr int kTargetItems = 16;                // items per int8 layer the grid aims for, per row block (≤ 2)
 constexpr int kI8Steps = 4;                     // 64-wide k-steps per wave of an int8 item: k ≤ 8·4·64
 constexpr int kMaxI8K = kWaves * kI8Steps * 64;
 constexpr int kF32Chunks = 8;                   // 16-wide k-chunks per wave and pass of an fp32 item
@@ -48,6 +53,7 @@ struct LayerDev {
     const float* x;     // input rows (layer 0: the caller's x, then the previous layer's y)
     float* y;
     int k, kp, n, ldw, ldx, ldy, act, i8, last;
+    int cb;             // 16-channel blocks per item (int8: 1, 2 or 4; fp32: 1)
     float alpha;
 };
 
@@ -89,35 +95,41 @@ __device__ __forceinline__ float mag(float v)
 constexpr int kQPitch = kMaxI8K + 16;  // bytes per quantized row in LDS
 
 struct Shared {
-    int part[kWaves][16][17];               // per-wave partial tiles (int32, or fp32 bits)
+    int part[kWaves][kMaxBlocks][16][17];   // per-wave partial tiles (int32, or fp32 bits), per channel block
     float rsx[16];                          // row scales of an int8 item's rows
     alignas(16) int8_t q[16][kQPitch];      // an int8 item's rows, quantized
 };
 
-// The item's output tile from the wave-partial tiles (summed in wave order), then bias, activation and the store.
-// Threads 0..255 hold (row t >> 4, channel t & 15); sw_n / b_n are that channel's scale and bias, loaded early.
-template <bool I8>
-__device__ void tile_epilogue(const LayerDev& L, int rows, int rb, int ct, float sw_n, float b_n, Shared& sh)
+// The item's output tile (16 rows × 16·CB channels) from the wave-partial tiles (summed in wave order), then bias,
+// activation and the store.  Output o = t + 512·p of the tile is row o / (16·CB), channel o % (16·CB) (a row's
+// channels to consecutive threads); sw_n[p] / b_n[p] are that channel's scale and bias, loaded early.
+template <bool I8, int CB>
+__device__ __forceinline__ void tile_epilogue(const LayerDev& L, int rows, int rb, int cg, const float* sw_n, const float* b_n,
+                              Shared& sh)
 {
+    constexpr int W16 = 16 * CB, EP = (16 * W16 + kThreads - 1) / kThreads;
     __syncthreads();
     const int t = threadIdx.x;
-    if (t < 256) {
-        const int i = t >> 4, col = t & 15, m = 16 * rb + i, n = 16 * ct + col;
+#pragma unroll
+    for (int p = 0; p < EP; ++p) {
+        const int o = t + kThreads * p;
+        if (o >= 16 * W16) break;
+        const int i = o / W16, cc = o % W16, b = cc >> 4, col = cc & 15, m = 16 * rb + i, n = W16 * cg + cc;
         if (m < rows && n < L.n) {
             float v;
             if (I8) {
                 int s = 0;
 #pragma unroll
-                for (int w = 0; w < kWaves; ++w) s += sh.part[w][i][col];
+                for (int w = 0; w < kWaves; ++w) s += sh.part[w][b][i][col];
                 // ((float)acc · sx) · scale + bias, each step rounded (reference include/kernix_model.h:167-177)
                 v = (float)s * sh.rsx[i];
-                v = v * sw_n;
+                v = v * sw_n[p];
             } else {
-                v = __int_as_float(sh.part[0][i][col]);
+                v = __int_as_float(sh.part[0][b][i][col]);
 #pragma unroll
-                for (int w = 1; w < kWaves; ++w) v = v + __int_as_float(sh.part[w][i][col]);
+                for (int w = 1; w < kWaves; ++w) v = v + __int_as_float(sh.part[w][b][i][col]);
             }
-            if (L.bias) v = v + b_n;
+            if (L.bias) v = v + b_n[p];
             v = knx_act(v, L.act, L.alpha);
             float* y = L.y + (size_t)m * L.ldy + n;
             if (L.last) *y = v;
@@ -127,20 +139,18 @@ __device__ void tile_epilogue(const LayerDev& L, int rows, int rb, int ct, float
     __syncthreads();  // the partial tiles are reused by the next item
 }
 
-// int8 item.  Loads: the 16 rows' fp32 values, thread t taking row t / 32 and the float4s t % 32, + 32, … (coalesced,
-// at most kXS = 16 per thread for k ≤ 2048); the weight fragments of lane (r, c) of wave w — output channel
-// 16·ct + r, bytes [16c, 16c + 16) of the 64-wide k-steps w, w + 8, w + 16, w + 24; the channel's scale and bias.
-// The 32 threads of a row reduce its maximum by lane exchanges (a half-wave) and quantize their values into the
-// row's LDS copy; the waves then read their MFMA fragments from there.
-constexpr int kXS = kMaxI8K / 4 / 32;
-
-__device__ void item_i8(const LayerDev& L, int rows, __amdgpu_buffer_rsrc_t xr, int rb, int ct, Shared& sh)
+// int8 item: rows 16·rb … and the CB channel blocks CB·cg … of 16 channels, at most KS 64-wide k-steps per wave
+// (kp ≤ 512·KS).  Loads: the 16 rows' fp32 values, thread t taking row t / 32 and the float4s t % 32, + 32, …
+// (coalesced, at most 4·KS per thread); per block b the weight fragments of lane (r, c) of wave w — output channel
+// 16·(CB·cg + b) + r, bytes [16c, 16c + 16) of the k-steps w, w + 8, …; the scales and biases of the channels the
+// thread stores.  The 32 threads of a row reduce its maximum by lane exchanges (a half-wave) and quantize their values
+// into the row's LDS copy; the waves then read their MFMA fragments from there, each fragment serving all blocks.
+template <int CB, int KS>
+__device__ __forceinline__ void item_i8(const LayerDev& L, int rows, __amdgpu_buffer_rsrc_t xr, int rb, int cg, Shared& sh)
 {
+    constexpr int W16 = 16 * CB, EP = (16 * W16 + kThreads - 1) / kThreads, kXS = KS * kWaves * 64 / 4 / 32;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6, r = lane & 15, c = lane >> 4;
     const __amdgpu_buffer_rsrc_t wr = rsrc(L.w, (long long)L.n * L.ldw);
-    const int n = 16 * ct + r;
-    const bool nok = n < L.n;
-    const int wbase = (nok ? n : 0) * L.ldw + c * 16;  // offsets of rows / channels that exist only (no overflow)
     const int nk = L.kp / 64;
     const int i = t >> 5, s0 = t & 31, m = 16 * rb + i;  // the row this thread quantizes
     const bool mok = m < rows;
@@ -152,15 +162,26 @@ __device__ void item_i8(const LayerDev& L, int rows, __amdgpu_buffer_rsrc_t xr, 
         const int j = s0 + 32 * q;
         xv[q] = ld4(xr, mok && j < K4 ? xbase + 16 * j : kOut);
     }
-    v4i wf[kI8Steps];
+    v4i wf[CB][KS];
 #pragma unroll
-    for (int j = 0; j < kI8Steps; ++j) {
-        const int kk = wave + j * kWaves;
-        wf[j] = ld4i(wr, nok && kk < nk ? wbase + kk * 64 : kOut);
+    for (int b = 0; b < CB; ++b) {
+        const int n = W16 * cg + 16 * b + r;
+        const bool nok = n < L.n;
+        const int wbase = (nok ? n : 0) * L.ldw + c * 16;  // offsets of channels that exist only (no overflow)
+#pragma unroll
+        for (int j = 0; j < KS; ++j) {
+            const int kk = wave + j * kWaves;
+            wf[b][j] = ld4i(wr, nok && kk < nk ? wbase + kk * 64 : kOut);
+        }
     }
-    const int ne = min(16 * ct + (t & 15), L.n - 1);
-    const float sw_n = ld1(rsrc(L.sw, (long long)L.n * 4), ne * 4);
-    const float b_n = ld1(rsrc(L.bias, L.bias ? (long long)L.n * 4 : 0), ne * 4);
+    const __amdgpu_buffer_rsrc_t swr = rsrc(L.sw, (long long)L.n * 4), br = rsrc(L.bias, L.bias ? (long long)L.n * 4 : 0);
+    float sw_n[EP], b_n[EP];
+#pragma unroll
+    for (int p = 0; p < EP; ++p) {
+        const int ne = min(W16 * cg + (t + kThreads * p) % W16, L.n - 1);
+        sw_n[p] = ld1(swr, ne * 4);
+        b_n[p] = ld1(br, ne * 4);
+    }
     // all of the above issued before the first wait: the scheduler would otherwise move the weight and scale loads
     // down to their first use, after the input rows' wait, for a second round trip
     __builtin_amdgcn_sched_barrier(0);
@@ -196,24 +217,29 @@ __device__ void item_i8(const LayerDev& L, int rows, __amdgpu_buffer_rsrc_t xr, 
     __syncthreads();
     // rows past the block's and bytes in [k, kp) hold stale LDS values: the former are never stored, the latter meet
     // the weight's zero padding
-    v4i acc = {0, 0, 0, 0};
+    v4i acc[CB];
 #pragma unroll
-    for (int j = 0; j < kI8Steps; ++j) {
+    for (int b = 0; b < CB; ++b) acc[b] = v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < KS; ++j) {
         const int kk = wave + j * kWaves;
         if (kk < nk) {
             const v4i af = *reinterpret_cast<const v4i*>(&sh.q[r][64 * kk + 16 * c]);
-            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, wf[j], acc, 0, 0, 0);
+#pragma unroll
+            for (int b = 0; b < CB; ++b) acc[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, wf[b][j], acc[b], 0, 0, 0);
         }
     }
-    // lane (r, c) holds rows 4c + e of channel r
+    // lane (r, c) holds rows 4c + e of channel r of each block
 #pragma unroll
-    for (int e = 0; e < 4; ++e) sh.part[wave][4 * c + e][r] = acc[e];
-    tile_epilogue<true>(L, rows, rb, ct, sw_n, b_n, sh);
+    for (int b = 0; b < CB; ++b)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sh.part[wave][b][4 * c + e][r] = acc[b][e];
+    tile_epilogue<true, CB>(L, rows, rb, cg, sw_n, b_n, sh);
 }
 
 // fp32 item: lane (r, q) of wave w holds row 16·rb + r and channel 16·ct + r, k = 16·kc + 4q + (0..3) of the
 // 16-wide k-chunks kc = w, w + 8, …, kF32Chunks of them per pass.
-__device__ void item_f32(const LayerDev& L, int rows, __amdgpu_buffer_rsrc_t xr, int rb, int ct, Shared& sh)
+__device__ __forceinline__ void item_f32(const LayerDev& L, int rows, __amdgpu_buffer_rsrc_t xr, int rb, int ct, Shared& sh)
 {
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6, r = lane & 15, q = lane >> 4;
     const __amdgpu_buffer_rsrc_t wr = rsrc(L.w, (long long)L.n * L.ldw * 4);
@@ -246,8 +272,9 @@ __device__ void item_f32(const LayerDev& L, int rows, __amdgpu_buffer_rsrc_t xr,
     }
     if (wave >= nkc) b_n = ld1(br, ne * 4);  // a wave without k-chunks (k < 128)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) sh.part[wave][4 * q + e][r] = __float_as_int(acc[e]);
-    tile_epilogue<false>(L, rows, rb, ct, 1.0f, b_n, sh);
+    for (int e = 0; e < 4; ++e) sh.part[wave][0][4 * q + e][r] = __float_as_int(acc[e]);
+    const float one = 1.0f;
+    tile_epilogue<false, 1>(L, rows, rb, ct, &one, &b_n, sh);
 }
 
 __global__ void __launch_bounds__(kThreads) linear_chain(ChainArgs a)
@@ -256,12 +283,25 @@ __global__ void __launch_bounds__(kThreads) linear_chain(ChainArgs a)
     const int rows = a.rows, RB = (rows + 15) / 16;
     for (int l = 0; l < a.layers; ++l) {
         const LayerDev& L = a.L[l];
-        const int items = RB * ((L.n + 15) / 16);
+        const int items = RB * ((L.n + 16 * L.cb - 1) / (16 * L.cb));
         const __amdgpu_buffer_rsrc_t xr = rsrc(L.x, (long long)rows * L.ldx * 4);
         for (int it = blockIdx.x; it < items; it += gridDim.x) {
-            const int rb = it % RB, ct = it / RB;
-            if (L.i8) item_i8(L, rows, xr, rb, ct, sh);
-            else item_f32(L, rows, xr, rb, ct, sh);
+            const int rb = it % RB, cg = it / RB;
+            if (!L.i8) item_f32(L, rows, xr, rb, cg, sh);
+            else if (L.kp > 1024) {
+                if (L.cb == 2) item_i8<2, 4>(L, rows, xr, rb, cg, sh);
+                else item_i8<1, 4>(L, rows, xr, rb, cg, sh);
+            } else if (L.kp > 512) {
+                if (L.cb == 8) item_i8<8, 2>(L, rows, xr, rb, cg, sh);
+                else if (L.cb == 4) item_i8<4, 2>(L, rows, xr, rb, cg, sh);
+                else if (L.cb == 2) item_i8<2, 2>(L, rows, xr, rb, cg, sh);
+                else item_i8<1, 2>(L, rows, xr, rb, cg, sh);
+            } else {
+                if (L.cb == 8) item_i8<8, 1>(L, rows, xr, rb, cg, sh);
+                else if (L.cb == 4) item_i8<4, 1>(L, rows, xr, rb, cg, sh);
+                else if (L.cb == 2) item_i8<2, 1>(L, rows, xr, rb, cg, sh);
+                else item_i8<1, 1>(L, rows, xr, rb, cg, sh);
+            }
         }
         if (l + 1 < a.layers) knx::grid_barrier(a.gs, (unsigned)l);
     }
@@ -291,7 +331,6 @@ extern "C" int knx_hip_linear_chain(const float* x, int ldx, int rows, const knx
     KNX_REQUIRE(layers != nullptr && n_layers >= 1 && n_layers <= KNX_CHAIN_MAX_LAYERS, name);
     KNX_REQUIRE(rows >= 1 && rows <= kMaxRows, name);
     KNX_REQUIRE(x != nullptr && ((uintptr_t)x & 15) == 0 && ldx % 4 == 0 && ldx >= layers[0].k, name);
-    int items_max = 1;
     for (int l = 0; l < n_layers; ++l) {
         const knx_chain_layer& L = layers[l];
         KNX_REQUIRE(L.k >= 4 && L.k % 4 == 0 && L.n >= 1 && L.n <= 1 << 20 && L.act >= -1 && L.act <= 15, name);
@@ -311,13 +350,15 @@ extern "C" int knx_hip_linear_chain(const float* x, int ldx, int rows, const knx
         KNX_REQUIRE(l == 0 || layers[l - 1].n == L.k, name);
         KNX_REQUIRE((long long)rows * ldin * 4 < (1LL << 31) - 16, name);
         KNX_REQUIRE(!overlaps(in, (size_t)rows * ldin * 4, L.y, (size_t)rows * L.ldy * 4), name);
-        const int items = (rows + 15) / 16 * ((L.n + 15) / 16);
-        items_max = items > items_max ? items : items_max;
     }
     KNX_REQUIRE(scratch != nullptr && ((uintptr_t)scratch & 255) == 0 && scratch_bytes >= kScratchBytes, name);
     int* err = knx::grid_error_word();
     if (err == nullptr) return knx::fail(KNX_EHIP, "%s: cannot allocate the error word", name);
 
+    // measured on the int8 MLP 784-512-256-10: 16 items at one row (14.3 µs against 15.2 at 32), 32 at 64 rows
+    // (16.8 µs against 19.1 at 16: with 16 workgroups each loads 156 KB of rows and weights in the first layer)
+    int target = kTargetItems * std::min((rows + 15) / 16, 2);
+    if (const char* e = getenv("KNX_CHAIN_ITEMS")) target = atoi(e) > 0 ? atoi(e) : target;  // tuning and tests
     ChainArgs a{};
     a.layers = n_layers;
     a.rows = rows;
@@ -331,6 +372,25 @@ extern "C" int knx_hip_linear_chain(const float* x, int ldx, int rows, const knx
         d.k = L.k; d.kp = L.kp; d.n = L.n; d.ldw = L.ldw; d.ldy = L.ldy; d.act = L.act; d.i8 = L.i8 != 0;
         d.alpha = L.alpha;
         d.last = l + 1 == n_layers;
+    }
+    // Items: an int8 layer's items take 1, 2, 4 or 8 blocks of 16 channels (at most 2 when kp > 1024).  A barrier
+    // costs more the more workgroups arrive at it (1.1 µs at 16, 1.2 at 32, 1.9 at 64, 3.1 at 128), and an item's
+    // input rows are loaded and quantized once for all of its blocks, so the grid is the largest layer's item count
+    // with the fewest blocks that bring each layer within the target (or as close as it gets), and then every layer
+    // takes the fewest blocks that fit that grid, i.e. as many workgroups as the barriers are paid for anyway.
+    const int RB = (rows + 15) / 16;
+    auto items_of = [&](const LayerDev& d, int cb) { return RB * (((d.n + 15) / 16 + cb - 1) / cb); };
+    auto max_blocks = [&](const LayerDev& d) { return !d.i8 ? 1 : d.kp > 1024 ? 2 : kMaxBlocks; };
+    int items_max = 1;
+    for (int l = 0; l < n_layers; ++l) {
+        int cb = 1;
+        while (cb < max_blocks(a.L[l]) && items_of(a.L[l], cb) > target) cb *= 2;
+        items_max = std::max(items_max, items_of(a.L[l], cb));
+    }
+    for (int l = 0; l < n_layers; ++l) {
+        LayerDev& d = a.L[l];
+        d.cb = 1;
+        while (d.cb < max_blocks(d) && items_of(d, d.cb) > items_max) d.cb *= 2;
     }
     // one workgroup per item of the widest layer, at most one per CU (all resident at once) and at most the
     // barrier's quantum

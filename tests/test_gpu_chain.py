@@ -183,6 +183,28 @@ def test_chain_few_workgroups(L, monkeypatch, wg):
     assert not (host(s[:64]).view(np.uint64) % 256).any()
 
 
+@pytest.mark.parametrize("target", ["1", "3", "1000"])
+@pytest.mark.parametrize("rows", [1, 17, 64])
+def test_chain_channel_blocks(L, monkeypatch, target, rows):
+    """int8 items of 1, 2, 4 or 8 blocks of 16 channels (the launch sizes the grid for a target item count and then
+    gives each layer the fewest blocks that fit it: 1 forces the most blocks, 1000 one block) over channel counts that
+    leave partial blocks and partial items, k > 1024 (at most 2 blocks), 512 < k ≤ 1024 and k ≤ 512, a NaN row
+    included; bit-exact against the oracle whatever the blocking"""
+    monkeypatch.setenv("KNX_CHAIN_ITEMS", target)
+    rng = np.random.default_rng(int(target) * 7 + rows)
+    dims = (1100, 700, 100, 36, 8)
+    ch = Chain(rng, rows, dims, ["i8", "i8", "f32", "i8"], [RELU, LEAKY, NONE, NONE])
+    x = rng.normal(0, 1, (rows, dims[0])).astype(np.float32)
+    if rows > 1:
+        x[rows - 1, 33] = np.nan
+    s, nb = ch.scratch(L)
+    for _ in range(2):
+        ch.run(L, x, s, nb)
+    check_layers(ch, x, ch.outputs())
+    assert not (host(s[:64]).view(np.uint64) % 256).any()
+    assert L.knx_hip_chain_status() == 0
+
+
 def test_chain_special_rows(L):
     """zero rows (scale 1), a row with inf and a row with NaN (int8: the row's outputs are NaN, and through a second
     int8 layer without activation NaN again; a ReLU in between turns NaN into 0, as the reference's threshold)"""
