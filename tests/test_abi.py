@@ -74,18 +74,20 @@ def test_forward_without_gpu_is_an_error_not_a_fallback(tmp_path):
 
 
 @pytest.mark.gpu
-def test_injected_device_failure_propagates(tmp_path):
-    """KNX_HIP_FAIL makes a kernel entry point fail: forward returns -1 (RuntimeError in Python), then recovers"""
+@pytest.mark.parametrize("batch,entry", [(32, "knx_hip_sgemm_nt_ep"), (3, "knx_hip_linear_chain")])
+def test_injected_device_failure_propagates(tmp_path, batch, entry):
+    """KNX_HIP_FAIL makes the kernel entry point the forward uses fail (fp32 Linears over 32 rows: one GEMM each; over
+    3 rows: one chain launch): forward returns -1 (RuntimeError in Python), then recovers"""
     code = f"""
 import os, sys
 sys.path.insert(0, {ROOT!r})
 import numpy as np
 from kernix_amd import configs
 from kernix_amd.kernix import Model
-x = configs.fp32_mlp({str(tmp_path / 'f.knx')!r}, batch=3, dims=(16, 32, 8))
+x = configs.fp32_mlp({str(tmp_path / 'f.knx')!r}, batch={batch}, dims=(16, 32, 8))
 m = Model({str(tmp_path / 'f.knx')!r})
 good = m(x)
-os.environ["KNX_HIP_FAIL"] = "knx_hip_sgemm_nt_ep"
+os.environ["KNX_HIP_FAIL"] = {entry!r}
 try:
     m(x)
     print("no error")

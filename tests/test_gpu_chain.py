@@ -122,6 +122,7 @@ def check_layers(ch, x, outs):
 
 
 MLP = (784, 512, 256, 10)
+QUANTUM = 256  # each launch adds this to every barrier word
 
 
 @pytest.mark.parametrize("rows", [1, 2, 3, 16, 17, 64])
@@ -140,7 +141,7 @@ def test_chain_mlp(L, rows, kind):
         for l in range(3):
             inp = ch.layer_ref(l, inp)
         assert np.array_equal(outs[-1], inp)
-    assert not (host(s[:64]).view(np.uint64) % 256).any(), "barrier words not at a multiple of 256"
+    assert not (host(s[:64]).view(np.uint64) % QUANTUM).any(), "barrier words not at a multiple of the quantum"
     assert L.knx_hip_chain_status() == 0
 
 
@@ -166,7 +167,7 @@ def test_chain_shapes(L, case):
     s, nb = ch.scratch(L)
     ch.run(L, x, s, nb)
     check_layers(ch, x, ch.outputs())
-    assert not (host(s[:64]).view(np.uint64) % 256).any()
+    assert not (host(s[:64]).view(np.uint64) % QUANTUM).any()
 
 
 @pytest.mark.parametrize("wg", ["1", "3", "7"])
@@ -180,7 +181,7 @@ def test_chain_few_workgroups(L, monkeypatch, wg):
     for _ in range(2):
         ch.run(L, x, s, nb)
     check_layers(ch, x, ch.outputs())
-    assert not (host(s[:64]).view(np.uint64) % 256).any()
+    assert not (host(s[:64]).view(np.uint64) % QUANTUM).any()
 
 
 @pytest.mark.parametrize("target", ["1", "3", "1000"])
@@ -201,7 +202,25 @@ def test_chain_channel_blocks(L, monkeypatch, target, rows):
     for _ in range(2):
         ch.run(L, x, s, nb)
     check_layers(ch, x, ch.outputs())
-    assert not (host(s[:64]).view(np.uint64) % 256).any()
+    assert not (host(s[:64]).view(np.uint64) % QUANTUM).any()
+    assert L.knx_hip_chain_status() == 0
+
+
+def test_chain_full_grid(L, monkeypatch):
+    """256 workgroups (one 16-channel block per item, 512 items in the wide layers, so two items each): every item
+    computed once, bit-exact, and the barrier words advance by one quantum per launch"""
+    monkeypatch.setenv("KNX_CHAIN_ITEMS", "100000")
+    rng = np.random.default_rng(11)
+    dims = (64, 2048, 64, 2048, 8)
+    ch = Chain(rng, 64, dims, ["i8", "i8", "i8", "i8"], [RELU, NONE, RELU, NONE])
+    x = rng.normal(0, 1, (64, dims[0])).astype(np.float32)
+    s, nb = ch.scratch(L)
+    before = host(s[:64]).view(np.uint64).copy()
+    for _ in range(3):
+        ch.run(L, x, s, nb)
+    check_layers(ch, x, ch.outputs())
+    words = host(s[:64]).view(np.uint64)
+    assert (words[:3] - before[:3] == 3 * QUANTUM).all(), words[:4]
     assert L.knx_hip_chain_status() == 0
 
 
