@@ -77,6 +77,10 @@ KNX_API int knx_hip_stream_destroy(void* stream);
 KNX_API int knx_hip_stream_sync(void* stream);
 /* Events (hipEvent_t as void*, created without timing): the runtime orders forwards issued on different streams. */
 KNX_API int knx_hip_event_create(void** event);
+/* An event that only orders this device's kernels: recording it performs no system-scope cache write-back or
+ * invalidation, so it must not publish data written by copies (host-to-device) or read by the host; for ordering
+ * kernels of one stream after kernels of another and for the host waiting until they are done. */
+KNX_API int knx_hip_event_create_ordering(void** event);
 KNX_API int knx_hip_event_destroy(void* event);
 KNX_API int knx_hip_event_record(void* event, void* stream);
 KNX_API int knx_hip_stream_wait_event(void* stream, void* event); /* later work on stream waits for the event */

@@ -184,7 +184,7 @@ static int ensure_device(kernix_model* m)
         m->dev = calloc(1, sizeof *m->dev);
         if (m->dev == NULL) return -1;
         if (hip_ok(knx_hip_stream_create(&m->dev->stream), "stream creation") != 0 ||
-            hip_ok(knx_hip_event_create(&m->dev->done), "event creation") != 0)
+            hip_ok(knx_hip_event_create_ordering(&m->dev->done), "event creation") != 0)
             return -1;
     }
     for (int i = 0; i < m->n_steps; i++) {
