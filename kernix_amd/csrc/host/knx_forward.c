@@ -413,7 +413,7 @@ void knx_model_release_device_all(kernix_model* m)
             knx_hip_event_destroy(m->dev->ev_in[h]);
             knx_hip_event_destroy(m->dev->ev_used[h]);
         }
-        for (int k = 0; k < 4; k++) {
+        for (int k = 0; k < KNX_RING_SLOTS; k++) {
             if (m->dev->ring_ev[k]) knx_hip_event_sync(m->dev->ring_ev[k]);
             knx_hip_event_destroy(m->dev->ring_ev[k]);
             knx_hip_host_free(m->dev->ring[k]);
@@ -1041,7 +1041,6 @@ static float* host_output(kernix_model* m, int samples, int chunked)
  * recorded after its DMA has completed.  fp32 MLP 8192 × 4096 forward from host buffers: 11.2 ms without overlap,
  * 8.2 ms overlapped with one copying thread, 7.4 ms with four.  Smaller inputs keep the runtime's copy (a 3 MB
  * input took 0.9 ms longer through the ring, the copying threads being woken for a single chunk). */
-#define KNX_RING_SLOTS 4
 #define KNX_RING_BYTES ((size_t)4 << 20)
 #define KNX_OVERLAP_MIN_BYTES ((size_t)32 << 20)
 

@@ -40,6 +40,8 @@ struct knx_dstep {
 };
 
 /* Device side of a model. */
+#define KNX_RING_SLOTS 4 /* pinned staging buffers of a host-buffer forward's input copies */
+
 struct knx_dmodel {
     void* stream;     /* hipStream_t owned by the model */
     int uploaded;     /* weights on the device */
@@ -61,8 +63,8 @@ struct knx_dmodel {
     void* ev_in[2];     /* piece's input copied into half h of d_in */
     void* ev_used[2];   /* the compute that reads half h of d_in has been enqueued before this point */
     /* pinned staging ring for input copies from pageable host memory (created on first use) */
-    void* ring[4];
-    void* ring_ev[4];   /* the copy out of slot k has completed after this event */
+    void* ring[KNX_RING_SLOTS];
+    void* ring_ev[KNX_RING_SLOTS];   /* the copy out of slot k has completed after this event */
     int ring_next;
 };
 
