@@ -758,20 +758,23 @@ int knx_conv_k32(const knx_conv_geom* g, const float* x, const float* wt, const 
         if (strcmp(tile, "256x256") == 0 && N >= 256 && M >= 256) return launch_conv_k32<256, 256, 4, 2>(p, s, name);
         if (strcmp(tile, "256x128") == 0 && N >= 128 && M >= 256) return launch_conv_k32<256, 128, 4, 2>(p, s, name);
         if (strcmp(tile, "128x128") == 0 && N >= 128 && M >= 128) return launch_conv_k32<128, 128, 2, 2>(p, s, name);
-        if (strcmp(tile, "64x128") == 0 && N >= 128 && M >= 64) return launch_conv_k32<64, 128, 2, 2>(p, s, name);
+        if (strcmp(tile, "128x128w8") == 0 && N >= 128 && M >= 128) return launch_conv_k32<128, 128, 4, 2>(p, s, name);
+        if (strcmp(tile, "64x128") == 0 && N >= 128 && M >= 64) return launch_conv_k32<64, 128, 2, 4>(p, s, name);
         if (strcmp(tile, "256x64") == 0 && N >= 64 && M >= 256) return launch_conv_k32<256, 64, 4, 1>(p, s, name);
-        if (strcmp(tile, "128x64") == 0 && N >= 64 && M >= 128) return launch_conv_k32<128, 64, 2, 2>(p, s, name);
+        if (strcmp(tile, "128x64") == 0 && N >= 64 && M >= 128) return launch_conv_k32<128, 64, 4, 2>(p, s, name);
     }
     if (N >= 256 && M >= 256 && tiles(256, 256) >= cus) return launch_conv_k32<256, 256, 4, 2>(p, s, name);
-    // 128 or more output channels: 64×128 tiles when that gives every CU two or more workgroups, so that one's
-    // prologue and epilogue overlap another's multiplies (CNN conv3, 256×32×32×64 → 128 stride 2: 84 µs as against 84
-    // for 256×128; conv4, 256×16×16×128 → 256 stride 2: 80 µs against 84 for 128×128)
-    if (N >= 128 && M >= 64 && tiles(64, 128) >= 2 * cus) return launch_conv_k32<64, 128, 2, 2>(p, s, name);
+    // Below that, 8 waves of 32×32 or 32×64 outputs per workgroup and two or more workgroups per CU: the tap gathers
+    // of 16 to 24 waves per CU hide each other's latency (CNN 3×3 convolutions over 256 images, 16 and 32 KB of
+    // weights: conv3, 32×32×64 → 128 stride 2, 80.3 µs on 128×128 tiles of 4×2 waves against 84.0 on 64×128 of 2×2;
+    // conv4, 16×16×128 → 256 stride 2, 77.7 µs on 64×128 of 2×4 waves against 80.0; 3 stages: 83-89 µs)
+    if (N >= 128 && M >= 128 && tiles(128, 128) >= 2 * cus) return launch_conv_k32<128, 128, 4, 2>(p, s, name);
+    if (N >= 128 && M >= 64 && tiles(64, 128) >= 2 * cus) return launch_conv_k32<64, 128, 2, 4>(p, s, name);
     if (N >= 128 && M >= 256 && tiles(256, 128) >= cus) return launch_conv_k32<256, 128, 4, 2>(p, s, name);
     if (N >= 128 && M >= 128 && tiles(128, 128) >= cus) return launch_conv_k32<128, 128, 2, 2>(p, s, name);
-    // 64 output channels: 128×64 tiles on 2×2 waves, several workgroups per CU (CNN conv2, 256×32×32×64 → 64:
-    // 169 µs, the same as 64×64 and 128×64 on 4×1 waves, against 174 for 256×64)
-    if (N >= 64 && M >= 128 && tiles(128, 64) >= 2 * cus) return launch_conv_k32<128, 64, 2, 2>(p, s, name);
+    // 64 output channels: 128×64 tiles on 4×2 waves (CNN conv2, 32×32×64 → 64: 161.7 µs, against 168.4 on 2×2 waves,
+    // 167.2 for 64×64 and 174 for 256×64)
+    if (N >= 64 && M >= 128 && tiles(128, 64) >= 2 * cus) return launch_conv_k32<128, 64, 4, 2>(p, s, name);
     if (N >= 64 && M >= 256 && tiles(256, 64) >= cus) return launch_conv_k32<256, 64, 4, 1>(p, s, name);
     return 1;
 }

@@ -521,7 +521,7 @@ def test_conv_residual(L, case):
     assert np.array_equal(host(dR), host(y))
 
 
-CONV_TILES = ["256x256", "256x128", "128x128", "64x128", "256x64", "128x64"]
+CONV_TILES = ["256x256", "256x128", "128x128", "128x128w8", "64x128", "256x64", "128x64"]
 # the tap mask of the pipelined gather: 1 tap, 25 taps, 49 (bits past 32), and 81 taps (more than the mask holds:
 # the general kernel); output pixels not a multiple of the tile
 CONV_TILE_CASES = [(64, 32, 32, 64, 64, 3, 1, 1, 1, 1), (128, 16, 16, 64, 128, 3, 1, 1, 1, 1),
