@@ -18,6 +18,8 @@ bandwidth-bound row kernels the same two ways; the convolution layers and the at
 samples/sec of the int8 MLP, fp32 MLP, CNN and int8-weight Transformer workloads (device-resident and end to end
 through kernix_capi_forward), each beside the reference's CPU path (oracle/cpu_forward.py: the plain-C kernels of
 the oracle) timed on this machine's host cores on a sample of the same batch; and the CPU oracle's int8 GEMM.
+Each of these lines is timed after 100 ms of untimed launches of its own (the clock ramps up over the first tens of
+milliseconds of work after an idle spell); profiling runs (--no-sustained) skip that warm-up.
 One JSON line is printed on stdout.
 """
 import argparse
@@ -34,6 +36,7 @@ sys.path.insert(0, ROOT)
 PEAK_I8_TOPS = 5000.0      # MI355X dense int8 MFMA
 PEAK_F32_TFLOPS = 157.3    # MI355X fp32 MFMA
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+WARM_MS = 100.0            # untimed launches before each line beside the headline (clock ramp)
 METRIC = "int8 GEMM TOPS + .knx forward samples/sec on 1 MI355X, % of roofline"
 
 
@@ -41,15 +44,23 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def time_launches(fn, steps, warmup):
+def time_launches(fn, steps, warmup, warm_ms=0.0):
     """(ms per launch, wall ms per launch): `steps` launches back to back between two HIP events on torch's current
     stream, which is the stream the launches go to.  An event pair around every single launch would add a
-    system-scope cache flush per launch (≈10 µs for a 64 MB output) that a kernel-trace profile does not see."""
+    system-scope cache flush per launch (≈10 µs for a 64 MB output) that a kernel-trace profile does not see.
+    warm_ms > 0: after the `warmup` launches, more untimed launches until that much time has passed (the GPU's clock
+    ramps up over the first tens of milliseconds of work after an idle spell: the CNN forward's convolutions ran 12%
+    slower in its first 45 forwards than in the next)."""
     import torch
 
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < warm_ms:
+        for _ in range(8):
+            fn()
+        torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     start.record()
@@ -87,7 +98,7 @@ def time_sustained(fn, steps, warm_ms=200.0, windows=20, per_window=50):
     return ms, statistics.median(per), per[len(per) // 10], per[(9 * len(per)) // 10]
 
 
-def i8gemm_bench(M, steps, warmup, N=4096, K=4096, sustained=True, rotate_bytes=0):
+def i8gemm_bench(M, steps, warmup, N=4096, K=4096, sustained=True, rotate_bytes=0, warm_ms=0.0):
     """The int8 GEMM at M×N×K.  rotate_bytes > 0: launches cycle over copies of A and W (and of the output) that
     together exceed rotate_bytes, so no launch finds its operands in the 256 MB last-level cache."""
     import numpy as np
@@ -115,7 +126,7 @@ def i8gemm_bench(M, steps, warmup, N=4096, K=4096, sustained=True, rotate_bytes=
         hipabi.check(L.knx_hip_i8gemm(*args[turn[0]]))
         turn[0] = (turn[0] + 1) % len(args)
 
-    ms, wall = time_launches(run, steps, warmup)
+    ms, wall = time_launches(run, steps, warmup, warm_ms)
     sus = time_sustained(run, steps) if sustained else (ms, ms, ms, ms)
     ops, algo_bytes = configs.i8gemm_work(M, N, K)
     return dict(M=M, N=N, K=K, ms=sus[0], ms_median=sus[1], ms_p10=sus[2], ms_p90=sus[3], burst_ms=ms, wall_ms=wall,
@@ -153,7 +164,7 @@ def cpu_baseline(g, threads, target_s=10.0):
 ROTATE_BYTES = 320 << 20  # more than the 256 MB last-level cache: a rotating working set comes from HBM
 
 
-def rows_bench(steps, warmup):
+def rows_bench(steps, warmup, warm_ms=0.0):
     """The bandwidth-bound kernels at the Transformer / CNN workload shapes: algorithmic bytes (every fp32 input read
     once, every output written once) per launch ÷ time, against HBM peak.  Two figures each: `cached`, the same
     buffers every launch (16-134 MB working sets stay in the 256 MB last-level cache, so this can exceed what HBM
@@ -182,7 +193,7 @@ def rows_bench(steps, warmup):
                 if mode == "hbm":
                     turn[0] = (turn[0] + 1) % copies
 
-            ms, _ = time_launches(one, steps, warmup)
+            ms, _ = time_launches(one, steps, warmup, warm_ms)
             gbs = nbytes / (ms * 1e-3) / 1e9
             res[mode] = dict(us=round(ms * 1e3, 2), gbs=round(gbs, 1), hbm_frac=round(gbs / PEAK_HBM_GBS, 4))
         res["rotating_copies"] = copies
@@ -212,7 +223,7 @@ def rows_bench(steps, warmup):
     return out
 
 
-def conv_bench(steps, warmup):
+def conv_bench(steps, warmup, warm_ms=0.0):
     """The four convolutions of the CNN configuration (batch 256, NHWC, 3×3, pad 1, bias + ReLU fused) through
     knx_hip_conv_t: algorithmic flops 2·B·Ho·Wo·Co·9·Cin per launch against the fp32 MFMA peak, and the minimum HBM
     bytes (input + weights + output once)."""
@@ -233,7 +244,7 @@ def conv_bench(steps, warmup):
         b = torch.randn(cout, device="cuda") * 0.01
         y = torch.empty(256, ho, ho, cout, device="cuda")
         ms, _ = time_launches(lambda: hipabi.check(L.knx_hip_conv_t(ctypes.byref(g), P(x), P(wt), P(b), 0, 0.0, P(y), S)),
-                              steps, warmup)
+                              steps, warmup, warm_ms)
         flops = 2.0 * 256 * ho * ho * cout * 9 * cin
         nbytes = 4 * (x.numel() + wt.numel() + cout + y.numel())
         tf = flops / (ms * 1e-3) / 1e12
@@ -243,7 +254,7 @@ def conv_bench(steps, warmup):
     return out
 
 
-def attention_bench(steps, warmup):
+def attention_bench(steps, warmup, warm_ms=0.0):
     """The attention core of the Transformer configuration (batch 64, 8 heads, 128 queries and keys, dk = dv = 64):
     algorithmic flops 2·B·H·Rq·S·(dk + dv) per launch against the fp32 MFMA peak, and the minimum HBM bytes (Q, K,
     V read once, the context written once), for the fused kernel and for the three-launch path it replaces."""
@@ -268,7 +279,7 @@ def attention_bench(steps, warmup):
         try:
             ms, _ = time_launches(lambda: hipabi.check(L.knx_hip_attention_core_ex(
                 P(q), H * d, P(k), H * d, P(v), H * d, P(vt), P(ctx), P(sc), B, H, T, T, d, d, 0.125, 0, S)), steps,
-                warmup)
+                warmup, warm_ms)
         finally:
             os.environ.pop("KNX_ATTN_KERNEL", None)
         tf = flops / (ms * 1e-3) / 1e12
@@ -329,7 +340,7 @@ def cpu_forward_baseline(path, xr, seq_len, threads, target_s):
                 sample=f"first {n} of the {B} samples, one forward")
 
 
-def forward_bench(name, make, flops, steps, warmup, mode="ref", i8_ops=0.0, cpu=None):
+def forward_bench(name, make, flops, steps, warmup, mode="ref", i8_ops=0.0, cpu=None, warm_ms=0.0):
     """`flops` of one forward, `i8_ops` of them on the int8 MFMA (`i8` mode): the roofline time is the fp32 part at
     the fp32 MFMA peak plus the int8 part at the int8 peak, and roofline_frac that time over the measured one.
     cpu: None, or (list of thread counts, seconds per measurement) for the CPU baseline of the same workload."""
@@ -360,7 +371,7 @@ def forward_bench(name, make, flops, steps, warmup, mode="ref", i8_ops=0.0, cpu=
             m.forward_device(dx.data_ptr(), xr.shape[0], dy.data_ptr(), st)
 
         with torch.cuda.stream(stream):
-            ms, _ = time_launches(run, steps, warmup)
+            ms, _ = time_launches(run, steps, warmup, warm_ms)
         m(x)  # end to end through kernix_capi_forward (host buffers, PCIe included)
         t0 = time.perf_counter()
         n_e2e = max(2, steps // 4)
@@ -392,11 +403,13 @@ def run_parts(args, out, want, configs):
     few = args.no_sustained
     n_small = (args.steps, args.warmup) if few else (max(args.steps, 50), max(args.warmup, 20))
     n_layer = (args.steps, args.warmup) if few else (max(args.steps, 20), max(args.warmup, 3))
+    warm_ms = 0.0 if few else WARM_MS
     small = {}
     for M in (() if args.no_small or not want("gemm_small") else (1, 16, 256)):
         entry = {}
         for mode, rot in (("cached", 0), ("hbm", ROTATE_BYTES)):
-            r = i8gemm_bench(M, n_small[0], n_small[1], sustained=False, rotate_bytes=rot)
+            r = i8gemm_bench(M, n_small[0], n_small[1], sustained=False, rotate_bytes=rot,
+                             warm_ms=warm_ms)
             entry[mode] = dict(us=round(r["burst_ms"] * 1e3, 2), tops=round(r["burst_tops"], 2),
                                gbs=round(r["algo_bytes"] / (r["burst_ms"] * 1e-3) / 1e9, 1),
                                hbm_frac=round(r["algo_bytes"] / (r["burst_ms"] * 1e-3) / 1e9 / PEAK_HBM_GBS, 4))
@@ -415,36 +428,37 @@ def run_parts(args, out, want, configs):
     if small:
         out["i8gemm_small_m"] = small
     if not args.no_small and want("rows"):
-        out["row_kernels"] = rows_bench(*n_small)
+        out["row_kernels"] = rows_bench(*n_small, warm_ms)
     if not args.no_small and want("conv"):
-        out["conv_layers"] = conv_bench(*n_layer)
+        out["conv_layers"] = conv_bench(*n_layer, warm_ms)
     if not args.no_small and want("attention"):
-        out["attention_core"] = attention_bench(*n_layer)
+        out["attention_core"] = attention_bench(*n_layer, warm_ms)
     if not args.no_forward and want("forward"):
         fw = {}
         st = max(10, args.steps)
         fwarm = max(3, args.warmup)
         cpu = None if args.no_cpu else (threads, 2.0)
         mlp = (784, 512, 256, 10)
+        kw = dict(cpu=cpu, warm_ms=warm_ms)
         lines = {
             "int8_mlp_784_512_256_10_b64": lambda: forward_bench(
-                "mlp", lambda p: configs.int8_mlp(p, batch=64), configs.mlp_flops(64, mlp), st, fwarm, cpu=cpu),
+                "mlp", lambda p: configs.int8_mlp(p, batch=64), configs.mlp_flops(64, mlp), st, fwarm, **kw),
             # batch 1: the reference's int8 latency path (int8 arithmetic at ≤ 2 rows), quantize fused into the GEMM
             "int8_mlp_784_512_256_10_b1": lambda: forward_bench(
                 "mlp", lambda p: configs.int8_mlp(p, batch=1), configs.mlp_flops(1, mlp), st, fwarm,
-                i8_ops=configs.mlp_flops(1, mlp), cpu=cpu),
+                i8_ops=configs.mlp_flops(1, mlp), **kw),
             "int8_mlp_784_512_256_10_b64_i8": lambda: forward_bench(
                 "mlp", lambda p: configs.int8_mlp(p, batch=64), configs.mlp_flops(64, mlp), st, fwarm, mode="i8",
-                i8_ops=configs.mlp_flops(64, mlp), cpu=cpu),
+                i8_ops=configs.mlp_flops(64, mlp), **kw),
             "fp32_mlp_4096_4096_4096_1000_b8192": lambda: forward_bench(
                 "f32", lambda p: configs.fp32_mlp(p), configs.mlp_flops(8192, (4096, 4096, 4096, 1000)), st, fwarm,
-                cpu=cpu),
-            "cnn_b256": lambda: forward_bench("cnn", lambda p: configs.cnn(p), configs.cnn_flops(), st, fwarm, cpu=cpu),
+                **kw),
+            "cnn_b256": lambda: forward_bench("cnn", lambda p: configs.cnn(p), configs.cnn_flops(), st, fwarm, **kw),
             "transformer_4l_d512_b64": lambda: forward_bench(
-                "tr", lambda p: configs.transformer(p), configs.transformer_flops(), st, fwarm, cpu=cpu),
+                "tr", lambda p: configs.transformer(p), configs.transformer_flops(), st, fwarm, **kw),
             "transformer_4l_d512_b64_i8": lambda: forward_bench(
                 "tr", lambda p: configs.transformer(p), configs.transformer_flops(), st, fwarm, mode="i8",
-                i8_ops=configs.transformer_ffn_flops(), cpu=cpu),
+                i8_ops=configs.transformer_ffn_flops(), **kw),
         }
         only = {k for k in args.forward_only.split(",") if k}
         for k, run in lines.items():
