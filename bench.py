@@ -19,7 +19,8 @@ samples/sec of the int8 MLP, fp32 MLP, CNN and int8-weight Transformer workloads
 through kernix_capi_forward), each beside the reference's CPU path (oracle/cpu_forward.py: the plain-C kernels of
 the oracle) timed on this machine's host cores on a sample of the same batch; and the CPU oracle's int8 GEMM.
 Each of these lines is timed after 100 ms of untimed launches of its own (the clock ramps up over the first tens of
-milliseconds of work after an idle spell); profiling runs (--no-sustained) skip that warm-up.
+milliseconds of work after an idle spell; --warm-ms sets it, and profiling runs with --no-sustained skip it unless
+--warm-ms is given).  A forward line's `forwards` counts the device and host-buffer forwards the run made.
 One JSON line is printed on stdout.
 """
 import argparse
@@ -367,8 +368,11 @@ def forward_bench(name, make, flops, steps, warmup, mode="ref", i8_ops=0.0, cpu=
         stream = torch.cuda.Stream()
         st = stream.cuda_stream
 
+        n_dev = [0]
+
         def run():
             m.forward_device(dx.data_ptr(), xr.shape[0], dy.data_ptr(), st)
+            n_dev[0] += 1
 
         with torch.cuda.stream(stream):
             ms, _ = time_launches(run, steps, warmup, warm_ms)
@@ -389,7 +393,8 @@ def forward_bench(name, make, flops, steps, warmup, mode="ref", i8_ops=0.0, cpu=
     ideal_ms = ((flops - i8_ops) / (PEAK_F32_TFLOPS * 1e12) + i8_ops / (PEAK_I8_TOPS * 1e12)) * 1e3
     res = dict(batch=B, ms=round(ms, 4), samples_per_s=round(B / (ms * 1e-3), 1),
                e2e_ms=round(e2e, 3), e2e_samples_per_s=round(B / (e2e * 1e-3), 1),
-               tflops=round(tf, 2), roofline_frac=round(ideal_ms / ms, 4), mode=mode)
+               tflops=round(tf, 2), roofline_frac=round(ideal_ms / ms, 4), mode=mode,
+               forwards={"device": n_dev[0], "host": 1 + n_e2e})
     if base:
         res["cpu_baseline"] = base
     return res
@@ -403,7 +408,7 @@ def run_parts(args, out, want, configs):
     few = args.no_sustained
     n_small = (args.steps, args.warmup) if few else (max(args.steps, 50), max(args.warmup, 20))
     n_layer = (args.steps, args.warmup) if few else (max(args.steps, 20), max(args.warmup, 3))
-    warm_ms = 0.0 if few else WARM_MS
+    warm_ms = args.warm_ms if args.warm_ms is not None else 0.0 if few else WARM_MS
     small = {}
     for M in (() if args.no_small or not want("gemm_small") else (1, 16, 256)):
         entry = {}
@@ -493,6 +498,9 @@ def main():
                     help="comma-separated subset of the .knx forward lines (their keys, e.g. cnn_b256), for profiling runs")
     ap.add_argument("--no-sustained", action="store_true",
                     help="time the headline GEMM only in the burst form (profiling runs with few launches)")
+    ap.add_argument("--warm-ms", type=float, default=None,
+                    help="untimed launches (ms) before each line beside the headline; default 100, 0 with "
+                         "--no-sustained")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run a 256 MiB read (sum) and a 256 MiB copy: reference kernels of known HBM traffic for "
                          "scaling the FETCH_SIZE / WRITE_SIZE counters")
