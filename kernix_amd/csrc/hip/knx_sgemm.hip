@@ -686,12 +686,13 @@ int dispatch_nt(SgArgs p, int batch, hipStream_t s, const char* name)
     const long cus = knx::num_cus();
     const long t256 = (long)((p.M + 255) / 256) * ((p.N + 255) / 256) * batch;
     const long t128 = (long)((p.M + 127) / 128) * ((p.N + 127) / 128) * batch;
-    // KNX_SGEMM_KERNEL forces the general kernel ("general"), one pipelined tile ("t256", "t128", "t64") or the
+    // KNX_SGEMM_KERNEL forces the general kernel ("general"), one pipelined tile ("t256", "t128", "t128w8", "t64") or the
     // small-GEMM kernel ("skinny") where the shape allows it, else the general kernel (tests, tuning)
     const char* force = getenv("KNX_SGEMM_KERNEL");
     if (force != nullptr && *force) {
         if (strcmp(force, "t256") == 0 && k32_ok(p, 256, 256)) return launch_k32<256, 256, 4, 2>(p, batch, s, name);
         if (strcmp(force, "t128") == 0 && k32_ok(p, 128, 128)) return launch_k32<128, 128, 2, 2>(p, batch, s, name);
+        if (strcmp(force, "t128w8") == 0 && k32_ok(p, 128, 128)) return launch_k32<128, 128, 4, 2>(p, batch, s, name);
         if (strcmp(force, "t64") == 0 && k32_ok(p, 128, 64)) return launch_k32<128, 64, 4, 1>(p, batch, s, name);
 #ifdef KNX_TUNING
         // variants no shape selects (measured slower where they fit), built only for tuning (-DKNX_TUNING)
@@ -709,6 +710,11 @@ int dispatch_nt(SgArgs p, int batch, hipStream_t s, const char* name)
     const long t64x64 = (long)((p.M + 63) / 64) * ((p.N + 63) / 64) * batch;
     if (t64x64 * 4 < cus && skinny_ok(p, batch)) return launch_skinny(p, s, name);
     const long t64 = (long)((p.M + 127) / 128) * ((p.N + 63) / 64) * batch;
+    // short K with 128×128 tiles enough for three or more workgroups per CU: those tiles on 8 waves of 32×64 (one box,
+    // same process: 8192×2048×512 + GELU 138.7 µs against 142.5 on the 128×64 tiles below, 8192×4096×1024 492.4
+    // against 499.4, 4096×4096×512 131.7 against 133.9, 8192×3072×768 282.8 against 287.7, 8192×1536×512 100.0
+    // against 100.3; the same bits: every tile of this kernel sums each output in the same order)
+    if (p.K <= 2048 && t128 >= 3 * cus && k32_ok(p, 128, 128)) return launch_k32<128, 128, 4, 2>(p, batch, s, name);
     // short K: 128×64 tiles, at least two per CU, so that several workgroups share a CU and one's prologue and
     // epilogue overlap another's multiplies (Transformer layers at 8192 rows, one box after a 2 s warm-up:
     // 8192×1536×512 105 µs against 113 for 128×128, 8192×512×512 41 against 47, 8192×2048×512 + GELU 145 against
