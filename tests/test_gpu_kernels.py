@@ -531,6 +531,13 @@ CONV_TILE_CASES = [(64, 32, 32, 64, 64, 3, 1, 1, 1, 1), (128, 16, 16, 64, 128, 3
                    (2, 12, 12, 32, 64, 9, 1, 4, 1, 1)]
 
 
+@pytest.mark.parametrize("tile", ["128x128w8", "64x128", "128x64", "256x128"])
+def test_conv_residual_tiles(L, tile, monkeypatch):
+    """the residual epilogue on the 8-wave tiles (and one 4-wave tile), pixels not a multiple of the tile"""
+    monkeypatch.setenv("KNX_CONV_TILE", tile)
+    test_conv_residual(L, (17, 15, 15, 64, 128, 3, 1, 1, 1, 1))
+
+
 @pytest.mark.parametrize("tile", CONV_TILES)
 @pytest.mark.parametrize("case", CONV_TILE_CASES)
 def test_conv_tiles(L, case, tile, monkeypatch):
