@@ -73,7 +73,6 @@ typedef struct kernix_qweight {
     int kp, np;
     int8_t* q;
     float* scale;
-    struct knx_qdev* dev;      /* device copy made by the first kernix_qmatmul, released by kernix_qweight_free */
 } kernix_qweight;
 
 /* One graph value (edge). Stored as (batch·r) × c. */
@@ -184,6 +183,10 @@ KERNIX_API int kernix_model_set_int8_mode(kernix_model* m, int mode);
  * both device pointers; stream is a hipStream_t (NULL = the model's own stream). Work is stream-ordered; the call
  * returns after enqueueing (it synchronizes only when it has to allocate). 0 or -1. */
 KERNIX_API int kernix_model_forward_device(kernix_model* m, const float* d_x, int rows, float* d_out, void* stream);
+/* Waits for the model's last forward and reports the device forwards since the previous call: -1 if one of them ran a
+ * Linear chain whose workgroups could not all be resident (more chains running at once than the GPU holds), so its
+ * outputs are wrong and it must be run again; else 0.  Host-buffer forwards recompute such a forward themselves. */
+KERNIX_API int kernix_model_device_status(kernix_model* m);
 
 KERNIX_API kernix_qweight* kernix_qweight_pack(const int8_t* q, const float* scale, int k, int n);
 KERNIX_API void kernix_qweight_unpack(const kernix_qweight* w, float* dst);

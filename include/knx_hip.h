@@ -136,11 +136,14 @@ KNX_API int knx_hip_qlinear_noalloc(const float* x, int ldx, int rows, int k, in
  * and computes the epilogue of knx_hip_i8gemm, the same bits as knx_hip_qlinear; an fp32 layer (w: n rows of k
  * floats, stride ldw) sums in its own order.  1 ≤ rows ≤ 64, at most KNX_CHAIN_MAX_LAYERS layers, every k a multiple
  * of 4, x and every y but the last 16-byte aligned with strides multiple of 4 floats; a layer's output must not
- * overlap its input.  The layers are separated by barriers across the launch's workgroups (at most one per CU, all
- * resident at once).  scratch (knx_hip_linear_chain_scratch bytes, 256-byte aligned) holds the barrier words: zero
- * before the first call (each call leaves them ready for the next); calls that share a scratch must not overlap.  A barrier that
- * waits ≈ 1 s without the other workgroups arriving (they could not be resident) stops waiting and raises a flag
- * that knx_hip_chain_status reports (the outputs are then wrong). */
+ * overlap its input.  The layers are separated by barriers across the launch's workgroups (at most 64, one per CU,
+ * all resident at once; more items than workgroups are taken in turn).  scratch (knx_hip_linear_chain_scratch bytes,
+ * 256-byte aligned) holds the barrier words: zero before the first call (each call leaves them ready for the next);
+ * calls that share a scratch must not overlap.  status is the caller's host-visible int (pinned host memory,
+ * knx_hip_host_malloc): a barrier that waits ≈ 1 s without the other workgroups arriving (they could not all be
+ * resident, e.g. more chains than the GPU holds running at once) stops waiting and sets it to 1 — the outputs of
+ * that launch are then wrong and must be recomputed.  The kernel never clears it: the caller reads it after
+ * synchronizing and clears it. */
 #define KNX_CHAIN_MAX_LAYERS 8
 typedef struct {
     const void* w;
@@ -154,10 +157,7 @@ typedef struct {
 } knx_chain_layer;
 KNX_API size_t knx_hip_linear_chain_scratch(const knx_chain_layer* layers, int n_layers, int rows); /* 0: bad shape */
 KNX_API int knx_hip_linear_chain(const float* x, int ldx, int rows, const knx_chain_layer* layers, int n_layers,
-                                 void* scratch, size_t scratch_bytes, void* stream);
-/* 1 if a launch with a grid barrier (knx_hip_linear_chain) stopped waiting since the previous call (read after
- * synchronizing), else 0 */
-KNX_API int knx_hip_chain_status(void);
+                                 void* scratch, size_t scratch_bytes, int* status, void* stream);
 /* Fills bytes of device memory with a byte value, ordered on stream. */
 KNX_API int knx_hip_memset(void* p, int value, size_t bytes, void* stream);
 

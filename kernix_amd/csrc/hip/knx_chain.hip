@@ -314,6 +314,7 @@ bool overlaps(const void* a, size_t na, const void* b, size_t nb)
 }
 
 constexpr size_t kScratchBytes = 256;  // the barrier words (one 64-bit word per barrier, layers − 1 of them)
+constexpr int kMaxGrid = 64;           // workgroups of a chain launch at most
 
 }  // namespace
 
@@ -324,7 +325,7 @@ extern "C" size_t knx_hip_linear_chain_scratch(const knx_chain_layer* layers, in
 }
 
 extern "C" int knx_hip_linear_chain(const float* x, int ldx, int rows, const knx_chain_layer* layers, int n_layers,
-                                    void* scratch, size_t scratch_bytes, void* stream)
+                                    void* scratch, size_t scratch_bytes, int* status, void* stream)
 {
     const char* name = "knx_hip_linear_chain";
     KNX_ENTRY(name);
@@ -352,8 +353,7 @@ extern "C" int knx_hip_linear_chain(const float* x, int ldx, int rows, const knx
         KNX_REQUIRE(!overlaps(in, (size_t)rows * ldin * 4, L.y, (size_t)rows * L.ldy * 4), name);
     }
     KNX_REQUIRE(scratch != nullptr && ((uintptr_t)scratch & 255) == 0 && scratch_bytes >= kScratchBytes, name);
-    int* err = knx::grid_error_word();
-    if (err == nullptr) return knx::fail(KNX_EHIP, "%s: cannot allocate the error word", name);
+    KNX_REQUIRE(status != nullptr && ((uintptr_t)status & 3) == 0, name);
 
     // measured on the int8 MLP 784-512-256-10: 16 items at one row (14.3 µs against 15.2 at 32), 32 at 64 rows
     // (16.8 µs against 19.1 at 16: with 16 workgroups each loads 156 KB of rows and weights in the first layer)
@@ -362,7 +362,7 @@ extern "C" int knx_hip_linear_chain(const float* x, int ldx, int rows, const knx
     ChainArgs a{};
     a.layers = n_layers;
     a.rows = rows;
-    a.gs = knx::GridSync{static_cast<unsigned long long*>(scratch), err};
+    a.gs = knx::GridSync{static_cast<unsigned long long*>(scratch), status, knx::grid_spin_limit()};
     for (int l = 0; l < n_layers; ++l) {
         const knx_chain_layer& L = layers[l];
         LayerDev& d = a.L[l];
@@ -392,10 +392,10 @@ extern "C" int knx_hip_linear_chain(const float* x, int ldx, int rows, const knx
         d.cb = 1;
         while (d.cb < max_blocks(d) && items_of(d, d.cb) > items_max) d.cb *= 2;
     }
-    // one workgroup per item of the widest layer, at most one per CU (all resident at once) and at most the
-    // barrier's quantum
-    int G = items_max < knx::num_cus() ? items_max : knx::num_cus();
-    G = G < (int)KNX_GRID_QUANTUM ? G : (int)KNX_GRID_QUANTUM;
+    // one workgroup per item of the widest layer, at most kMaxGrid (a quarter of the CUs: four chains launched at the
+    // same time from different threads or processes still find all of their workgroups resident; above it the
+    // workgroups take several items each, and a barrier at 64 workgroups costs 1.9 µs against 3.1 at 128)
+    int G = std::min(std::min(items_max, kMaxGrid), knx::num_cus());
     if (const char* e = getenv("KNX_CHAIN_WG")) {  // tuning and tests: fewer workgroups (each then takes several items)
         const int g = atoi(e);
         if (g >= 1 && g < G) G = g;

@@ -18,8 +18,8 @@ bool injected(const char* name);
 int check_launch(const char* what);
 // Number of compute units of the current device (cached).
 int num_cus();
-// Pinned host word that a grid barrier (knx_grid.hpp) raises when it stops waiting; null if it cannot be allocated.
-int* grid_error_word();
+// Polls of a grid barrier (knx_grid.hpp) before it stops waiting: KNX_GRID_SPIN_LIMIT, or KNX_GRID_SPIN (tests).
+unsigned grid_spin_limit();
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 

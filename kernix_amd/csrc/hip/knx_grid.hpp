@@ -13,8 +13,12 @@
 // own atomic add returns the word before it, so the word's value at the end of this barrier is the next multiple
 // of 256, and the workgroup waits (polling) until the word reaches it.  Words are never reset and never need to be:
 // launches on one scratch are ordered by their stream, and 2^64 / 256 launches do not wrap.  The wait is bounded:
-// after KNX_GRID_SPIN_LIMIT polls (about a second) the workgroup stops waiting and raises the error word, so every
-// wave of the grid still reaches the end of the kernel.
+// after `spin` polls (KNX_GRID_SPIN_LIMIT by default, about a second) the workgroup stops waiting and sets the
+// caller's status word, so every wave of the grid still reaches the end of the kernel.  The status word belongs to
+// the launch's caller (one per model), is host-visible (pinned host memory) and is only ever set, never cleared, by
+// the kernel; the caller reads and clears it after synchronizing.  A launch that gave up computed with incomplete
+// inputs: its outputs are wrong and must be recomputed.  Every launch still adds exactly 256 to each barrier word
+// (every workgroup arrives once at every barrier, waiting or not), so the scratch stays ready for the next launch.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -26,7 +30,8 @@ namespace knx {
 
 struct GridSync {
     unsigned long long* words;  // one per barrier
-    int* err;                   // raised (set to 1) by a workgroup that stopped waiting; host-visible memory, or null
+    int* err;                   // set to 1 by a workgroup that stopped waiting; the caller's host-visible word
+    unsigned spin;              // polls before a workgroup stops waiting
 };
 
 __device__ __forceinline__ void grid_barrier(const GridSync& gs, unsigned b)
@@ -39,12 +44,14 @@ __device__ __forceinline__ void grid_barrier(const GridSync& gs, unsigned b)
         const unsigned long long old = __hip_atomic_fetch_add(w, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const unsigned long long target = (old / KNX_GRID_QUANTUM + 1) * KNX_GRID_QUANTUM;
         if (old + add < target) {
-            // one poll at a time: polls in flight from every workgroup contend with the arrivals on the word
-            for (unsigned polls = 0; __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target; ++polls) {
-                if (polls > KNX_GRID_SPIN_LIMIT) {
-                    if (gs.err) __hip_atomic_store(gs.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            // one poll at a time: polls in flight from every workgroup contend with the arrivals on the word.  With
+            // a limit of 0 every workgroup but the last to arrive stops without polling.
+            for (unsigned polls = 0;; ++polls) {
+                if (polls >= gs.spin) {
+                    __hip_atomic_store(gs.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
                     break;
                 }
+                if (__hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= target) break;
                 __builtin_amdgcn_s_sleep(1);
             }
         }

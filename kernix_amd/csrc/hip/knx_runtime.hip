@@ -7,6 +7,7 @@
 #include <mutex>
 
 #include "knx_common.hpp"
+#include "knx_grid.hpp"
 
 namespace knx {
 
@@ -57,29 +58,18 @@ int num_cus()
     return g_cus;
 }
 
-static int* g_grid_err = nullptr;  // pinned host word raised by a grid barrier that stopped waiting
-static std::mutex g_grid_err_mu;
-
-int* grid_error_word()
+unsigned grid_spin_limit()
 {
-    std::lock_guard<std::mutex> lk(g_grid_err_mu);
-    if (g_grid_err == nullptr) {
-        void* p = nullptr;
-        if (hipHostMalloc(&p, sizeof(int), hipHostMallocDefault) != hipSuccess) return nullptr;
-        g_grid_err = static_cast<int*>(p);
-        *g_grid_err = 0;
+    // KNX_GRID_SPIN: tests force a barrier to give up (0 = stop waiting at the first poll); every wave still ends
+    const char* e = getenv("KNX_GRID_SPIN");
+    if (e != nullptr && *e != '\0') {
+        const long v = strtol(e, nullptr, 10);
+        if (v >= 0 && v <= (long)KNX_GRID_SPIN_LIMIT) return (unsigned)v;
     }
-    return g_grid_err;
+    return KNX_GRID_SPIN_LIMIT;
 }
 
 }  // namespace knx
-
-extern "C" int knx_hip_chain_status(void)
-{
-    std::lock_guard<std::mutex> lk(knx::g_grid_err_mu);
-    if (knx::g_grid_err == nullptr) return 0;
-    return __atomic_exchange_n(knx::g_grid_err, 0, __ATOMIC_SEQ_CST) != 0;
-}
 
 static std::once_flag g_init_once;
 static int g_init_rc = KNX_ENODEV;

@@ -80,6 +80,8 @@ KERNIX_API int kernix_capi_forward_device(kernix_model* m, const float* d_x, int
     return kernix_model_forward_device(m, d_x, rows, d_out, stream);
 }
 
+KERNIX_API int kernix_capi_device_status(kernix_model* m) { return kernix_model_device_status(m); }
+
 /* Workspace accounting, for tests of the chunking rules: floats per sample, batch-independent floats, current batch. */
 KERNIX_API void kernix_capi_ws_info(const kernix_model* m, size_t* per_sample, size_t* fixed, int* batch)
 {

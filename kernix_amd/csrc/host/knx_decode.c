@@ -89,7 +89,6 @@ void kernix_qweight_unpack(const kernix_qweight* w, float* dst)
 void kernix_qweight_free(kernix_qweight* w)
 {
     if (w == NULL) return;
-    knx_qweight_release_device(w);
     free(w->q);
     free(w->scale);
     free(w);

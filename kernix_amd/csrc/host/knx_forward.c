@@ -184,8 +184,10 @@ static int ensure_device(kernix_model* m)
         m->dev = calloc(1, sizeof *m->dev);
         if (m->dev == NULL) return -1;
         if (hip_ok(knx_hip_stream_create(&m->dev->stream), "stream creation") != 0 ||
-            hip_ok(knx_hip_event_create_ordering(&m->dev->done), "event creation") != 0)
+            hip_ok(knx_hip_event_create_ordering(&m->dev->done), "event creation") != 0 ||
+            hip_ok(knx_hip_host_malloc((void**)&m->dev->chain_status, sizeof(int)), "status word allocation") != 0)
             return -1;
+        *m->dev->chain_status = 0;
     }
     for (int i = 0; i < m->n_steps; i++) {
         if (m->steps[i].dev != NULL) continue;
@@ -418,6 +420,7 @@ void knx_model_release_device_all(kernix_model* m)
             knx_hip_event_destroy(m->dev->ring_ev[k]);
             knx_hip_host_free(m->dev->ring[k]);
         }
+        knx_hip_host_free(m->dev->chain_status);
         free(m->dev);
         m->dev = NULL;
     }
@@ -879,13 +882,14 @@ static int run_chunk(kernix_model* m, const float* in, int B, float* out, void* 
     }
     if (out != NULL) m->views[m->out_v].tensor = out;
     if (B == 0) return 0;
-    const int fuse = fuse_enabled(), chains = chain_enabled();
+    const int fuse = fuse_enabled(), chains = chain_enabled() && !m->dev->no_chain;
     knx_chain_layer cl[KNX_CHAIN_MAX_LAYERS];
     for (int i = 0; i < m->n_steps; i++) {
         const int nc = chains ? chain_len(m, i, fuse, cl) : 0;
         if (nc >= 2) {
             const float_tensor* x = &m->views[m->steps[i].inp[0]];
-            if (hip_ok(knx_hip_linear_chain(x->tensor, x->col, x->row, cl, nc, m->dev->chain, m->dev->chain_bytes, st),
+            if (hip_ok(knx_hip_linear_chain(x->tensor, x->col, x->row, cl, nc, m->dev->chain, m->dev->chain_bytes,
+                                            m->dev->chain_status, st),
                        "Linear chain"))
                 return -1;
             i += nc - 1;
@@ -1201,7 +1205,7 @@ static int forward_overlapped(kernix_model* m, const float* x, int samples, int 
     return 0;
 }
 
-const float_tensor* kernix_model_forward(kernix_model* m, const float_tensor* x)
+static const float_tensor* forward_host(kernix_model* m, const float_tensor* x)
 {
     if (m == NULL || x == NULL || x->tensor == NULL || x->row < 0 || x->col != m->in_dim || x->row % m->seq_len != 0)
         return NULL;
@@ -1233,13 +1237,23 @@ const float_tensor* kernix_model_forward(kernix_model* m, const float_tensor* x)
         }
     }
     if (mark_done(m, st) != 0 || hip_ok(knx_hip_stream_sync(st), "forward")) return NULL;
-    if (knx_hip_chain_status()) {
-        KNX_LOG("KERNIX: a Linear chain's workgroups were not all resident (barrier wait abandoned)\n");
-        return NULL;
-    }
     if (chunked) return m->out_all;
     m->out_view = (float_tensor){ samples, m->out_dim, out };
     return &m->out_view;
+}
+
+/* A chain launch whose workgroups could not all be resident (its barrier stopped waiting, so its outputs are wrong)
+ * is recomputed in the same call: the whole forward again, every Linear its own launch. */
+const float_tensor* kernix_model_forward(kernix_model* m, const float_tensor* x)
+{
+    const float_tensor* y = forward_host(m, x);
+    if (y == NULL || !__atomic_exchange_n(m->dev->chain_status, 0, __ATOMIC_SEQ_CST)) return y;
+    KNX_LOG("KERNIX: a Linear chain's workgroups were not all resident; forward recomputed one launch per layer\n");
+    m->dev->no_chain = 1;
+    y = forward_host(m, x);
+    m->dev->no_chain = 0;
+    if (y != NULL && __atomic_exchange_n(m->dev->chain_status, 0, __ATOMIC_SEQ_CST)) return NULL; /* cannot happen */
+    return y;
 }
 
 int kernix_model_forward_device(kernix_model* m, const float* d_x, int rows, float* d_out, void* stream)
@@ -1258,16 +1272,24 @@ int kernix_model_forward_device(kernix_model* m, const float* d_x, int rows, flo
     return mark_done(m, st);
 }
 
-/* ---------------------------------------------------------------- kernel-level int8 contract
- * kernix_qmatmul on host pointers.  The packed weight is uploaded once per kernix_qweight (kept in w->dev until
- * kernix_qweight_free); the input, output, bias and int8 scratch live in one growable device buffer shared by all
- * calls (kept until the process ends), used on one stream under a lock, so a call allocates only when it needs more
- * scratch than any call before it. */
-struct knx_qdev {
-    int8_t* q;
-    float* scale;
-};
+/* Waits for the model's last forward; -1 if a Linear chain launch of a device forward since the previous call could
+ * not have all of its workgroups resident (the outputs of that forward are wrong: run it again), else 0. */
+int kernix_model_device_status(kernix_model* m)
+{
+    if (m == NULL || m->dev == NULL || m->dev->chain_status == NULL) return 0;
+    struct knx_dmodel* d = m->dev;
+    if (d->have_last) {
+        const int rc = d->done_recorded ? knx_hip_event_sync(d->done) : knx_hip_stream_sync(d->last_stream);
+        if (hip_ok(rc, "device forward")) return -1;
+    }
+    return __atomic_exchange_n(d->chain_status, 0, __ATOMIC_SEQ_CST) ? -1 : 0;
+}
 
+/* ---------------------------------------------------------------- kernel-level int8 contract
+ * kernix_qmatmul on host pointers.  Like the reference, every call reads the weight (w->q, w->scale) as it is at that
+ * call: the packed weight, the input, output, bias and int8 scratch are copied into one growable device buffer shared
+ * by all calls (kept until the process ends), used on one stream under a lock, so a call allocates only when it needs
+ * more device memory than any call before it.  Nothing is attached to the weight. */
 static struct {
     pthread_mutex_t lock;
     void* stream;
@@ -1275,33 +1297,15 @@ static struct {
     size_t bytes;
 } g_qm = { PTHREAD_MUTEX_INITIALIZER, NULL, NULL, 0 };
 
-void knx_qweight_release_device(kernix_qweight* w)
-{
-    if (w == NULL || w->dev == NULL) return;
-    pthread_mutex_lock(&g_qm.lock);
-    if (g_qm.stream) knx_hip_stream_sync(g_qm.stream); /* a call may still read it */
-    knx_hip_free(w->dev->q);
-    knx_hip_free(w->dev->scale);
-    pthread_mutex_unlock(&g_qm.lock);
-    free(w->dev);
-    w->dev = NULL;
-}
-
 static size_t qm_round(size_t b) { return (b + KNX_ALIGN - 1) / KNX_ALIGN * KNX_ALIGN; }
 
-static int qm_call(const float* x, int rows, kernix_qweight* w, const float* bias, int accumulate, float* y)
+static int qm_call(const float* x, int rows, const kernix_qweight* w, const float* bias, int accumulate, float* y)
 {
-    const size_t k = (size_t)w->k, n = (size_t)w->n, kp = (size_t)w->kp, R = (size_t)rows;
+    const size_t k = (size_t)w->k, n = (size_t)w->n, kp = (size_t)w->kp, np = (size_t)w->np, R = (size_t)rows;
     if (g_qm.stream == NULL && knx_hip_stream_create(&g_qm.stream) != KNX_OK) return -1;
-    if (w->dev == NULL) {
-        struct knx_qdev* d = calloc(1, sizeof *d);
-        if (d == NULL) return -1;
-        w->dev = d;
-        if (up((void**)&d->q, w->q, (size_t)w->np * kp, g_qm.stream) || up_f(&d->scale, w->scale, (size_t)w->np, g_qm.stream))
-            return -1;
-    }
+    const size_t sz_w = qm_round(np * kp), sz_s = qm_round(np * 4);
     const size_t sz_x = qm_round(R * k * 4), sz_y = qm_round(R * n * 4), sz_b = qm_round(n * 4), sz_q = qm_round(R * kp);
-    const size_t need = sz_x + sz_y + sz_b + sz_q + qm_round(R * 4);
+    const size_t need = sz_w + sz_s + sz_x + sz_y + sz_b + sz_q + qm_round(R * 4);
     if (need > g_qm.bytes) {
         knx_hip_stream_sync(g_qm.stream);
         knx_hip_free(g_qm.buf);
@@ -1310,16 +1314,20 @@ static int qm_call(const float* x, int rows, kernix_qweight* w, const float* bia
         if (knx_hip_malloc((void**)&g_qm.buf, need) != KNX_OK) return -1;
         g_qm.bytes = need;
     }
-    float* dx = (float*)g_qm.buf;
-    float* dy = (float*)(g_qm.buf + sz_x);
-    float* db = bias ? (float*)(g_qm.buf + sz_x + sz_y) : NULL;
-    int8_t* dxq = (int8_t*)(g_qm.buf + sz_x + sz_y + sz_b);
-    float* dsx = (float*)(g_qm.buf + sz_x + sz_y + sz_b + sz_q);
+    char* at = g_qm.buf;
+    int8_t* dw = (int8_t*)at;                 at += sz_w;
+    float* dscale = (float*)at;               at += sz_s;
+    float* dx = (float*)at;                   at += sz_x;
+    float* dy = (float*)at;                   at += sz_y;
+    float* db = bias ? (float*)at : NULL;     at += sz_b;
+    int8_t* dxq = (int8_t*)at;                at += sz_q;
+    float* dsx = (float*)at;
     void* st = g_qm.stream;
-    if (knx_hip_memcpy_h2d(dx, x, R * k * 4, st) || (db && knx_hip_memcpy_h2d(db, bias, n * 4, st)) ||
+    if (knx_hip_memcpy_h2d(dw, w->q, np * kp, st) || knx_hip_memcpy_h2d(dscale, w->scale, np * 4, st) ||
+        knx_hip_memcpy_h2d(dx, x, R * k * 4, st) || (db && knx_hip_memcpy_h2d(db, bias, n * 4, st)) ||
         (accumulate && knx_hip_memcpy_h2d(dy, y, R * n * 4, st)))
         return -1;
-    if (knx_hip_qlinear(dx, (int)k, rows, (int)k, (int)kp, dxq, dsx, w->dev->q, (int)kp, (int)n, w->dev->scale, db, -1,
+    if (knx_hip_qlinear(dx, (int)k, rows, (int)k, (int)kp, dxq, dsx, dw, (int)kp, (int)n, dscale, db, -1,
                         0.0f, accumulate, NULL, 0, dy, (int)n, st) != KNX_OK)
         return -1;
     return knx_hip_memcpy_d2h(y, dy, R * n * 4, st) == KNX_OK && knx_hip_stream_sync(st) == KNX_OK ? 0 : -1;
@@ -1334,8 +1342,7 @@ int kernix_qmatmul(const float* x, int rows, const kernix_qweight* w, const floa
         return -1;
     }
     pthread_mutex_lock(&g_qm.lock);
-    /* the device copy is a cache attached to the weight: the weight's values are not changed */
-    const int rc = qm_call(x, rows, (kernix_qweight*)w, bias, accumulate, y);
+    const int rc = qm_call(x, rows, w, bias, accumulate, y);
     pthread_mutex_unlock(&g_qm.lock);
     if (rc != 0) KNX_LOG("KERNIX: kernix_qmatmul failed: %s\n", knx_hip_last_error());
     return rc;

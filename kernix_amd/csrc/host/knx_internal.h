@@ -50,6 +50,8 @@ struct knx_dmodel {
     float* d_in;      /* device copy of the current chunk's input */
     void* chain;      /* scratch of knx_hip_linear_chain (barrier words, zero between launches; partial maxima) */
     size_t chain_bytes;
+    int* chain_status;  /* pinned host word: set by a chain launch of this model whose barrier stopped waiting */
+    int no_chain;       /* a host forward recomputing without chains after such a launch */
     float* h_out;     /* pinned host output of an unchunked forward (batch × out_dim) */
     size_t h_out_floats;
     int out_all_pinned; /* out_all->tensor was allocated pinned */
@@ -88,7 +90,6 @@ int knx_storage_overlaps(const kernix_model* m, int a, int b); /* values a, b sh
 
 /* workspace / device (knx_forward.c) */
 int knx_model_count_ws(kernix_model* m, size_t* per_sample); /* floats per sample of workspace, 0 or -1 */
-void knx_qweight_release_device(kernix_qweight* w);          /* kernix_qmatmul's cached device copy */
 
 /* workspace / device (knx_forward.c) */
 void knx_model_release_device_ws(kernix_model* m);

@@ -26,6 +26,8 @@ class ChainLayer(ctypes.Structure):
 
 SIGS = {
     "knx_hip_init": ([], I),
+    "knx_hip_host_malloc": ([ctypes.POINTER(ctypes.c_void_p), Z], I),
+    "knx_hip_host_free": ([P], I),
     "knx_hip_last_error": ([], ctypes.c_char_p),
     "knx_hip_quantize_rows": ([P, I, I, I, I, P, I, P, P], I),
     "knx_hip_i8gemm": ([I, I, I, P, I, P, P, I, P, P, I, F, I, P, I, P, I, P], I),
@@ -51,8 +53,7 @@ SIGS = {
     "knx_hip_attention_core": ([P, P, P, P, P, I, I, I, I, I, I, F, I, P], I),
     "knx_hip_attention_core_ex": ([P, I, P, I, P, I, P, P, P, I, I, I, I, I, I, F, I, P], I),
     "knx_hip_linear_chain_scratch": ([ctypes.POINTER(ChainLayer), I, I], Z),
-    "knx_hip_linear_chain": ([P, I, I, ctypes.POINTER(ChainLayer), I, P, Z, P], I),
-    "knx_hip_chain_status": ([], I),
+    "knx_hip_linear_chain": ([P, I, I, ctypes.POINTER(ChainLayer), I, P, Z, P, P], I),
     "knx_hip_memset": ([P, I, Z, P], I),
 }
 

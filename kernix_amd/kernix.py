@@ -43,6 +43,7 @@ _ABI = {
     # extensions of this build
     "kernix_capi_set_int8_mode": ((_VOID, _INT), _INT),
     "kernix_capi_forward_device": ((_VOID, _VOID, _INT, _VOID, _VOID), _INT),
+    "kernix_capi_device_status": ((_VOID,), _INT),
     "kernix_capi_ws_info": ((_VOID, _PSIZE, _PSIZE, _PINT), None),
 }
 
@@ -191,6 +192,14 @@ class Model:
         with self._lock:
             if _lib.kernix_capi_forward_device(self._h, x_ptr, int(rows), out_ptr, stream) != 0:
                 raise RuntimeError("KERNIX device forward failed (see stderr)")
+
+    def device_status(self):
+        """Wait for the last forward; True if every device forward since the previous check computed correctly,
+        False if one ran a Linear chain whose workgroups could not all be resident at once (more chains running
+        than the GPU holds): its outputs are wrong and it must be run again.  Host forwards (__call__) recompute such
+        a forward themselves."""
+        with self._lock:
+            return _lib.kernix_capi_device_status(self._h) == 0
 
     def ws_info(self):
         """(workspace floats per sample, batch-independent floats, rows the workspace holds or -1)"""

@@ -30,7 +30,9 @@ def test_every_declared_symbol_is_exported():
 
 
 def test_reference_capi_signatures_bind(tmp_path):
-    """the ten reference exports bind with the reference binding's ctypes table (reference python/kernix.py:21-40)"""
+    """this repository's binding (kernix_amd/kernix.py), whose ctypes table gives the ten reference exports the argument
+    types of the reference binding's table (reference python/kernix.py:21-40), drives the reference's Model API; the
+    reference binding itself is not loaded"""
     from kernix_amd import kernix as kx
 
     p = str(tmp_path / "c.knx")

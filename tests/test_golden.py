@@ -97,6 +97,40 @@ def test_gpu_qmatmul_golden(L):
             L.kernix_qweight_free(w)
 
 
+class _QWeight(ctypes.Structure):
+    _fields_ = [("k", ctypes.c_int), ("n", ctypes.c_int), ("kp", ctypes.c_int), ("np", ctypes.c_int),
+                ("q", ctypes.POINTER(ctypes.c_int8)), ("scale", ctypes.POINTER(ctypes.c_float))]
+
+
+@pytest.mark.gpu
+def test_gpu_qmatmul_reads_the_weight_every_call(L):
+    """a weight whose values change in place between calls gives the new values' results (the reference reads w->q
+    and w->scale on every call, include/kernix_model.h:143-175); the struct has the reference's six fields"""
+    d = load("qmatmul_lcg.npz")
+    k, n, rows = (int(v) for v in d["cases"][1])
+    q = np.ascontiguousarray(d["q1"])
+    scale, bias, x = (np.ascontiguousarray(d[f"{v}1"]) for v in ("scale", "bias", "x"))
+    w = L.kernix_qweight_pack(_p(q), _p(scale), k, n)
+    assert w
+    try:
+        y = np.zeros((rows, n), np.float32)
+        assert L.kernix_qmatmul(_p(x), rows, w, _p(bias), 0, _p(y)) == 0
+        assert same(y, d["y1"])
+        s = _QWeight.from_address(w)
+        assert (s.k, s.n) == (k, n)
+        qv = np.ctypeslib.as_array(s.q, shape=(s.np * s.kp,))
+        sv = np.ctypeslib.as_array(s.scale, shape=(s.np,))
+        qv[:] = -qv                         # every weight negated in place, every scale halved (exact)
+        sv[:n] = sv[:n] * np.float32(0.5)
+        y2 = np.zeros((rows, n), np.float32)
+        assert L.kernix_qmatmul(_p(x), rows, w, _p(bias), 0, _p(y2)) == 0
+        want = knx_ref.qmatmul(x, -q, scale * np.float32(0.5), bias)
+        assert same(y2, want)
+        assert not same(y2, y)
+    finally:
+        L.kernix_qweight_free(w)
+
+
 @pytest.mark.gpu
 def test_gpu_i8gemm_golden(L):
     import torch

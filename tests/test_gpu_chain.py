@@ -45,6 +45,31 @@ def L():
     return lib
 
 
+_STATUS = []
+
+
+def status_word():
+    """the launches' status word: one int of pinned host memory (set by a barrier that stopped waiting), held until
+    the process ends"""
+    if not _STATUS:
+        p = ctypes.c_void_p()
+        hipabi.check(hipabi.lib().knx_hip_host_malloc(ctypes.byref(p), 4))
+        w = ctypes.c_int.from_address(p.value)
+        w.value = 0
+        _STATUS.append((p.value, w))
+    return _STATUS[0][0]
+
+
+def chain_status():
+    """the status word after the launches so far (synchronized), then cleared"""
+    torch.cuda.synchronize()
+    status_word()
+    w = _STATUS[0][1]
+    v = w.value
+    w.value = 0
+    return v
+
+
 class Chain:
     """Random layers (int8: weights in [-127, 127] with per-channel scales; fp32: N(0, 1/√k)) and their device
     buffers; run() calls the chain, outputs() reads every layer's output."""
@@ -91,7 +116,7 @@ class Chain:
         dx = dev(x)
         self.keep.append(dx)
         hipabi.check(L.knx_hip_linear_chain(ptr(dx), x.shape[1], self.rows, self.layers, len(self.kinds), ptr(scratch),
-                                            nb, hipabi.stream()))
+                                            nb, status_word(), hipabi.stream()))
 
     def outputs(self):
         return [host(y) for y in self.ys]
@@ -142,7 +167,7 @@ def test_chain_mlp(L, rows, kind):
             inp = ch.layer_ref(l, inp)
         assert np.array_equal(outs[-1], inp)
     assert not (host(s[:64]).view(np.uint64) % QUANTUM).any(), "barrier words not at a multiple of the quantum"
-    assert L.knx_hip_chain_status() == 0
+    assert chain_status() == 0
 
 
 CASES = [
@@ -203,12 +228,12 @@ def test_chain_channel_blocks(L, monkeypatch, target, rows):
         ch.run(L, x, s, nb)
     check_layers(ch, x, ch.outputs())
     assert not (host(s[:64]).view(np.uint64) % QUANTUM).any()
-    assert L.knx_hip_chain_status() == 0
+    assert chain_status() == 0
 
 
 def test_chain_full_grid(L, monkeypatch):
-    """256 workgroups (one 16-channel block per item, 512 items in the wide layers, so two items each): every item
-    computed once, bit-exact, and the barrier words advance by one quantum per launch"""
+    """the largest grid, 64 workgroups (one 16-channel block per item, 512 items in the wide layers, so eight items
+    each): every item computed once, bit-exact, and the barrier words advance by one quantum per launch"""
     monkeypatch.setenv("KNX_CHAIN_ITEMS", "100000")
     rng = np.random.default_rng(11)
     dims = (64, 2048, 64, 2048, 8)
@@ -221,7 +246,7 @@ def test_chain_full_grid(L, monkeypatch):
     check_layers(ch, x, ch.outputs())
     words = host(s[:64]).view(np.uint64)
     assert (words[:3] - before[:3] == 3 * QUANTUM).all(), words[:4]
-    assert L.knx_hip_chain_status() == 0
+    assert chain_status() == 0
 
 
 def test_chain_special_rows(L):
@@ -256,14 +281,35 @@ def test_chain_repeated_and_rejected(L):
     assert np.array_equal(ch.outputs()[-1], first)
     dx = dev(x)
     st = hipabi.stream()
-    assert L.knx_hip_linear_chain(ptr(dx), MLP[0], 65, ch.layers, 3, ptr(s), nb, st) == -1  # > 64 rows
-    assert L.knx_hip_linear_chain(ptr(dx), MLP[0], 8, ch.layers, 3, ptr(s), 255, st) == -1  # scratch too small
-    assert L.knx_hip_linear_chain(ptr(dx), MLP[0], 8, ch.layers, 0, ptr(s), nb, st) == -1
+    assert L.knx_hip_linear_chain(ptr(dx), MLP[0], 65, ch.layers, 3, ptr(s), nb, status_word(), st) == -1  # > 64 rows
+    assert L.knx_hip_linear_chain(ptr(dx), MLP[0], 8, ch.layers, 3, ptr(s), 255, status_word(), st) == -1  # scratch too small
+    assert L.knx_hip_linear_chain(ptr(dx), MLP[0], 8, ch.layers, 0, ptr(s), nb, status_word(), st) == -1
     bad = (ChainLayer * 3)(*ch.layers)
     bad[1].y = bad[0].y  # output over its own input
-    assert L.knx_hip_linear_chain(ptr(dx), MLP[0], 8, bad, 3, ptr(s), nb, st) == -1
+    assert L.knx_hip_linear_chain(ptr(dx), MLP[0], 8, bad, 3, ptr(s), nb, status_word(), st) == -1
     bad = (ChainLayer * 3)(*ch.layers)
     bad[1].k = 510  # not the previous layer's n
-    assert L.knx_hip_linear_chain(ptr(dx), MLP[0], 8, bad, 3, ptr(s), nb, st) == -1
+    assert L.knx_hip_linear_chain(ptr(dx), MLP[0], 8, bad, 3, ptr(s), nb, status_word(), st) == -1
+    assert L.knx_hip_linear_chain(ptr(dx), MLP[0], 8, ch.layers, 3, ptr(s), nb, None, st) == -1  # no status word
     assert L.knx_hip_linear_chain_scratch(ch.layers, 3, 0) == 0
-    assert L.knx_hip_chain_status() == 0
+    assert chain_status() == 0
+
+
+def test_chain_barrier_gives_up(L, monkeypatch):
+    """a barrier that stops waiting sets the caller's status word and every workgroup still ends: KNX_GRID_SPIN=0
+    makes every workgroup but the last to arrive stop without polling (forced from the host: all loads and stores
+    stay where a normal launch puts them); the barrier words still advance by one quantum per launch, so the next
+    launch with the normal wait on the same scratch is bit-exact again and leaves the word at 0"""
+    rng = np.random.default_rng(21)
+    ch = Chain(rng, 16, MLP, ["i8"] * 3, [RELU, RELU, NONE])
+    x = rng.uniform(0, 1, (16, MLP[0])).astype(np.float32)
+    s, nb = ch.scratch(L)
+    monkeypatch.setenv("KNX_GRID_SPIN", "0")
+    for _ in range(3):
+        ch.run(L, x, s, nb)
+        assert chain_status() == 1, "a barrier of more than one workgroup must stop waiting at a spin limit of 0"
+    assert not (host(s[:64]).view(np.uint64) % QUANTUM).any()
+    monkeypatch.delenv("KNX_GRID_SPIN")
+    ch.run(L, x, s, nb)
+    assert chain_status() == 0
+    check_layers(ch, x, ch.outputs())

@@ -288,6 +288,43 @@ def test_linear_chain_matches_separate_steps(tmp_path, monkeypatch, mode, batch)
         assert rel_err(got["1"], got["0"]) <= 1e-5
 
 
+@pytest.mark.parametrize("batch", [1, 16])
+def test_linear_chain_gave_up_is_recomputed(tmp_path, monkeypatch, capfd, batch):
+    """A chain launch whose barrier stops waiting (forced from the host: KNX_GRID_SPIN=0 stops every workgroup but
+    the last to arrive without polling; all accesses stay those of a normal launch) does not leave wrong outputs:
+    the host forward recomputes the whole forward one launch per layer in the same call, so its result is the bits of
+    KNX_CHAIN=0; a device forward reports it through device_status() (False once, then True after a normal
+    forward).  i8 mode at batch 16, the reference's int8 dispatch at batch 1: every layer int8, so the chain and the
+    separate launches give the same bits."""
+    import torch
+
+    p = str(tmp_path / "mlp.knx")
+    x = configs.int8_mlp(p, batch=batch)
+    m = Model(p)
+    if batch > 2:
+        m.set_int8_mode(INT8_I8)
+    monkeypatch.setenv("KNX_CHAIN", "0")
+    want = m(x).copy()
+    monkeypatch.delenv("KNX_CHAIN")
+    capfd.readouterr()
+    monkeypatch.setenv("KNX_GRID_SPIN", "0")
+    got = m(x).copy()
+    assert "recomputed one launch per layer" in capfd.readouterr().err
+    assert np.array_equal(got, want)
+    dx = torch.from_numpy(np.ascontiguousarray(x)).cuda()
+    out = torch.zeros((len(x), m.out_dim), dtype=torch.float32, device="cuda")
+    for _ in range(3):
+        m.forward_device(dx.data_ptr(), dx.shape[0], out.data_ptr())
+        assert not m.device_status()
+    monkeypatch.delenv("KNX_GRID_SPIN")
+    m.forward_device(dx.data_ptr(), dx.shape[0], out.data_ptr())
+    assert m.device_status()
+    assert np.array_equal(out.cpu().numpy(), want)
+    assert np.array_equal(m(x), want)
+    assert "recomputed" not in capfd.readouterr().err
+    m.close()
+
+
 def test_linear_chain_graph_boundaries(tmp_path):
     """Chains inside a graph: a run broken by a value that two steps read, a Linear whose output feeds a fused add,
     a layer_norm between Linears, int8 and fp32 weights mixed, pieces of ≤ 64 rows through the workspace limit;

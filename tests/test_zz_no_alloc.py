@@ -89,7 +89,7 @@ def test_noalloc_residual_and_few_rows(L):
     R = rng.normal(0, 1, (96, 256)).astype(np.float32)
     got, want = _both(L, x, qp, scale, bias, kp, 0, R)
     assert _same(got, want)
-    # at <= 4 rows the quantizer runs inside the GEMM and the scratch is not used
+    # 3 rows of 784 -> 512 (rows <= 16 and rows*k*n <= 2^23): the quantizer runs inside the GEMM, no scratch
     x, q, qp, scale, bias, kp = _case(rng, 3, 784, 512)
     got, want = _both(L, x, qp, scale, bias, kp, 0)
     assert _same(got, want)
@@ -115,3 +115,27 @@ def test_noalloc_at_the_limit_and_beyond(L):
     assert rc == -1  # KNX_EINVAL
     assert b"limit" in L.knx_hip_last_error()
     assert bool((host(Y) == 5.0).all())
+
+
+def test_noalloc_allocates_nothing(L):
+    """after one warm-up call, further calls leave the device's free memory unchanged (hipMemGetInfo)"""
+    rng = np.random.default_rng(11)
+    x, q, qp, scale, bias, kp = _case(rng, 512, 2048, 1024)
+    rows, k = x.shape
+    n = qp.shape[0]
+    dx, dq, ds, db = dev(x), dev(qp), dev(scale), dev(bias)
+    Y = torch.empty((rows, n), dtype=torch.float32, device="cuda")
+    s = hipabi.stream()
+
+    def call(r):
+        hipabi.check(L.knx_hip_qlinear_noalloc(ptr(dx), k, r, k, kp, ptr(dq), kp, n, ptr(ds), ptr(db), 0, 0.0, 0,
+                                               None, 0, ptr(Y), n, s))
+
+    call(rows)
+    torch.cuda.synchronize()
+    free0, _ = torch.cuda.mem_get_info()
+    for r in (rows, 7, 300, 1, rows):
+        call(r)
+    torch.cuda.synchronize()
+    free1, _ = torch.cuda.mem_get_info()
+    assert free1 == free0, (free0, free1)
