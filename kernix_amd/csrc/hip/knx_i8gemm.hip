@@ -20,6 +20,8 @@
 
 #include <string>
 #include <mutex>
+#include <unordered_map>
+#include <algorithm>
 #include <type_traits>
 #include <utility>
 
@@ -27,6 +29,7 @@
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
+typedef unsigned v4u_t __attribute__((ext_vector_type(4)));
 
 namespace {
 
@@ -49,6 +52,8 @@ struct I8Args {
     int tiles_m, tiles_n;
     const float* R;  // residual added after the activation (same layout as Y, stride ldr), or null
     int ldr;
+    int32_t* part;   // K split across workgroups: int32 partial tiles (split kernels only)
+    unsigned* cnt;   // K split: one arrival counter per output tile, a multiple of the split count between launches
 };
 
 // 16-byte chunk swizzle within a 64-byte LDS row: distinct chunks for the rows that share a bank group, whether the
@@ -559,7 +564,64 @@ int launch_pipe(I8Args p, hipStream_t s, const char* name)
 // (row-in-slot · ld + chunk).  A tile that would run past M (or N) is moved back to end at row M (column N): it
 // recomputes a few rows of its neighbour and stores only the rows (columns) it owns, so every operand row it reads
 // exists.  A half k-tile at the end (K % 128 == 64) loads its lower 64 bytes twice and multiplies two k-steps only.
-template <int BM, int BN, int WM, int WN, int ASTG, bool EARLY = false>
+// ---- K split across workgroups (KS > 1), for shapes whose output tiles are fewer than the CUs (M = 256,
+// N = K = 4096 in 128×128 tiles: 64 tiles, 4 workgroups each over a quarter of K).  Every workgroup stores its int32
+// partial tile at device scope (sc1 stores, through to the coherence point the XCDs share) into the stream's
+// scratch, then increments its tile's arrival counter; the workgroup whose increment completes a multiple of KS is
+// the last of the tile: it loads the other KS − 1 partial tiles (sc1 loads), adds them to its own (int32: exact in
+// any order) and runs the epilogue.  No workgroup waits for another, so residency does not matter, and every
+// launch adds exactly kSplitQuantum to each counter, so nothing is reset between launches.  Partial layout: unit (tile, split)
+// owns FM·FN·4 × NT 16-byte pieces, piece q of thread t at (q·NT + t)·16 — each store instruction of a wave writes
+// 1 KB of consecutive bytes.
+constexpr unsigned kSplitRsrcWord3 = 0x00020000u;  // raw buffer, 32-bit data format
+constexpr int kSc1 = 16;                           // cache policy of a buffer access: sc1 (device scope)
+
+constexpr unsigned kSplitQuantum = 256;            // added to a tile's arrival counter per launch
+
+template <int FM, int FN, int NT, int KS>
+__device__ __forceinline__ bool split_reduce(const I8Args& p, v16i (&acc)[FM][FN], int tile, int split, unsigned* flag)
+{
+    constexpr int Q = FM * FN * 4;
+    static_assert(KS >= 2 && kSplitQuantum % KS == 0, "split count");
+    const int t = threadIdx.x;
+    const long long bytes = (long long)p.tiles_m * p.tiles_n * KS * Q * NT * 16;
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(p.part, (short)0, (int)bytes, kSplitRsrcWord3);
+    const int own = (tile * KS + split) * Q * NT * 16;
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+        const v16i& a = acc[(q >> 2) / FN][(q >> 2) % FN];
+        const v4i v = {a[4 * (q & 3)], a[4 * (q & 3) + 1], a[4 * (q & 3) + 2], a[4 * (q & 3) + 3]};
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u_t, v), r, own + (q * NT + t) * 16, 0, kSc1);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial is at the coherence point
+    __syncthreads();
+    if (t == 0) {
+        // the counter is a multiple of kSplitQuantum when the launch starts; the KS-th arrival completes the tile and
+        // tops the counter up to the next multiple, whatever KS the next launch on this scratch uses
+        const unsigned old = __hip_atomic_fetch_add(p.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const bool last = old % kSplitQuantum == KS - 1;
+        if (last) __hip_atomic_fetch_add(p.cnt + tile, kSplitQuantum - KS, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *flag = last;
+    }
+    __syncthreads();
+    if (!*flag) return false;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+        if (s == split) continue;
+        const int base = (tile * KS + s) * Q * NT * 16;
+        v4i got[Q];
+#pragma unroll
+        for (int q = 0; q < Q; ++q)
+            got[q] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, base + (q * NT + t) * 16, 0, kSc1));
+#pragma unroll
+        for (int q = 0; q < Q; ++q)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[(q >> 2) / FN][(q >> 2) % FN][4 * (q & 3) + e] += got[q][e];
+    }
+    return true;
+}
+
+template <int BM, int BN, int WM, int WN, int ASTG, bool EARLY = false, int KS = 1>
 __global__ void __launch_bounds__(WM * WN * 64) i8gemm_k128(I8Args p)
 {
     constexpr int NW = WM * WN;
@@ -582,8 +644,18 @@ __global__ void __launch_bounds__(WM * WN * 64) i8gemm_k128(I8Args p)
     const int t = threadIdx.x, lane = t & 63;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int wm = wave / WN, wn = wave % WN;
-    int tm, tn;
-    tile_of_best(blockIdx.x, p.tiles_m, p.tiles_n, BM, BN, tm, tn);
+    int tm, tn, split = 0;
+    if (KS == 1) {
+        tile_of_best(blockIdx.x, p.tiles_m, p.tiles_n, BM, BN, tm, tn);
+    } else {
+        // consecutive workgroups go to consecutive XCDs: XCD x takes units [x·G/8, (x+1)·G/8), tm fastest, then the
+        // split, then tn, so the splits of a tile and the tiles that share W rows stay on one XCD
+        const int G = gridDim.x;
+        const int g = G % 8 == 0 ? (blockIdx.x & 7) * (G / 8) + (blockIdx.x >> 3) : blockIdx.x;
+        tm = g % p.tiles_m;
+        split = (g / p.tiles_m) % KS;
+        tn = g / p.tiles_m / KS;
+    }
     const int mlo = tm * BM, nlo = tn * BN;                  // first row / column this tile owns
     const int m0 = min(mlo, p.M - BM), n0 = min(nlo, p.N - BN);  // first row / column it computes
 
@@ -599,12 +671,14 @@ __global__ void __launch_bounds__(WM * WN * 64) i8gemm_k128(I8Args p)
 
     // slot i covers rows (i·NW + wave)·8 + 0..7 of the tile's A rows then W rows; lane l loads row l >> 3 of the slot,
     // global chunk (l & 7) ^ swz8(row) = (l & 7) ^ (l >> 3) ^ ((i·NW + wave) & 7) into LDS position l & 7.  The
-    // address is a scalar base (operand tile + slot row · ld + k) plus this lane's 32-bit offset.
-    const int8_t* tile_a = p.A + (size_t)m0 * p.lda;
-    const int8_t* tile_w = p.W + (size_t)n0 * p.ldw;
+    // address is a scalar base (operand tile + slot row · ld + k) plus this lane's 32-bit offset.  With a K split
+    // the workgroup's K range is [split·K/KS, (split+1)·K/KS), whole k-tiles (K % (128·KS) == 0).
+    const int kspan = p.K / KS;
+    const int8_t* tile_a = p.A + (size_t)m0 * p.lda + (size_t)split * kspan;
+    const int8_t* tile_w = p.W + (size_t)n0 * p.ldw + (size_t)split * kspan;
     const int cl = (lane & 7) ^ (lane >> 3), rs = lane >> 3;
-    const int nk = (p.K + 127) / 128;
-    const bool half = (p.K & 127) != 0;
+    const int nk = (kspan + 127) / 128;
+    const bool half = (kspan & 127) != 0;
     auto abuf = [&](int kt) { return lds + (ASTG == 2 ? (kt & 1) : kt % 3) * ABYTES; };
     auto wbuf = [&](int kt) { return lds + WRING + (kt & 1) * WBYTES; };
     // load slot i of k-tile kt into its stage
@@ -742,18 +816,73 @@ __global__ void __launch_bounds__(WM * WN * 64) i8gemm_k128(I8Args p)
     if (nk >= 2) ktile(kt++, yes{}, no{}, no{}, w0{}, true);
     ktile(kt, no{}, no{}, no{}, w0{}, !half);
 
+    if constexpr (KS > 1) {
+        __shared__ unsigned arrived;
+        if (!split_reduce<FM, FN, NW * 64, KS>(p, acc, tm * p.tiles_n + tn, split, &arrived)) return;
+    }
     // the row scales go to the W stage that the last k-tile does not use (free since the barrier of k-tile nk-2)
     float* row_scale = reinterpret_cast<float*>(wbuf(nk) + WBYTES - BM * 4);
     tile_epilogue<BM, BN, WM, WN>(p, acc, lds, row_scale, my_sa, m0, nb, swv, bv, mlo, nlo);
 }
 
-template <int BM, int BN, int WM, int WN, int ASTG, bool EARLY = false>
+__global__ void zero_words(unsigned* w, size_t n)
+{
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) w[i] = 0;
+}
+
+// Scratch of the K-split kernels, one per stream (launches on one stream are ordered, so they may share it; launches
+// on different streams never do): arrival counters (zero when allocated, a multiple of the split count after every
+// launch) followed by the partial tiles.  Grown when a launch needs more (the stream is synchronized first: earlier
+// launches may still use the old one); kept until the process ends.
+struct SplitScratch {
+    char* buf = nullptr;
+    size_t cnt_bytes = 0, part_bytes = 0;
+};
+std::mutex g_split_mu;
+std::unordered_map<hipStream_t, SplitScratch> g_split;
+thread_local bool g_no_alloc = false;  // inside knx_hip_qlinear_noalloc: no K split (it would allocate)
+
+int split_scratch(hipStream_t s, size_t part_bytes, size_t cnt_words, int32_t** part, unsigned** cnt, const char* name)
+{
+    const size_t cb = (cnt_words * sizeof(unsigned) + 255) / 256 * 256;
+    std::lock_guard<std::mutex> lock(g_split_mu);
+    SplitScratch& sc = g_split[s];
+    if (sc.buf == nullptr || sc.cnt_bytes < cb || sc.part_bytes < part_bytes) {
+        const size_t nc = std::max(cb, sc.cnt_bytes), np = std::max(part_bytes, sc.part_bytes);
+        if (sc.buf != nullptr) {
+            if (hipStreamSynchronize(s) != hipSuccess || hipFree(sc.buf) != hipSuccess)
+                return knx::fail(KNX_EHIP, "%s: K-split scratch release failed", name);
+            sc = SplitScratch{};
+        }
+        void* b = nullptr;
+        const hipError_t e = hipMalloc(&b, nc + np);
+        if (e != hipSuccess) return knx::fail(KNX_EHIP, "%s: K-split scratch (%zu bytes): %s", name, nc + np, hipGetErrorString(e));
+        hipLaunchKernelGGL(zero_words, dim3(64), dim3(256), 0, s, static_cast<unsigned*>(b), nc / sizeof(unsigned));
+        if (knx::check_launch(name) != KNX_OK) {
+            hipFree(b);
+            return KNX_EHIP;
+        }
+        sc.buf = static_cast<char*>(b);
+        sc.cnt_bytes = nc;
+        sc.part_bytes = np;
+    }
+    *cnt = reinterpret_cast<unsigned*>(sc.buf);
+    *part = reinterpret_cast<int32_t*>(sc.buf + sc.cnt_bytes);
+    return KNX_OK;
+}
+
+template <int BM, int BN, int WM, int WN, int ASTG, bool EARLY = false, int KS = 1>
 int launch_k128(I8Args p, hipStream_t s, const char* name)
 {
     p.tiles_m = (p.M + BM - 1) / BM;
     p.tiles_n = (p.N + BN - 1) / BN;
-    const unsigned grid = (unsigned)p.tiles_m * (unsigned)p.tiles_n;
-    hipLaunchKernelGGL((i8gemm_k128<BM, BN, WM, WN, ASTG, EARLY>), dim3(grid), dim3(WM * WN * 64), 0, s, p);
+    const unsigned grid = (unsigned)p.tiles_m * (unsigned)p.tiles_n * (unsigned)KS;
+    if (KS > 1) {
+        const size_t tiles = (size_t)p.tiles_m * (size_t)p.tiles_n;
+        const int rc = split_scratch(s, tiles * KS * BM * BN * sizeof(int32_t), tiles, &p.part, &p.cnt, name);
+        if (rc != KNX_OK) return rc;
+    }
+    hipLaunchKernelGGL((i8gemm_k128<BM, BN, WM, WN, ASTG, EARLY, KS>), dim3(grid), dim3(WM * WN * 64), 0, s, p);
     return knx::check_launch(name);
 }
 
@@ -924,6 +1053,15 @@ template <int BM, int BN>
 bool k128_fits(const I8Args& p)
 {
     return p.M >= BM && p.N >= BN && (long)8 * p.lda < 0x7fffffffL && (long)8 * p.ldw < 0x7fffffffL;
+}
+
+// the K split: whole 128-byte k-tiles per split, partial tiles addressable by 32-bit buffer offsets, and no
+// allocation inside knx_hip_qlinear_noalloc
+template <int BM, int BN, int KS>
+bool ksplit_fits(const I8Args& p)
+{
+    const long long tiles = (long long)((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
+    return k128_fits<BM, BN>(p) && p.K % (128 * KS) == 0 && tiles * KS * BM * BN * 4 < (1LL << 31) - 256 && !g_no_alloc;
 }
 
 // f(integral_constant<int, d>) for d = 0, 1, …: a loop whose index is a compile-time constant in the body
@@ -1600,6 +1738,11 @@ static int i8gemm_run(I8Args p, hipStream_t s, const char* name)
         if (f == "k128ma3" && k128_fits<128, 128>(p)) return launch_k128<128, 128, 2, 2, 3>(p, s, name);
         if (f == "ring64s4" && k128_fits<64, 64>(p)) return launch_ring<64, 64, 2, 2, 4, 1>(p, s, name);
         if (f == "ring64g2" && k128_fits<64, 64>(p) && ring_split_fits<2, 4>(p)) return launch_ring<64, 64, 2, 2, 4, 1, 2>(p, s, name);
+        if (f == "k128ms4" && ksplit_fits<128, 128, 4>(p)) return launch_k128<128, 128, 2, 2, 2, false, 4>(p, s, name);
+        if (f == "k128ma3s4" && ksplit_fits<128, 128, 4>(p)) return launch_k128<128, 128, 2, 2, 3, false, 4>(p, s, name);
+        if (f == "k128m8s4" && ksplit_fits<128, 128, 4>(p)) return launch_k128<128, 128, 4, 2, 2, false, 4>(p, s, name);
+        if (f == "k128ms2" && ksplit_fits<128, 128, 2>(p)) return launch_k128<128, 128, 2, 2, 2, false, 2>(p, s, name);
+        if (f == "k128ms8" && ksplit_fits<128, 128, 8>(p)) return launch_k128<128, 128, 2, 2, 2, false, 8>(p, s, name);
 #ifdef KNX_TUNING
         // variants no shape selects (measured slower where they fit), built only for tuning (-DKNX_TUNING)
         if (f == "tile256") return launch_tile<256, 256, 2, 2>(p, s, name);
@@ -1795,7 +1938,11 @@ extern "C" int knx_hip_qlinear_noalloc(const float* x, int ldx, int rows, int k,
         sx = reinterpret_cast<float*>(base);
         xq = reinterpret_cast<int8_t*>(base + ((size_t)rows * sizeof(float) + 255) / 256 * 256);
     }
-    // the same kernels and arguments as knx_hip_qlinear (its one-kernel form writes no scratch)
-    return knx_hip_qlinear(x, ldx, rows, k, kp, xq, sx, W, ldw, n, sw, bias, act, alpha, accumulate, R, ldr, Y, ldy,
-                           stream);
+    // the same kernels and arguments as knx_hip_qlinear (its one-kernel form writes no scratch), without the K split
+    // (its scratch is allocated on first use)
+    g_no_alloc = true;
+    const int rc = knx_hip_qlinear(x, ldx, rows, k, kp, xq, sx, W, ldw, n, sw, bias, act, alpha, accumulate, R, ldr,
+                                   Y, ldy, stream);
+    g_no_alloc = false;
+    return rc;
 }

@@ -92,7 +92,8 @@ def test_i8gemm_standalone_config(L, M):
 # every kernel instantiation a shape can select, each forced onto every edge shape (a library built with KNX_TUNING=1
 # also has the tuning-only variants: pp, k128, k128w8, k128w8ta3, k128w16, ring64s8k2, ring64s8, pipe256, pipe256w8,
 # pipe256s3, pipe128, tile256, which this list can name there)
-I8_VARIANTS = ["default", "k128w8t", "k128m", "k128ma3", "k128w8ta3e", "ring64s4", "ring64g2", "pipe64", "tile64"]
+I8_VARIANTS = ["default", "k128w8t", "k128m", "k128ma3", "k128w8ta3e", "ring64s4", "ring64g2", "pipe64", "tile64",
+               "k128ms4", "k128ma3s4", "k128m8s4", "k128ms2", "k128ms8"]
 # tiles moved back at the M/N edges, half k-tiles (K % 128 == 64), N % 4 != 0, one whole 256x256 tile, 2..4 k-tiles
 # (every branch of the three-stage A ring's prologue and tail), an 8 x 8 tile grid split into XCD blocks, and for the
 # K split between two rings: 6 k-tiles per ring, ragged tiles with 8 per ring, 13 k-tiles (no split)
@@ -127,6 +128,45 @@ def test_i8gemm_variants_y_only(L, monkeypatch, variant, M, N, K):
     assert np.array_equal(host(Y2), (y0 + plain).astype(np.float32))
 
 
+def test_i8gemm_ksplit_sequence(L, monkeypatch):
+    """The K split across workgroups (exact int32 partial tiles, the last workgroup of a tile adds them): the
+    standalone M = 256 workload (K = N = 4096, the config's inputs) bit-exact in accumulators and outputs for every
+    split count, called in turn on one stream so that launches of 2, 4 and 8 splits share the arrival counters (each
+    launch leaves them at the next multiple of the counter quantum), then a larger shape that grows the scratch, then
+    the first again (reference include/kernix_model.h:143-178)"""
+    from kernix_amd import configs
+
+    A, W, sa, sw, bias = configs.i8gemm_inputs(256)
+    M, K = A.shape
+    N = W.shape[0]
+    want_y, want_acc = knx_ref.i8gemm(A, W, sa, sw, bias, act_id=0, threads=16)
+    dA, dW, dsa, dsw, db = dev(A), dev(W), dev(sa), dev(sw), dev(bias)
+    rng = np.random.default_rng(3)
+    A2 = rng.integers(-127, 128, (640, 2048), dtype=np.int8)
+    W2 = rng.integers(-128, 128, (1000, 2048), dtype=np.int8)
+    s2 = rng.uniform(0.001, 0.01, 640).astype(np.float32)
+    w2 = rng.uniform(0.001, 0.01, 1000).astype(np.float32)
+    b2 = rng.normal(0, 0.1, 1000).astype(np.float32)
+    want2, acc2 = knx_ref.i8gemm(A2, W2, s2, w2, b2, act_id=0)
+    d2 = [dev(a) for a in (A2, W2, s2, w2, b2)]
+    for variant in ("k128ms2", "k128ms4", "k128ms8", "k128ms4", "k128m8s4", "big", "k128ms4", "k128ma3s4"):
+        if variant == "big":
+            monkeypatch.setenv("KNX_I8_KERNEL", "k128ms4")
+            Y2 = torch.full((640, 1000), 7.0, dtype=torch.float32, device="cuda")
+            C2 = torch.zeros((640, 1000), dtype=torch.int32, device="cuda")
+            hipabi.check(L.knx_hip_i8gemm(640, 1000, 2048, ptr(d2[0]), 2048, ptr(d2[2]), ptr(d2[1]), 2048, ptr(d2[3]),
+                                          ptr(d2[4]), 0, 0.0, 0, ptr(Y2), 1000, ptr(C2), 1000, hipabi.stream()))
+            assert np.array_equal(host(C2), acc2) and np.array_equal(host(Y2), want2), variant
+            continue
+        monkeypatch.setenv("KNX_I8_KERNEL", variant)
+        Y = torch.full((M, N), 7.0, dtype=torch.float32, device="cuda")
+        acc = torch.zeros((M, N), dtype=torch.int32, device="cuda")
+        hipabi.check(L.knx_hip_i8gemm(M, N, K, ptr(dA), K, ptr(dsa), ptr(dW), K, ptr(dsw), ptr(db), 0, 0.0, 0,
+                                      ptr(Y), N, ptr(acc), N, hipabi.stream()))
+        assert np.array_equal(host(acc), want_acc), variant
+        assert np.array_equal(host(Y), want_y), variant
+
+
 I8_SKINNY_VARIANTS = ["default", "skinny"]
 # every row-block count (1, 2, 4 blocks of 16), a lone half k-tile (K = 64), trailing half k-tiles (K % 128 == 64)
 I8_SKINNY_SHAPES = [(1, 16, 64), (3, 100, 192), (16, 4096, 4096), (17, 300, 320), (33, 64, 448), (64, 520, 1024),
@@ -155,7 +195,7 @@ def test_i8gemm_skinny_variants(L, monkeypatch, variant, M, N, K):
 
 
 @pytest.mark.parametrize("variant", ["default", "k128w8t", "k128w8ta3e", "k128m", "ring64s4", "ring64g2", "pipe64", "tile64",
-                                     "skinny"])
+                                     "skinny", "k128ms4", "k128m8s4"])
 @pytest.mark.parametrize("M,N,K,inplace", [(300, 300, 1024, False), (520, 700, 320, True), (2048, 2048, 2048, False),
                                            (48, 520, 192, True)])
 def test_i8gemm_residual(L, monkeypatch, variant, M, N, K, inplace):
