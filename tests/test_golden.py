@@ -56,6 +56,38 @@ def test_library_loads_golden_model():
     m.close()
 
 
+def test_quantizer_matches_reference_exporter():
+    """tests/golden/quant_blocks.npz, written by the reference's own tools/knx_quant.py (make_quant_golden.py): the
+    package writer's quantize and weight blocks and the oracle's ko_quantize_cols reproduce its scales, int8 values
+    and bytes exactly, on matrices holding all-zero columns and rows, exact ties, quotients next to a half-way point
+    and float64 weights whose column maximum rounds differently through float32; the fixture also tells apart the
+    plausible restatement mistakes (float32 quotient, reciprocal multiply, ties away from zero, scale from a float32
+    maximum)"""
+    from kernix_amd import knxfile
+
+    d = load("quant_blocks.npz")
+    for name in ("w32", "w64"):
+        w = d[f"{name}_w"]
+        for axis, per in (("col", "column"), ("row", "row")):
+            scale, q = knxfile.quantize(w, per)
+            assert np.array_equal(scale, d[f"{name}_scale_{axis}"]) and scale.dtype == np.float32, (name, axis)
+            assert np.array_equal(q, d[f"{name}_q_{axis}"]), (name, axis)
+        scale, q = knx_ref.quantize_cols(w)
+        assert np.array_equal(scale, d[f"{name}_scale_col"]) and np.array_equal(q, d[f"{name}_q_col"]), name
+        for mode in ("f32", "i8_col", "i8_row"):
+            assert knxfile._weight(w, mode, 2) == d[f"{name}_block_{mode}"].tobytes(), (name, mode)
+        assert knxfile._weight(w, "f32", 1) == d[f"{name}_block_v1"].tobytes(), name
+    # the mistakes the fixture must catch, planted here on the CPU
+    w, s, q = d["w32_w"], d["w32_scale_col"], d["w32_q_col"]
+    assert (np.clip(np.rint(w.astype(np.float32) / s), -127, 127).astype(np.int8) != q).any()
+    assert (np.clip(np.rint(w.astype(np.float32) * (np.float32(1) / s)), -127, 127).astype(np.int8) != q).any()
+    away = np.clip(np.trunc(w / s.astype(np.float64) + 0.5 * np.sign(w)), -127, 127).astype(np.int8)
+    assert (away != q).any()
+    w64, s64 = d["w64_w"], d["w64_scale_col"]
+    m32 = np.abs(w64.astype(np.float32)).max(axis=0)
+    assert (np.where(m32 > 0, m32 / np.float32(127), np.float32(1)).astype(np.float32) != s64).any()
+
+
 # ---------------------------------------------------------------- GPU path
 
 @pytest.fixture(scope="module")
