@@ -1755,6 +1755,8 @@ static int i8gemm_run(I8Args p, hipStream_t s, const char* name)
         if (f == "k128w8ta3" && k128_fits<256, 256>(p)) return launch_k128<256, 256, 4, 2, 3>(p, s, name);
         if (f == "k128w16" && k128_fits<256, 256>(p)) return launch_k128<256, 256, 4, 4, 2>(p, s, name);
         if (f == "pp" && k128_fits<256, 256>(p)) return launch_pp<256, 256>(p, s, name);
+        if (f == "k128r" && k128_fits<256, 128>(p)) return launch_k128<256, 128, 4, 2, 3, true>(p, s, name);
+        if (f == "k128c" && k128_fits<128, 256>(p)) return launch_k128<128, 256, 2, 4, 3, true>(p, s, name);
         if (f == "ring64s8k2" && k128_fits<64, 64>(p)) return launch_ring<64, 64, 2, 2, 8, 2>(p, s, name);
         if (f == "ring64s8" && k128_fits<64, 64>(p)) return launch_ring<64, 64, 2, 2, 8, 1>(p, s, name);
 #endif

@@ -90,8 +90,8 @@ def test_i8gemm_standalone_config(L, M):
 
 
 # every kernel instantiation a shape can select, each forced onto every edge shape (a library built with KNX_TUNING=1
-# also has the tuning-only variants: pp, k128, k128w8, k128w8ta3, k128w16, ring64s8k2, ring64s8, pipe256, pipe256w8,
-# pipe256s3, pipe128, tile256, which this list can name there)
+# also has the tuning-only variants: pp, k128, k128w8, k128w8ta3, k128w16, k128r, k128c, ring64s8k2, ring64s8,
+# pipe256, pipe256w8, pipe256s3, pipe128, tile256, which this list can name there)
 I8_VARIANTS = ["default", "k128w8t", "k128m", "k128ma3", "k128w8ta3e", "ring64s4", "ring64g2", "pipe64", "tile64",
                "k128ms4", "k128ma3s4", "k128m8s4", "k128ms2", "k128ms8"]
 # tiles moved back at the M/N edges, half k-tiles (K % 128 == 64), N % 4 != 0, one whole 256x256 tile, 2..4 k-tiles
