@@ -465,6 +465,27 @@ def run_parts(args, out, want, configs):
                 "tr", lambda p: configs.transformer(p), configs.transformer_flops(), st, fwarm, mode="i8",
                 i8_ops=configs.transformer_ffn_flops(), **kw),
         }
+        # recurrent models (reference kernix_rnn_dir): LSTM over T = 32 steps of 128 features, 128 units, then a
+        # dense 10; each timestep's h·U + cell in one launch of the whole sequence, and the same forward with one
+        # launch per timestep for the product and another for the cell (KNX_RNN_PERSISTENT=0) beside it
+        for bsz in (1, 64):
+            for q8, mode in ((False, "ref"), (True, "ref" if bsz <= 2 else "i8")):
+                key = f"lstm{'_int8' if q8 else ''}_t32_f128_u128_b{bsz}{'_i8' if mode == 'i8' else ''}"
+                fl = configs.lstm_flops(batch=bsz)
+                rec_i8 = configs.lstm_flops(batch=bsz, fin=0, classes=0) if q8 and (mode == "i8" or bsz <= 2) else 0.0
+
+                def line(bsz=bsz, q8=q8, mode=mode, fl=fl, rec_i8=rec_i8):
+                    mk = lambda p: configs.lstm(p, batch=bsz, int8=q8)  # noqa: E731
+                    r = forward_bench("lstm", mk, fl, st, fwarm, mode=mode, i8_ops=rec_i8, **kw)
+                    os.environ["KNX_RNN_PERSISTENT"] = "0"
+                    try:
+                        r0 = forward_bench("lstm", mk, fl, st, fwarm, mode=mode, i8_ops=rec_i8, warm_ms=warm_ms)
+                    finally:
+                        del os.environ["KNX_RNN_PERSISTENT"]
+                    r["per_timestep_launches"] = dict(ms=r0["ms"], samples_per_s=r0["samples_per_s"])
+                    return r
+
+                lines[key] = line
         only = {k for k in args.forward_only.split(",") if k}
         for k, run in lines.items():
             if not only or k in only:

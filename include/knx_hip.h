@@ -38,6 +38,7 @@
  *   knx_hip_upsample        kernix_upsample_run                                 include/kernix_model.h:970-984
  *   knx_hip_embedding       kernix_embedding_run                                include/kernix_model.h:987-1000
  *   knx_hip_rnn_gates       per-timestep gate update of kernix_rnn_dir          include/kernix_model.h:580-631
+ *   knx_hip_rnn_recurrence  one RNN direction's timesteps in one launch         include/kernix_model.h:563-632
  *   knx_hip_linear_chain    consecutive LINEAR steps of a small batch           include/kernix_model.h:1843-1860,
  *                           (kernix_step_run layer after layer, int8 ones       :99-182
  *                           through kernix_qmatmul)
@@ -254,6 +255,21 @@ KNX_API int knx_hip_embedding(const float* ids, int n, const float* table, int V
 /* RNN gate update for one timestep (see the definition for the exact per-kind formulas). */
 KNX_API int knx_hip_rnn_gates(int kind, int act, float alpha, int B, int u, int first_step, float* z, const float* zh,
                               float* c, float* h, float* dst, int dst_stride, void* stream);
+/* The recurrence of one RNN direction over T timesteps as one launch (reference include/kernix_model.h:563-632,
+ * the loop after the input projection).  kind 4 LSTM / 5 GRU / 6 simple RNN with u units; zx: the input projection
+ * x·W + b, B·T rows of gates·u (row b·T + t); the recurrent weight is either int8 (q: gates·u rows of kp bytes, k
+ * contiguous, with qscale per row: h·U in int8 arithmetic with the rows of h quantized as knx_hip_quantize_rows, the
+ * bits of knx_hip_qlinear) or fp32 (U: u × gates·u, or gates·u × u when u_nt); brec: the GRU's recurrent bias.
+ * dir 1 runs t = T−1 … 0.  Output: ret_seq: the state of timestep t of sample b at dst + (b·T + t)·stride, else the
+ * last state at dst + b·stride.  h0, h1: B × u floats each (scratch); scratch: 8 bytes, 256-byte aligned, a multiple
+ * of 256 as the chain's barrier words (the chain and this kernel may share them); status as for knx_hip_linear_chain
+ * (the launch's workgroups, at most 64, must all be resident).  Shapes knx_hip_rnn_recurrence_fits rejects
+ * (B > 64, a weight slice or h that does not fit the workgroup's LDS) are KNX_EINVAL. */
+KNX_API int knx_hip_rnn_recurrence_fits(int kind, int B, int u, int i8);
+KNX_API int knx_hip_rnn_recurrence(int kind, int act, float alpha, int B, int T, int u, int dir, const float* zx,
+                                   const float* U, int u_nt, const int8_t* q, int kp, const float* qscale,
+                                   const float* brec, float* h0, float* h1, float* dst, int stride, int ret_seq,
+                                   void* scratch, size_t scratch_bytes, int* status, void* stream);
 
 #ifdef __cplusplus
 }

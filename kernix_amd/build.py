@@ -19,7 +19,7 @@ OUT = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libkernix.so")
 INC = os.path.join(ROOT, "include")
 
-HIP_SOURCES = ["knx_runtime", "knx_i8gemm", "knx_sgemm", "knx_conv", "knx_rows", "knx_attn", "knx_chain"]
+HIP_SOURCES = ["knx_runtime", "knx_i8gemm", "knx_sgemm", "knx_conv", "knx_rows", "knx_attn", "knx_chain", "knx_rnn"]
 C_SOURCES = ["knx_decode", "knx_graph", "knx_forward", "knx_capi"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

@@ -6,6 +6,8 @@
     cnn           conv3x3 3→64 → conv3x3 64→64 → residual add → conv3x3/2 64→128 → conv3x3/2 128→256 → GAP → dense 10,
                   ReLU after each conv, KNX3 layout 1 (NCHW input), batch 256 × 3×32×32, x ~ N(0,1)
     transformer   4 pre-LN encoder layers, d_model 512, 8 heads, FFN 2048 GELU, seq 128, int8 (I8_COL) weights, batch 64
+    lstm          one LSTM layer over T × F (F = 128, 128 units, T = 32, last state), then a dense 10; KNX3, fp32 or int8
+                  (I8_ROW input / I8_COL recurrent weights) weights, x ~ N(0,1)
 
 Weight init: Linear W ~ N(0, 1/√fan_in) (int8 MLP) or Kaiming-normal N(0, √(2/fan_in)); biases N(0, 0.01);
 conv He-normal with the BatchNorm already folded (a plain conv bias).  Every generator takes a scale divisor so the
@@ -103,6 +105,30 @@ def i8gemm_work(M, N=4096, K=4096):
     ops = 2.0 * M * N * K
     bytes_ = M * K + N * K + 4 * M + 8 * N + 4 * M * N
     return ops, bytes_
+
+
+def lstm(path, seed=0, batch=64, T=32, fin=128, units=128, classes=10, int8=False, cell="LSTM", directions=1):
+    """Recurrent model (reference kernix_rnn_dir, include/kernix_model.h:563-632): one recurrent layer (gates in Keras
+    order), W ~ N(0, 1/√fin), U ~ N(0, 1/√units), bias N(0, 0.01) (a GRU's holds the input and recurrent halves),
+    then a Linear to `classes`."""
+    rng = np.random.default_rng(seed)
+    g = {"LSTM": 4, "GRU": 3, "RNN": 1}[cell] * units
+    b = ModelBuilder((T, fin), int8=int8)
+    dirs = []
+    for _ in range(directions):
+        w = rng.normal(0.0, 1.0 / np.sqrt(fin), (fin, g))
+        u = rng.normal(0.0, 1.0 / np.sqrt(units), (units, g))
+        bias = rng.normal(0.0, 0.01, 2 * g if cell == "GRU" else g)
+        dirs.append((w, u, bias))
+    h = b.recurrent(b.input, cell, units, dirs)
+    width = units * directions
+    h = b.linear(h, rng.normal(0.0, 1.0 / np.sqrt(width), (width, classes)), rng.normal(0.0, 0.01, classes))
+    b.save(path)
+    return rng.normal(0.0, 1.0, (batch, T, fin)).astype(np.float32)
+
+
+def lstm_flops(batch=64, T=32, fin=128, units=128, classes=10, gates=4, directions=1):
+    return directions * 2.0 * batch * T * gates * units * (fin + units) + 2.0 * batch * units * directions * classes
 
 
 def mlp_flops(batch, dims):

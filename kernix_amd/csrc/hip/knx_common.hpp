@@ -75,6 +75,29 @@ __device__ __forceinline__ float knx_act(float x, int act, float alpha)
     }
 }
 
+// Recurrent cells on the summed gate inputs (x·W + b + h·U; reference include/kernix_model.h:595-626), shared by the
+// per-timestep gates kernel and the persistent recurrence so that both give the same bits.
+// LSTM (gates i, f, g, o): c = f·c + i·g (c = i·g at the first step), h = o·act(c).
+__device__ __forceinline__ float knx_lstm_cell(float zi, float zf, float zg, float zo, int act, float alpha, bool step0,
+                                               float& c)
+{
+    const float ig = knx_act(zi, 3, 0.0f), fg = knx_act(zf, 3, 0.0f), gg = knx_act(zg, act, alpha);
+    const float og = knx_act(zo, 3, 0.0f);
+    float cv = step0 ? ig * gg : fg * c;
+    if (!step0) cv = ig * gg + cv;
+    c = cv;
+    return knx_act(cv, act, alpha) * og;
+}
+// GRU (reset after; gates z, r, h~): x* the input side, h* the recurrent side with its bias; h = z·(h − h~) + h~.
+__device__ __forceinline__ float knx_gru_cell(float xz, float xr, float xh, float hz, float hr, float hh_in, int act,
+                                              float alpha, bool step0, float prev)
+{
+    const float zg = knx_act(xz + hz, 3, 0.0f);
+    const float rg = knx_act(xr + hr, 3, 0.0f);
+    const float hh = knx_act(rg * hh_in + xh, act, alpha);
+    return step0 ? (-hh) * zg + hh : (prev - hh) * zg + hh;
+}
+
 // Wave-wide (64 lanes) reductions through DPP/permute; every lane gets the result.
 __device__ __forceinline__ float knx_wave_sum(float v)
 {

@@ -458,7 +458,6 @@ __global__ void __launch_bounds__(256) embedding_kernel(const float* __restrict_
 // kind 4 LSTM (i f g o), 5 GRU (z r h, reset_after), 6 SimpleRNN.  z: B×gu input projection of this step (+ h·U for
 // LSTM/RNN when hu == NULL it is already included); hu: B×gu recurrent term to add (LSTM/RNN) or the GRU recurrent
 // term zh = brec + h·U (GRU).  c, h: B×u state.  dst: h written at dst + b·dst_stride when dst != NULL.
-__device__ __forceinline__ float sigm(float v) { return knx_act(v, 3, 0.0f); }
 
 __global__ void __launch_bounds__(256) rnn_gates_kernel(int kind, int act, float alpha, int B, int u, int step0, float* z,
                                                          const float* hu, float* c, float* h, float* dst, int dst_stride)
@@ -473,21 +472,17 @@ __global__ void __launch_bounds__(256) rnn_gates_kernel(int kind, int act, float
                 const float* hb = hu + (size_t)b * 4 * u;
                 zi = zi + hb[j]; zf = zf + hb[u + j]; zg = zg + hb[2 * u + j]; zo = zo + hb[3 * u + j];
             }
-            const float ig = sigm(zi), fg = sigm(zf), gg = knx_act(zg, act, alpha), og = sigm(zo);
-            float cv = step0 ? ig * gg : fg * c[i];
-            if (!step0) cv = ig * gg + cv;
+            float cv = step0 ? 0.0f : c[i];
+            const float hv = knx_lstm_cell(zi, zf, zg, zo, act, alpha, step0, cv);
             c[i] = cv;
-            const float hv = knx_act(cv, act, alpha) * og;
             h[i] = hv;
             if (dst) dst[(size_t)b * dst_stride + j] = hv;
         } else if (kind == 5) {
             float* zb = z + (size_t)b * 3 * u;
             const float* hz = hu + (size_t)b * 3 * u;
-            const float zg = sigm(zb[j] + hz[j]);
-            const float rg = sigm(zb[u + j] + hz[u + j]);
-            const float hh = knx_act(rg * hz[2 * u + j] + zb[2 * u + j], act, alpha);
             const float prev = step0 ? 0.0f : h[i];
-            const float hv = step0 ? (-hh) * zg + hh : (prev - hh) * zg + hh;
+            const float hv = knx_gru_cell(zb[j], zb[u + j], zb[2 * u + j], hz[j], hz[u + j], hz[2 * u + j], act, alpha,
+                                          step0, prev);
             h[i] = hv;
             if (dst) dst[(size_t)b * dst_stride + j] = hv;
         } else {

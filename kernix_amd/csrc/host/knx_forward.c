@@ -241,13 +241,17 @@ static int int8_rows(const kernix_model* m, size_t rows)
     return (int)(rows < KERNIX_INT8_MAX_ROWS ? rows : KERNIX_INT8_MAX_ROWS);
 }
 
-/* Scratch for knx_hip_linear_chain launches (their barrier words): one block when the model has two LINEAR steps or
- * more, else none. */
+/* Scratch for the grid-barrier launches (knx_hip_linear_chain, knx_hip_rnn_recurrence: their barrier words): one
+ * block when the model has two LINEAR steps or more, or a recurrent step, else none. */
 static size_t chain_scratch_bound(const kernix_model* m)
 {
-    int n = 0;
-    for (int i = 0; i < m->n_steps; i++) n += m->steps[i].kind == KERNIX_OP_LINEAR;
-    return n >= 2 ? KNX_ALIGN : 0;
+    int n = 0, rnn = 0;
+    for (int i = 0; i < m->n_steps; i++) {
+        const int k = m->steps[i].kind;
+        n += k == KERNIX_OP_LINEAR;
+        rnn |= k == KERNIX_OP_LSTM || k == KERNIX_OP_GRU || k == KERNIX_OP_RNN;
+    }
+    return n >= 2 || rnn ? KNX_ALIGN : 0;
 }
 
 /* Walks every workspace tensor for chunks of B samples.  ALLOC also places the dequantized int8 copies (the
@@ -502,8 +506,17 @@ static int run_qlinear(const kernix_model* m, const kernix_qweight* q, const int
     return fp32_linear(rows, q->n, q->k, x, deq->tensor, bias, act, alpha, res, y, st);
 }
 
+/* KNX_RNN_PERSISTENT=0: every timestep as its own launches (tests); also off while a host forward recomputes one
+ * whose grid-barrier launch gave up */
+static int rnn_persistent(const kernix_model* m)
+{
+    const char* e = getenv("KNX_RNN_PERSISTENT");
+    return m->dev->chain != NULL && !m->dev->no_chain && (e == NULL || *e != '0');
+}
+
 /* One direction of an RNN, reference include/kernix_model.h:563-632: the input projection of all timesteps is one
- * GEMM; each timestep adds h·U (int8 or fp32) and applies the gates on the device. */
+ * GEMM; then the timesteps in one launch (knx_hip_rnn_recurrence) where the shape fits it, else per timestep h·U
+ * (int8 or fp32) and the gates as launches of their own. */
 static int run_rnn_dir(const kernix_model* m, kernix_step* s, int dir, const float_tensor* x, float* dst, int stride, void* st)
 {
     struct knx_dstep* d = s->dev;
@@ -528,6 +541,14 @@ static int run_rnn_dir(const kernix_model* m, kernix_step* s, int dir, const flo
     float* sx = d->sx;
     if (hip_ok(knx_hip_sgemm_ep(x->row, gu, s->in, x->tensor, s->in, W, gu, bias, -1, 0.0f, zx, gu, st), "RNN input projection")) return -1;
     const int i8 = q != NULL && (m->int8_mode == KERNIX_INT8_I8 || B <= KERNIX_INT8_MAX_ROWS);
+    if (rnn_persistent(m) && knx_hip_rnn_recurrence_fits(kind, B, u, i8)) {
+        /* every timestep in one launch; h alternates between h and the recurrent-term buffer (B × gu ≥ B × u) */
+        if (!i8 && U == NULL) return -1;
+        return hip_ok(knx_hip_rnn_recurrence(kind, s->act, s->alpha, B, T, u, dir, zx, i8 ? NULL : U, q != NULL,
+                                             i8 ? dq : NULL, q != NULL ? q->kp : 0, dsc, brec, h, hu, dst, stride,
+                                             s->ret_seq, m->dev->chain, m->dev->chain_bytes, m->dev->chain_status, st),
+                      "RNN recurrence");
+    }
     for (int step = 0; step < T; step++) {
         const int t = dir ? T - 1 - step : step;
         if (hip_ok(knx_hip_copy_cols(zx + (size_t)t * gu, T * gu, 0, z, gu, 0, B, gu, st), "RNN gate copy")) return -1;

@@ -55,6 +55,7 @@ SIGS = {
     "knx_hip_linear_chain_scratch": ([ctypes.POINTER(ChainLayer), I, I], Z),
     "knx_hip_linear_chain": ([P, I, I, ctypes.POINTER(ChainLayer), I, P, Z, P, P], I),
     "knx_hip_memset": ([P, I, Z, P], I),
+    "knx_hip_rnn_recurrence_fits": ([I, I, I, I], I),
 }
 
 _lib = None

@@ -1,0 +1,134 @@
+"""The persistent RNN recurrence (knx_hip_rnn_recurrence: every timestep of a direction in one launch; one workgroup
+at <= 2 rows, a grid of workgroups with a barrier per timestep above, KNX_RNN_SOLO=0 forcing the latter) against the
+per-timestep launches (KNX_RNN_PERSISTENT=0) and the oracle (reference kernix_rnn_dir, include/kernix_model.h:563-632).
+
+Where the recurrence runs int8 arithmetic (int8 recurrent weights in i8 mode, or at <= 2 rows in the reference's
+dispatch) both paths quantize the same rows with the quantizer's operations and sum exactly in int32, so they give the
+same bits; fp32 recurrences sum in different orders, within 1e-5 of each other.  Against the oracle: 1e-4 for fp32
+(reference test/model_test.c:268-272 holds the LSTM to 1e-5 of a double loop), and for int8 recurrences the
+reference's int8 bound 1e-2 (test/model_test.c:651).
+"""
+import numpy as np
+import pytest
+
+from kernix_amd import configs, hipabi
+from kernix_amd.kernix import INT8_I8, Model
+from oracle import knx_ref
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+def rel_err(got, want):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    return float(np.max(np.abs(got - want)) / max(1.0, float(np.max(np.abs(want)))))
+
+
+def forward(path, x, mode, monkeypatch, persistent, solo=True):
+    monkeypatch.setenv("KNX_RNN_PERSISTENT", "1" if persistent else "0")
+    monkeypatch.setenv("KNX_RNN_SOLO", "1" if solo else "0")
+    m = Model(path)
+    try:
+        if mode == "i8":
+            m.set_int8_mode(INT8_I8)
+        return m(x).copy()
+    finally:
+        m.close()
+
+
+CASES = [
+    # cell, directions, units, fin, T
+    ("LSTM", 1, 40, 20, 9),
+    ("GRU", 2, 33, 12, 7),
+    ("RNN", 2, 64, 16, 5),
+    ("LSTM", 2, 128, 128, 6),
+    ("GRU", 1, 200, 24, 4),
+    ("LSTM", 1, 3, 5, 1),
+]
+
+
+@pytest.mark.parametrize("case", range(len(CASES)))
+@pytest.mark.parametrize("int8,mode", [(False, "ref"), (True, "ref"), (True, "i8")])
+@pytest.mark.parametrize("batch", [1, 2, 17, 64])
+def test_persistent_matches_per_step_and_oracle(tmp_path, monkeypatch, case, int8, mode, batch):
+    cell, dirs, units, fin, T = CASES[case]
+    p = str(tmp_path / "r.knx")
+    x = configs.lstm(p, seed=case, batch=batch, T=T, fin=fin, units=units, int8=int8, cell=cell, directions=dirs)
+    got = forward(p, x, mode, monkeypatch, True)
+    per_step = forward(p, x, mode, monkeypatch, False)
+    int8_rec = int8 and (mode == "i8" or batch <= 2)
+    if int8_rec:
+        assert np.array_equal(got, per_step), (cell, dirs, units, batch, mode)
+    else:
+        assert rel_err(got, per_step) <= 1e-5, (cell, dirs, units, batch, mode)
+    want, _ = knx_ref.forward(knx_ref.parse(p), x.reshape(-1, fin), mode=mode)
+    assert rel_err(got.reshape(want.shape), want) <= (1e-2 if int8_rec else 1e-4)
+    if batch <= 2:  # the single-workgroup kernel above; the multi-workgroup one at the same shape
+        multi = forward(p, x, mode, monkeypatch, True, solo=False)
+        if int8_rec:
+            assert np.array_equal(multi, got)
+        else:
+            assert rel_err(multi, got) <= 1e-5
+
+
+def test_persistent_returns_sequences_and_nan_rows(tmp_path, monkeypatch):
+    """a sequence-returning bidirectional LSTM (every timestep's state at its own position, the backward direction
+    from t = T-1) feeding a GRU, int8 in i8 mode; a sample holding NaN gives a NaN output row and leaves the others
+    untouched, bit for bit as the per-step path"""
+    from kernix_amd.knxfile import ModelBuilder
+
+    rng = np.random.default_rng(5)
+    T, F, u1, u2 = 8, 10, 24, 16
+    b = ModelBuilder((T, F), int8=True)
+
+    def cell(kind, fin, units):
+        g = {"LSTM": 4, "GRU": 3}[kind] * units
+        return (rng.normal(0, 0.3, (fin, g)), rng.normal(0, 0.3, (units, g)),
+                rng.normal(0, 0.1, 2 * g if kind == "GRU" else g))
+
+    h = b.recurrent(b.input, "LSTM", u1, [cell("LSTM", F, u1), cell("LSTM", F, u1)], return_sequences=True)
+    h = b.recurrent(h, "GRU", u2, [cell("GRU", 2 * u1, u2)], return_sequences=True)
+    p = str(tmp_path / "s.knx")
+    b.save(p)
+    x = rng.normal(0, 1, (5, T, F)).astype(np.float32)
+    x[3, 4, 2] = np.nan
+    got = forward(p, x, "i8", monkeypatch, True)
+    assert np.array_equal(got, forward(p, x, "i8", monkeypatch, False), equal_nan=True)
+    assert np.isnan(got[3]).all() and np.isfinite(np.delete(got, 3, axis=0)).all()
+    want, _ = knx_ref.forward(knx_ref.parse(p), x.reshape(-1, F), mode="i8")
+    ok = np.isfinite(want)
+    assert np.array_equal(np.isnan(got.reshape(want.shape)), ~ok)
+    assert rel_err(got.reshape(want.shape)[ok], want[ok]) <= 1e-2
+
+
+def test_recurrence_entry_point_rejects(monkeypatch):
+    L = hipabi.lib()
+    hipabi.check(L.knx_hip_init())
+    assert L.knx_hip_rnn_recurrence_fits(4, 64, 128, 0) == 1
+    assert L.knx_hip_rnn_recurrence_fits(4, 65, 128, 0) == 0  # more than 64 rows: the per-timestep path
+    assert L.knx_hip_rnn_recurrence_fits(7, 1, 128, 0) == 0
+    assert L.knx_hip_rnn_recurrence_fits(4, 64, 4096, 0) == 0  # h does not fit a workgroup's LDS
+
+
+@pytest.mark.parametrize("batch,expect", [(1, True), (64, True), (65, False)])
+def test_forward_uses_the_persistent_recurrence(tmp_path, monkeypatch, batch, expect):
+    """the forward takes the one-launch recurrence wherever it fits (an injected failure of that entry point fails the
+    forward) and the per-timestep launches otherwise or with KNX_RNN_PERSISTENT=0"""
+    p = str(tmp_path / "l.knx")
+    x = configs.lstm(p, batch=batch, T=4, fin=16, units=32)
+    monkeypatch.setenv("KNX_HIP_FAIL", "knx_hip_rnn_recurrence")
+    m = Model(p)
+    try:
+        if expect:
+            with pytest.raises(RuntimeError):
+                m(x)
+        else:
+            m(x)
+        monkeypatch.setenv("KNX_RNN_PERSISTENT", "0")
+        y = m(x)
+    finally:
+        m.close()
+    want, _ = knx_ref.forward(knx_ref.parse(p), x.reshape(-1, 16))
+    assert rel_err(y, want) <= 1e-4
