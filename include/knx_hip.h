@@ -64,7 +64,9 @@ enum {
 };
 
 /* ---- runtime ---- */
-KNX_API int knx_hip_init(void);              /* selects device 0 once; KNX_ENODEV without a GPU */
+KNX_API int knx_hip_init(void);              /* checks the calling thread's current device; KNX_ENODEV unless gfx950 */
+KNX_API int knx_hip_get_device(int* device); /* the current device of the calling thread */
+KNX_API int knx_hip_set_device(int device);
 KNX_API const char* knx_hip_last_error(void);
 KNX_API int knx_hip_malloc(void** p, size_t bytes);
 KNX_API int knx_hip_free(void* p);

@@ -46,16 +46,19 @@ int check_launch(const char* what)
     return KNX_OK;
 }
 
-static int g_cus = 0;
+constexpr int kMaxDevices = 64;
+static int g_cus[kMaxDevices];  // compute units per device, 0 until queried
 
 int num_cus()
 {
-    if (g_cus == 0) {
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&g_cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-            g_cus = 256;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+    if (g_cus[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1) n = 256;
+        __atomic_store_n(&g_cus[dev], n, __ATOMIC_RELAXED);
     }
-    return g_cus;
+    return g_cus[dev];
 }
 
 unsigned grid_spin_limit()
@@ -71,35 +74,46 @@ unsigned grid_spin_limit()
 
 }  // namespace knx
 
-static std::once_flag g_init_once;
-static int g_init_rc = KNX_ENODEV;
+// The library runs on the device current on the calling thread (one process per GPU selects it with
+// HIP_VISIBLE_DEVICES or hipSetDevice); each device is checked once for gfx950.
+static std::mutex g_dev_mu;
+static int g_dev_state[knx::kMaxDevices];  // 0 unchecked, 1 gfx950, -1 another architecture
 
 extern "C" int knx_hip_init(void)
 {
     KNX_ENTRY("knx_hip_init");
-    std::call_once(g_init_once, [] {
-        int n = 0;
-        if (hipGetDeviceCount(&n) != hipSuccess || n < 1) {
-            g_init_rc = knx::fail(KNX_ENODEV, "knx_hip_init: no HIP device");
-            return;
-        }
+    int n = 0, cur = -1;
+    if (hipGetDevice(&cur) == hipSuccess && cur >= 0 && cur < knx::kMaxDevices &&
+        __atomic_load_n(&g_dev_state[cur], __ATOMIC_ACQUIRE) > 0)
+        return KNX_OK;  // checked before
+    if (hipGetDeviceCount(&n) != hipSuccess || n < 1) return knx::fail(KNX_ENODEV, "knx_hip_init: no HIP device");
+    if (hipGetDevice(&cur) != hipSuccess || cur < 0 || cur >= knx::kMaxDevices)
+        return knx::fail(KNX_ENODEV, "knx_hip_init: no current device");
+    std::lock_guard<std::mutex> lock(g_dev_mu);
+    if (g_dev_state[cur] == 0) {
         hipDeviceProp_t prop;
-        if (hipGetDeviceProperties(&prop, 0) != hipSuccess) {
-            g_init_rc = knx::fail(KNX_ENODEV, "knx_hip_init: cannot query device 0");
-            return;
-        }
-        if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
-            g_init_rc = knx::fail(KNX_ENODEV, "knx_hip_init: device 0 is %s, this library is built for gfx950", prop.gcnArchName);
-            return;
-        }
-        g_init_rc = KNX_OK;
-    });
-    if (g_init_rc != KNX_OK) return g_init_rc;
-    int cur = -1;
-    if (hipGetDevice(&cur) != hipSuccess || cur != 0) {
-        if (hipSetDevice(0) != hipSuccess) return knx::fail(KNX_EHIP, "knx_hip_init: hipSetDevice(0) failed");
+        if (hipGetDeviceProperties(&prop, cur) != hipSuccess)
+            return knx::fail(KNX_ENODEV, "knx_hip_init: cannot query device %d", cur);
+        __atomic_store_n(&g_dev_state[cur], strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : -1, __ATOMIC_RELEASE);
+        if (g_dev_state[cur] < 0)
+            return knx::fail(KNX_ENODEV, "knx_hip_init: device %d is %s, this library is built for gfx950", cur,
+                             prop.gcnArchName);
     }
-    return KNX_OK;
+    return g_dev_state[cur] > 0 ? KNX_OK : knx::fail(KNX_ENODEV, "knx_hip_init: device %d is not gfx950", cur);
+}
+
+extern "C" int knx_hip_get_device(int* device)
+{
+    KNX_REQUIRE(device != nullptr, "knx_hip_get_device");
+    return hipGetDevice(device) == hipSuccess ? KNX_OK : knx::fail(KNX_EHIP, "knx_hip_get_device failed");
+}
+
+extern "C" int knx_hip_set_device(int device)
+{
+    const hipError_t e = hipSetDevice(device);
+    if (e == hipSuccess) return KNX_OK;
+    (void)hipGetLastError();  // a failed call leaves its error for the next launch check: clear it
+    return knx::fail(KNX_EHIP, "knx_hip_set_device(%d): %s", device, hipGetErrorString(e));
 }
 
 extern "C" const char* knx_hip_last_error(void) { return knx::g_err; }
@@ -111,7 +125,11 @@ extern "C" int knx_hip_malloc(void** p, size_t bytes)
     *p = nullptr;
     if (bytes == 0) bytes = 256;  // non-NULL handle for empty tensors
     const hipError_t e = hipMalloc(p, bytes);
-    if (e != hipSuccess) { *p = nullptr; return knx::fail(KNX_EHIP, "knx_hip_malloc(%zu): %s", bytes, hipGetErrorString(e)); }
+    if (e != hipSuccess) {
+        *p = nullptr;
+        (void)hipGetLastError();  // not left for the next launch check
+        return knx::fail(KNX_EHIP, "knx_hip_malloc(%zu): %s", bytes, hipGetErrorString(e));
+    }
     return KNX_OK;
 }
 
@@ -129,7 +147,11 @@ extern "C" int knx_hip_host_malloc(void** p, size_t bytes)
     *p = nullptr;
     if (bytes == 0) bytes = 256;
     const hipError_t e = hipHostMalloc(p, bytes, hipHostMallocDefault);
-    if (e != hipSuccess) { *p = nullptr; return knx::fail(KNX_EHIP, "knx_hip_host_malloc(%zu): %s", bytes, hipGetErrorString(e)); }
+    if (e != hipSuccess) {
+        *p = nullptr;
+        (void)hipGetLastError();
+        return knx::fail(KNX_EHIP, "knx_hip_host_malloc(%zu): %s", bytes, hipGetErrorString(e));
+    }
     return KNX_OK;
 }
 

@@ -183,6 +183,7 @@ static int ensure_device(kernix_model* m)
     if (m->dev == NULL) {
         m->dev = calloc(1, sizeof *m->dev);
         if (m->dev == NULL) return -1;
+        if (hip_ok(knx_hip_get_device(&m->dev->device), "device query") != 0) return -1;
         if (hip_ok(knx_hip_stream_create(&m->dev->stream), "stream creation") != 0 ||
             hip_ok(knx_hip_event_create_ordering(&m->dev->done), "event creation") != 0 ||
             hip_ok(knx_hip_host_malloc((void**)&m->dev->chain_status, sizeof(int)), "status word allocation") != 0)
@@ -383,8 +384,37 @@ static void free_out_all(kernix_model* m)
     if (m->dev) m->dev->out_all_pinned = 0;
 }
 
+/* Every call on a model runs on the model's device (the one current at its first forward), whatever device the
+ * calling thread has current; the thread's own device is restored on return.  prev: the device to restore, or -1. */
+static int enter_device(const kernix_model* m, int* prev)
+{
+    *prev = -1;
+    int cur = -1;
+    if (m == NULL || m->dev == NULL) return 0;
+    if (knx_hip_get_device(&cur) != KNX_OK) return -1;
+    if (cur == m->dev->device) return 0;
+    if (knx_hip_set_device(m->dev->device) != KNX_OK) return -1;
+    *prev = cur;
+    return 0;
+}
+
+static void leave_device(int prev)
+{
+    if (prev >= 0) knx_hip_set_device(prev);
+}
+
+static void release_ws(kernix_model* m);
+
 /* Releases the workspace (arena, views, host output buffers); weights stay on the device. */
 void knx_model_release_device_ws(kernix_model* m)
+{
+    int prev;
+    if (m == NULL || enter_device(m, &prev) != 0) return;
+    release_ws(m);
+    leave_device(prev);
+}
+
+static void release_ws(kernix_model* m)
 {
     if (m == NULL) return;
     m->batch = -1;
@@ -408,8 +438,9 @@ void knx_model_release_device_ws(kernix_model* m)
 
 void knx_model_release_device_all(kernix_model* m)
 {
-    if (m == NULL) return;
-    knx_model_release_device_ws(m);
+    int prev;
+    if (m == NULL || enter_device(m, &prev) != 0) return;
+    release_ws(m);
     for (int i = 0; m->steps != NULL && i < m->n_steps; i++) free_dstep(&m->steps[i]);
     if (m->dev != NULL) {
         knx_hip_stream_destroy(m->dev->stream);
@@ -428,6 +459,7 @@ void knx_model_release_device_all(kernix_model* m)
         free(m->dev);
         m->dev = NULL;
     }
+    leave_device(prev);
 }
 
 void kernix_model_trim(kernix_model* m) { knx_model_release_device_ws(m); }
@@ -435,7 +467,7 @@ void kernix_model_trim(kernix_model* m) { knx_model_release_device_ws(m); }
 /* Allocates the workspace for chunks of `rows` input rows (the old one is released first). */
 static int alloc_ws(kernix_model* m, int rows)
 {
-    knx_model_release_device_ws(m);
+    release_ws(m);
     const size_t B = (size_t)rows / (size_t)m->seq_len;
     ws_ctx c = { WS_SIZE, 0, NULL, 0 };
     if (ws_walk(m, B, &c) != 0) return -1;
@@ -1267,17 +1299,32 @@ static const float_tensor* forward_host(kernix_model* m, const float_tensor* x)
  * is recomputed in the same call: the whole forward again, every Linear its own launch. */
 const float_tensor* kernix_model_forward(kernix_model* m, const float_tensor* x)
 {
+    int prev;
+    if (enter_device(m, &prev) != 0) return NULL;
     const float_tensor* y = forward_host(m, x);
-    if (y == NULL || !__atomic_exchange_n(m->dev->chain_status, 0, __ATOMIC_SEQ_CST)) return y;
-    KNX_LOG("KERNIX: a Linear chain's workgroups were not all resident; forward recomputed one launch per layer\n");
-    m->dev->no_chain = 1;
-    y = forward_host(m, x);
-    m->dev->no_chain = 0;
-    if (y != NULL && __atomic_exchange_n(m->dev->chain_status, 0, __ATOMIC_SEQ_CST)) return NULL; /* cannot happen */
+    if (y != NULL && __atomic_exchange_n(m->dev->chain_status, 0, __ATOMIC_SEQ_CST)) {
+        KNX_LOG("KERNIX: a Linear chain's workgroups were not all resident; forward recomputed one launch per layer\n");
+        m->dev->no_chain = 1;
+        y = forward_host(m, x);
+        m->dev->no_chain = 0;
+        if (y != NULL && __atomic_exchange_n(m->dev->chain_status, 0, __ATOMIC_SEQ_CST)) y = NULL; /* cannot happen */
+    }
+    leave_device(prev);
     return y;
 }
 
+static int forward_device(kernix_model* m, const float* d_x, int rows, float* d_out, void* stream);
+
 int kernix_model_forward_device(kernix_model* m, const float* d_x, int rows, float* d_out, void* stream)
+{
+    int prev;
+    if (enter_device(m, &prev) != 0) return -1;
+    const int rc = forward_device(m, d_x, rows, d_out, stream);
+    leave_device(prev);
+    return rc;
+}
+
+static int forward_device(kernix_model* m, const float* d_x, int rows, float* d_out, void* stream)
 {
     if (m == NULL || d_x == NULL || d_out == NULL || rows < 0 || rows % m->seq_len != 0) return -1;
     const int samples = rows / m->seq_len;
@@ -1298,12 +1345,17 @@ int kernix_model_forward_device(kernix_model* m, const float* d_x, int rows, flo
 int kernix_model_device_status(kernix_model* m)
 {
     if (m == NULL || m->dev == NULL || m->dev->chain_status == NULL) return 0;
+    int prev;
+    if (enter_device(m, &prev) != 0) return -1;
     struct knx_dmodel* d = m->dev;
+    int rc = 0;
     if (d->have_last) {
-        const int rc = d->done_recorded ? knx_hip_event_sync(d->done) : knx_hip_stream_sync(d->last_stream);
-        if (hip_ok(rc, "device forward")) return -1;
+        const int e = d->done_recorded ? knx_hip_event_sync(d->done) : knx_hip_stream_sync(d->last_stream);
+        if (hip_ok(e, "device forward")) rc = -1;
     }
-    return __atomic_exchange_n(d->chain_status, 0, __ATOMIC_SEQ_CST) ? -1 : 0;
+    if (__atomic_exchange_n(d->chain_status, 0, __ATOMIC_SEQ_CST)) rc = -1;
+    leave_device(prev);
+    return rc;
 }
 
 /* ---------------------------------------------------------------- kernel-level int8 contract

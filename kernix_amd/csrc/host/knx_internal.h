@@ -43,6 +43,7 @@ struct knx_dstep {
 #define KNX_RING_SLOTS 4 /* pinned staging buffers of a host-buffer forward's input copies */
 
 struct knx_dmodel {
+    int device;       /* the device current at the model's first forward: every later call runs on it */
     void* stream;     /* hipStream_t owned by the model */
     int uploaded;     /* weights on the device */
     void* arena;      /* workspace: storage buffers, step scratch, dequantized copies, input staging */

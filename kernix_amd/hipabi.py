@@ -26,6 +26,8 @@ class ChainLayer(ctypes.Structure):
 
 SIGS = {
     "knx_hip_init": ([], I),
+    "knx_hip_get_device": ([ctypes.POINTER(ctypes.c_int)], I),
+    "knx_hip_set_device": ([I], I),
     "knx_hip_host_malloc": ([ctypes.POINTER(ctypes.c_void_p), Z], I),
     "knx_hip_host_free": ([P], I),
     "knx_hip_last_error": ([], ctypes.c_char_p),

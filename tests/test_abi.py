@@ -101,3 +101,26 @@ print("recovered", bool(np.array_equal(m(x), good)))
     r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300)
     assert "raised" in r.stdout and "recovered True" in r.stdout, r.stdout + r.stderr
     assert "injected failure" in r.stderr
+
+
+@pytest.mark.gpu
+def test_runs_on_the_current_device(tmp_path):
+    """the library checks and uses the calling thread's current device (one process per GPU selects it), and a model
+    keeps running on the device current at its first forward; a device that does not exist is an error"""
+    import ctypes as C
+
+    L = hipabi.lib()
+    hipabi.check(L.knx_hip_init())
+    d = C.c_int(-1)
+    hipabi.check(L.knx_hip_get_device(C.byref(d)))
+    assert d.value >= 0
+    assert L.knx_hip_set_device(d.value) == 0
+    assert L.knx_hip_set_device(1 << 20) == -2  # KNX_EHIP
+    from kernix_amd.kernix import Model
+
+    p = str(tmp_path / "m.knx")
+    x = configs.int8_mlp(p, batch=3)
+    m = Model(p)
+    y = m(x).copy()
+    assert np.array_equal(m(x), y)
+    m.close()
