@@ -265,10 +265,10 @@ struct SmallConvArgs {
 
 __device__ float conv_zero_word = 0.0f;  // what the gather reads for padding: never written
 
-template <int NB, bool RES>
+template <int NB, bool RES, int KP = SMALL_K / 2>  // KP: the k pairs multiplied (⌈K/2⌉ ≤ KP ≤ 16)
 __global__ void __launch_bounds__(256) conv_small(SmallConvArgs a)
 {
-    constexpr int KP = SMALL_K / 2, CO = 32 * NB;
+    constexpr int CO = 32 * NB;
     __shared__ float wl[SMALL_K * CO];  // the weights, [k][co]: staged once per workgroup with coalesced loads
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int rl = lane & 31, g = lane >> 5;
@@ -307,15 +307,15 @@ __global__ void __launch_bounds__(256) conv_small(SmallConvArgs a)
             av[p] = *(in ? px + off[p] : &conv_zero_word);
         }
     };
-    // multiply the gathered group at m0 and write it
-    auto group = [&](long long m0, const float (&av)[KP]) {
+    // multiply the gathered group at m0 and write it (full: the whole group is inside M, known at the call site)
+    auto group = [&](long long m0, const float (&av)[KP], bool full) {
         v16f acc[NB];
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[nb][e] = 0.0f;
 #pragma unroll
-        for (int p = 0; p < KP; ++p)  // all 16 pairs: pairs past K multiply zeros (no branch between the MFMAs)
+        for (int p = 0; p < KP; ++p)  // every pair up to KP: pairs past K multiply zeros (no branch between the MFMAs)
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb)  // B fragment: weight (k = 2p + g, channel 32·nb + rl) from LDS
                 acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[p], wl[(2 * p + g) * CO + 32 * nb + rl], acc[nb], 0, 0, 0);
@@ -348,7 +348,7 @@ __global__ void __launch_bounds__(256) conv_small(SmallConvArgs a)
                     if (all || row < left) yl[row * CO + 32 * nb] = v;
                 }
         };
-        if (m0 + 32 <= a.M) write(true);  // m0 is the same in every lane: a scalar branch
+        if (full) write(true);
         else write(false);
     };
     // Each wave takes the groups of 32 pixels m0, m0 + step, …; the next group's inputs are in flight while one
@@ -359,11 +359,11 @@ __global__ void __launch_bounds__(256) conv_small(SmallConvArgs a)
     gather(m0, av0);
     while (m0 < a.M) {
         gather(m0 + step, av1);
-        group(m0, av0);
+        group(m0, av0, m0 + 32 <= a.M);  // m0 is the same in every lane: a scalar branch
         m0 += step;
         if (m0 >= a.M) break;
         gather(m0 + step, av0);
-        group(m0, av1);
+        group(m0, av1, m0 + 32 <= a.M);
         m0 += step;
     }
 }
@@ -399,6 +399,13 @@ int conv_small_entry(const knx_conv_geom* g, const float* x, const float* w, boo
     if (env != nullptr && env[0] == 'g') per_cu = std::max(1L, strtol(env + 1, nullptr, 10));
     const long blocks = std::min<long>((groups32 + 3) / 4, per_cu * knx::num_cus());
     const dim3 grid((unsigned)blocks);
+    // K = 27 (3×3 over RGB): 14 k pairs instead of 16
+    const bool k14 = K <= 28 && (env == nullptr || strcmp(env, "k16") != 0);
+    if (k14 && g->Co == 64) {
+        if (R) hipLaunchKernelGGL((conv_small<2, true, 14>), grid, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((conv_small<2, false, 14>), grid, dim3(256), 0, s, a);
+        return knx::check_launch(name);
+    }
     switch (g->Co / 32 * 2 + (R != nullptr)) {
     case 2: hipLaunchKernelGGL((conv_small<1, false>), grid, dim3(256), 0, s, a); break;
     case 3: hipLaunchKernelGGL((conv_small<1, true>), grid, dim3(256), 0, s, a); break;
