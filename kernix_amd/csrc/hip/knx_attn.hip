@@ -70,7 +70,7 @@ __device__ __attribute__((aligned(16))) float knx_attn_zero[4];
 //      one quarter-wave reads at one logical chunk fall on 16 distinct 16-byte bank groups;
 //   V: chunk position vrow(r)·CPR + (c ^ sv(r)), sv(r) = 8·((r/4) mod 2) (CPR ≥ 16) or 0, vrow(r) = r ^ ((r/4) mod
 //      2) (CPR = 8) or r: the two half-waves read rows 4 apart, which then occupy disjoint halves of the banks.
-template <int NS, int DK, int DV>
+template <int NS, int DK, int DV, int DEPTH = 2 * NS>  // DEPTH: staging tiles in flight before the first product
 __global__ void __launch_bounds__(256) attention_fused(const float* __restrict__ Q, int ldq, const float* __restrict__ K,
                                                        int ldk, const float* __restrict__ V, int ldv,
                                                        float* __restrict__ ctx, int H, int Rq, int S, float scale,
@@ -112,10 +112,12 @@ __global__ void __launch_bounds__(256) attention_fused(const float* __restrict__
             dma16_at(src, (isv ? vs : ks) + (size_t)p0 * 4);
         }
     };
+    // tile i of the staging order: K tile i (i < NS), then V tile i − NS; DEPTH of them issued up front, then one
+    // more each time a K tile has been consumed, the rest after the last K tile
+    static_assert(DEPTH >= 1 && DEPTH <= 2 * NS, "staging depth");
+    auto stage_tile = [&](int i) { stage(i >= NS, i >= NS ? i - NS : i); };
 #pragma unroll
-    for (int t = 0; t < NS; ++t) stage(false, t);
-#pragma unroll
-    for (int t = 0; t < NS; ++t) stage(true, t);
+    for (int i = 0; i < DEPTH; ++i) stage_tile(i);
 
     // K fragment of group g: row 32t + col, logical chunk 2g + hf (byte offset within the tile)
     int kb[DK / 8];
@@ -126,9 +128,14 @@ __global__ void __launch_bounds__(256) attention_fused(const float* __restrict__
         constexpr int t = decltype(tc)::value;
 #pragma unroll
         for (int e = 0; e < 16; ++e) sc[t][e] = 0.0f;
-        // tiles t + 1 .. NS − 1 of K and all of V may stay in flight
-        KNX_WAIT_VM_LDS((NS - 1 - t) * PW + NS * PW);
+        // the tiles issued after tile t may stay in flight (DEPTH + t issued so far, at most all 2·NS)
+        constexpr int issued = DEPTH + t < 2 * NS ? DEPTH + t : 2 * NS;
+        KNX_WAIT_VM_LDS((issued - t - 1) * PW);
         knx_barrier_nofence();
+        if (DEPTH + t < 2 * NS) stage_tile(DEPTH + t);  // its LDS region is its own: no wait needed
+        if (t == NS - 1)
+#pragma unroll
+            for (int i = DEPTH + NS; i < 2 * NS; ++i) stage_tile(i);  // the V tiles not issued yet
         const int8_t* kt = reinterpret_cast<const int8_t*>(ks) + t * TILE * 16;
 #pragma unroll
         for (int g = 0; g < DK / 8; ++g) {
@@ -226,12 +233,28 @@ struct AttnArgs {
     int causal;
 };
 
+template <int NS, int D, int DEPTH>
+int launch_fused_d(const AttnArgs& a, hipStream_t s, const char* name)
+{
+    constexpr int DP = DEPTH < 2 * NS ? DEPTH : 2 * NS;
+    hipLaunchKernelGGL((attention_fused<NS, D, D, DP>), dim3((a.Rq + 127) / 128, a.B * a.H), dim3(256), 0, s, a.Q, a.ldq,
+                       a.K, a.ldk, a.V, a.ldv, a.ctx, a.H, a.Rq, a.S, a.scale, a.causal);
+    return knx::check_launch(name);
+}
+
 template <int NS, int D>
 int launch_fused(const AttnArgs& a, hipStream_t s, const char* name)
 {
-    hipLaunchKernelGGL((attention_fused<NS, D, D>), dim3((a.Rq + 127) / 128, a.B * a.H), dim3(256), 0, s, a.Q, a.ldq, a.K,
-                       a.ldk, a.V, a.ldv, a.ctx, a.H, a.Rq, a.S, a.scale, a.causal);
-    return knx::check_launch(name);
+    // three 32-key tiles in flight up front, one more per consumed K tile: with all of K and V requested at once by
+    // every workgroup (64 KB each at S = 128, d = 64) a workgroup's first tile arrives anywhere in the 32 MB stream
+    // (B 64, H 8, S 128, d 64: 26.5 µs at depth 3, 26.7 at 2 and 4, 27.3 at 6, 27.8 with everything up front)
+    const char* dep = getenv("KNX_ATTN_DEPTH");  // tuning and tests: 2, 4, 6, or "all"
+    if (dep != nullptr && strcmp(dep, "all") == 0) return launch_fused_d<NS, D, 2 * NS>(a, s, name);
+    const int d = dep != nullptr ? atoi(dep) : 3;
+    if (d == 2) return launch_fused_d<NS, D, 2>(a, s, name);
+    if (d == 4) return launch_fused_d<NS, D, 4>(a, s, name);
+    if (d == 6) return launch_fused_d<NS, D, 6>(a, s, name);
+    return launch_fused_d<NS, D, 3>(a, s, name);
 }
 
 // the fused kernel when dk = dv ∈ {32, 64, 128}, S fits its LDS tiles and every row is 16-byte aligned; 1 = not eligible

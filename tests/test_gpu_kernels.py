@@ -649,10 +649,15 @@ ATTN_SHAPES = [(2, 2, 5, 5, 4, 4, 1), (2, 8, 128, 128, 64, 64, 0), (1, 3, 7, 9, 
 
 
 @pytest.mark.parametrize("B,H,Rq,S,dk,dv,causal", ATTN_SHAPES)
-@pytest.mark.parametrize("mode", ["fused", "unfused", "unfused_vt"])
+@pytest.mark.parametrize("mode", ["fused", "fused_d2", "fused_all", "unfused", "unfused_vt"])
 def test_attention_core(L, B, H, Rq, S, dk, dv, causal, mode, monkeypatch):
-    if mode != "fused":
+    """fused: K and V staged three 32-key tiles ahead (the default), fused_d2 / fused_all: two ahead / all up front"""
+    if mode.startswith("unfused"):
         monkeypatch.setenv("KNX_ATTN_KERNEL", "unfused")
+    if mode == "fused_d2":
+        monkeypatch.setenv("KNX_ATTN_DEPTH", "2")
+    if mode == "fused_all":
+        monkeypatch.setenv("KNX_ATTN_DEPTH", "all")
     vt = mode == "unfused_vt"
     rng = np.random.default_rng(B + H + Rq + S)
     Q = rng.standard_normal((B * Rq, H * dk)).astype(np.float32)
