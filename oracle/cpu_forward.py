@@ -7,7 +7,8 @@ int8 LINEAR weights as the reference dispatches them (the int8 kernel at <= 2 ro
 the dequantized fp32 copy above, :1616-1622), activations as a pass over the rows (:468-541), convolution as im2col
 tiles and the native GEMM (:677-771), layer_norm and softmax row by row (include/kernix.h:652-677), attention as the
 three projections, the per-(batch, head) scores / softmax / context loop and the output projection (:1005-1048),
-broadcasting binaries and global pooling (:810-906).  Only the op kinds of the benchmark models are covered;
+broadcasting binaries and global pooling (:810-906), recurrent layers as the input-projection GEMM and the
+per-timestep h·U and gates (:563-648).  Only the op kinds of the benchmark models are covered;
 anything else raises.  Accuracy is the reference's, not the oracle's float64: this is a baseline to time, not a
 checker.
 """
@@ -101,6 +102,9 @@ class CpuModel:
                 y = np.empty((B * R, C), np.float32)
                 L.ko_binary(op["op"], _p(a), ra, sa[-1], _p(b), rb, sb[-1], _p(y), B, R, C)
                 s = (sa if ra * sa[-1] >= rb * sb[-1] else sb)[:-1] + (C,)
+            elif k in (4, 5, 6):  # LSTM / GRU / RNN: the input projection and the fp32 recurrence on the native
+                # GEMM, int8 recurrences at <= 2 rows on the int8 kernel, the gates in float32 (include/kernix_model.h:563-648)
+                y, s = knx_ref._rnn(op, a, sa, B, "ref", dense=lambda x, w, b: _dense(x, w, b))
             elif k == 17:  # ATTENTION
                 y, s = self._attention(op, vals, shapes, B)
             else:

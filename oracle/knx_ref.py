@@ -478,7 +478,10 @@ def _attention(op, vals, shapes, B):
     return dense64(ctx, wo, bo), s
 
 
-def _rnn(op, a, sa, B, mode):
+def _rnn(op, a, sa, B, mode, dense=None):
+    """dense: the product x·W + b used for the input projection and the fp32 recurrence (default: float64
+    accumulation, the oracle; the CPU baseline passes the reference's fp32 native GEMM)"""
+    dense64_ = dense if dense is not None else dense64
     kind, u = op["kind"], op["u"]
     T, cin = sa[0], sa[1]
     G = {4: 4, 5: 3, 6: 1}[kind]
@@ -486,7 +489,9 @@ def _rnn(op, a, sa, B, mode):
     sig = lambda z: act(z, 3)  # noqa: E731
 
     def run_dir(W, U, bias, backward):
-        zx = dense64(a, W, bias[:gu]).reshape(B, T, gu)
+        zx = dense64_(a, W, bias[:gu]).reshape(B, T, gu)
+        # the fp32 recurrent weight (an int8 one dequantized once, as the reference's workspace keeps it)
+        Uf = U[1] if U[0] == "f32" else (U[1].astype(np.float32) * U[2][None, :]).astype(np.float32)
         brec = bias[gu:] if kind == 5 else None
         h = np.zeros((B, u), np.float32)
         c = np.zeros((B, u), np.float32)
@@ -503,8 +508,7 @@ def _rnn(op, a, sa, B, mode):
                     z = qmatmul(h, U[1], U[2], None, y_old=z)
                     rec = None
             else:
-                Uf = U[1] if U[0] == "f32" else (U[1].astype(np.float32) * U[2][None, :]).astype(np.float32)
-                rec = dense64(h, Uf, brec)
+                rec = dense64_(h, Uf, brec)
             if kind == 4:
                 if rec is not None:
                     z = (z + rec).astype(np.float32)
