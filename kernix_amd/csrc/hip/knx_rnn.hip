@@ -6,11 +6,13 @@
 // timestep for the product and another for the cell, a small batch is all launch latency; here one grid does every
 // timestep: workgroup w owns units [w·uw, (w+1)·uw), keeps the U columns of those units' gates in LDS for the whole
 // sequence and its cells' c in registers, and per timestep
-//   1. loads h_{t−1} (all B rows, written by every workgroup at t−1) into LDS — int8: quantizes each row there with
-//      the quantizer's operations (s = max|h|/127, 1 for an all-zero row, NaN for a row holding NaN or ±inf;
-//      q = clamp(rint(h·(1/s)), ±127)), as knx_hip_quantize_rows;
-//   2. forms its gate columns of h_{t−1}·U: fp32 dot products, or exact int32 sums of int8 products dequantized as the
-//      int8 GEMM's epilogue, ((float)acc·s)·scale (+ the GRU's recurrent bias);
+//   1. loads h_{t−1} (all B rows, written by every workgroup at t−1) into LDS, a row's float4s over a group of
+//      lanes — int8: quantizes each row from those registers with the quantizer's operations (s = max|h|/127, 1 for
+//      an all-zero row, NaN for a row holding NaN or ±inf; q = clamp(rint(h·(1/s)), ±127)), as
+//      knx_hip_quantize_rows;
+//   2. forms its gate columns of h_{t−1}·U on the matrix cores in 16 × 16 tiles: v_mfma_f32_16x16x4f32, or exact
+//      int32 sums from v_mfma_i32_16x16x64_i8 dequantized as the int8 GEMM's epilogue, ((float)acc·s)·scale (+ the
+//      GRU's recurrent bias);
 //   3. applies the cells (knx_lstm_cell / knx_gru_cell, the same functions as knx_hip_rnn_gates) to its (row, unit)
 //      pairs, writes h_t (at device scope, for the other workgroups) and the output;
 //   4. waits at a grid barrier (knx_grid.hpp: one 64-bit word, every barrier adds 256; at most 64 workgroups, all
@@ -31,12 +33,16 @@ constexpr int kThreads = 256, kWaves = 4;
 constexpr int kMaxPairs = 2;             // (row, unit) pairs per thread in the cell phase: B·uw ≤ 512
 constexpr int kMaxGrid = 64;
 constexpr int kLoads = 8;                // float4 loads of h in flight per thread
+constexpr int kMaxUnits = 2048;          // the multi-workgroup kernel: a row of h is at most kLoads float4s per lane
 constexpr size_t kMaxLds = 120 * 1024;
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef int v4i __attribute__((ext_vector_type(4)));
 
 struct RnnArgs {
     int kind, act;
     float alpha;
-    int B, T, u, gu, gates, dir, ret_seq, stride, uw, up;
+    int B, T, u, gu, gates, dir, ret_seq, stride, uw, up, ldh;
     const float* zx;      // B·T × gu (row b·T + t), the input projection with its bias
     const float* U;       // fp32 recurrent weight: u × gu (u_nt = 0) or gu × u (u_nt = 1)
     int u_nt;
@@ -44,7 +50,7 @@ struct RnnArgs {
     int kp;
     const float* qs;      // its gu scales
     const float* brec;    // GRU recurrent bias (gu), or null
-    float* h0;            // hidden states of even / odd timesteps (B × u each)
+    float* h0;            // hidden states of even / odd timesteps (B rows of ldh floats each)
     float* h1;
     float* dst;
     knx::GridSync gs;
@@ -52,29 +58,38 @@ struct RnnArgs {
 
 __host__ __device__ inline size_t round16(size_t b) { return (b + 15) / 16 * 16; }
 
-// Dot products of a timestep: each thread sums CB adjacent gate columns of one row over a slice of K (P consecutive
-// lanes split K, their partial sums reduced by lane exchanges), so a row value read from LDS serves CB products.
-constexpr int CB = 4;
+// Row pitch (4-byte words) of the LDS matrices that the MFMAs read: ≥ n and ≡ 4 (mod 32), so that the rows that 8
+// consecutive lanes read 16 bytes of at the same k start 4 banks apart.
+__host__ __device__ inline int mfma_pitch(int n) { return (n + 31) / 32 * 32 + 4; }
 
-// LDS layout (bytes): weight slice [ncp][upp] (fp32: upp = up + 1 floats; int8: upp = up/4 + 1 words), rows of h
-// [B][upp] fp32, int8 rows [B][up/4 + 1] words and their scales [B] (int8 only), recurrent terms [B][gates·uw].
-// The odd row pitches put the rows that one wave reads at the same k on different banks.  ncp: the workgroup's gate
-// columns rounded up to CB (the extra columns are zero).
+// k extent of the products: fp32 in 16-wide chunks (four v_mfma_f32_16x16x4f32, lane quarter q taking k = 4q…4q+3 of
+// each chunk), int8 in 64-wide chunks (one v_mfma_i32_16x16x64_i8, lane quarter q taking bytes 16q…16q+15); h and U
+// are zero past u
+__host__ __device__ inline int k_extent(int u, bool i8) { return i8 ? (u + 63) / 64 * 64 : (u + 15) / 16 * 16; }
+
+// LDS layout (bytes): weight slice [ncp][upp] (fp32 values or int8 words, k contiguous), column scales and biases
+// [ncp] each, h_{t−1} [b16][hp] fp32 (not for the int8 LSTM / RNN, whose cells do not read it), its int8 rows
+// [b16][hwp] words and their scales [b16] (int8), the K-split partial tiles [kWaves][256], recurrent terms
+// [B][gates·uw].  ncp: the workgroup's gate columns rounded up to 16, b16: B rounded up to 16 (zero columns and rows).
 struct Lds {
-    size_t us, hs, hq, sx, r, total;
-    int upp, hwp, ncp;
+    size_t us, cs, hs, hq, sx, pt, r, total;
+    int upp, hp, hwp, ncp, b16;
 };
-__host__ __device__ inline Lds lds_layout(int B, int gates, int uw, int up, bool i8)
+__host__ __device__ inline Lds lds_layout(int B, int gates, int uw, int up, bool i8, bool h32)
 {
     Lds l;
-    l.ncp = (gates * uw + CB - 1) / CB * CB;
-    l.upp = i8 ? up / 4 + 1 : up + 1;
-    l.hwp = up / 4 + 1;
+    l.ncp = (gates * uw + 15) / 16 * 16;
+    l.b16 = (B + 15) / 16 * 16;
+    l.upp = mfma_pitch(i8 ? up / 4 : up);
+    l.hp = mfma_pitch(up);
+    l.hwp = mfma_pitch(up / 4);
     l.us = 0;
-    l.hs = round16((size_t)l.ncp * l.upp * 4);
-    l.hq = l.hs + round16((size_t)B * (up + 1) * 4);
-    l.sx = l.hq + (i8 ? round16((size_t)B * l.hwp * 4) : 0);
-    l.r = l.sx + (i8 ? round16((size_t)B * 4) : 0);
+    l.cs = round16((size_t)l.ncp * l.upp * 4);
+    l.hs = l.cs + round16((size_t)l.ncp * 2 * 4);
+    l.hq = l.hs + (h32 ? round16((size_t)l.b16 * l.hp * 4) : 0);
+    l.sx = l.hq + (i8 ? round16((size_t)l.b16 * l.hwp * 4) : 0);
+    l.pt = l.sx + (i8 ? round16((size_t)l.b16 * 4) : 0);
+    l.r = l.pt + (size_t)kWaves * 256 * 4;
     l.total = l.r + round16((size_t)B * gates * uw * 4);
     return l;
 }
@@ -85,26 +100,47 @@ __device__ __forceinline__ float mag(float v)
     return a <= FLT_MAX ? a : INFINITY;
 }
 
+// unsigned maximum over aligned groups of n lanes (n a power of two ≤ 64, uniform; every lane active): row-local
+// DPP for groups up to 16, lane exchanges above
+__device__ __forceinline__ unsigned lane_group_max(unsigned v, int n)
+{
+    if (n > 1) v = max(v, (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));  // quad [1,0,3,2]
+    if (n > 2) v = max(v, (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));  // quad [2,3,0,1]
+    if (n > 4) v = max(v, (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false)); // half-row mirror
+    if (n > 8) v = max(v, (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false)); // row mirror
+    if (n > 16) v = max(v, (unsigned)__shfl_xor((int)v, 16, 64));
+    if (n > 32) v = max(v, (unsigned)__shfl_xor((int)v, 32, 64));
+    return v;
+}
+
+template <bool I8>
 __global__ void __launch_bounds__(kThreads) rnn_recurrence(RnnArgs a)
 {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-    const bool i8 = a.q != nullptr;
+    constexpr bool i8 = I8;  // a.q != nullptr
+    const bool h32 = !i8 || a.kind == 5;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int B = a.B, T = a.T, u = a.u, up = a.up, gu = a.gu, G = a.gates;
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);  // the same value, known to the compiler as uniform
+    const int B = a.B, T = a.T, u = a.u, up = a.up, gu = a.gu, G = a.gates, ldh = a.ldh;
     const int j0 = blockIdx.x * a.uw;
     const int nwu = min(a.uw, u - j0);  // ≥ 1: the grid has ⌈u / uw⌉ workgroups
     const int NC = G * nwu, NCM = G * a.uw;
-    const Lds L = lds_layout(B, G, a.uw, up, i8);
-    const int upp = L.upp, hp = up + 1, hwp = L.hwp, ncp = L.ncp;
+    const Lds L = lds_layout(B, G, a.uw, up, i8, h32);
+    const int upp = L.upp, hp = L.hp, hwp = L.hwp, ncp = L.ncp;
     float* usf = reinterpret_cast<float*>(smem + L.us);
     int* usw = reinterpret_cast<int*>(smem + L.us);
+    float* csc = reinterpret_cast<float*>(smem + L.cs);  // per local column: int8 scale, recurrent bias
+    float* cbi = csc + ncp;
     float* hs = reinterpret_cast<float*>(smem + L.hs);
     int* hqw = reinterpret_cast<int*>(smem + L.hq);
     float* sxs = reinterpret_cast<float*>(smem + L.sx);
+    int* pt = reinterpret_cast<int*>(smem + L.pt);
     float* r = reinterpret_cast<float*>(smem + L.r);
     auto column = [&](int cc) { return (cc / nwu) * u + j0 + cc % nwu; };  // gate column of local column cc
 
-    // the weight slice, once: local column cc = g·nwu + jj is gate g of unit j0 + jj; k ≥ u and columns ≥ NC are zero
+    // h rows (and the rows past B, k past u, which stay zero) cleared; the weight slice, once: local column
+    // cc = g·nwu + jj is gate g of unit j0 + jj; k ≥ u and columns ≥ NC are zero
+    for (size_t e = tid; e < (L.pt - L.hs) / 4; e += kThreads) reinterpret_cast<int*>(smem + L.hs)[e] = 0;
     if (i8) {
         for (int e = tid; e < ncp * (up / 4); e += kThreads) {
             const int cc = e / (up / 4), w = e % (up / 4);
@@ -127,18 +163,31 @@ __global__ void __launch_bounds__(kThreads) rnn_recurrence(RnnArgs a)
             usf[cc * upp + k] = v;
         }
     }
+    for (int cc = tid; cc < ncp; cc += kThreads) {
+        const int col = cc < NC ? column(cc) : 0;
+        csc[cc] = i8 && cc < NC ? a.qs[col] : 1.0f;
+        cbi[cc] = a.brec && cc < NC ? a.brec[col] : 0.0f;
+    }
     // this thread's (row, unit) pairs of the cell phase and their per-column constants
     const int npairs = B * nwu;
     float cst[kMaxPairs];
     for (int i = 0; i < kMaxPairs; ++i) cst[i] = 0.0f;
 
-    // dot products: O groups of CB columns of one row, P consecutive lanes each (a power of two ≤ 64)
-    const int ncg = ncp / CB, O = B * ncg;
-    int P = 1;
-    while (P < 64 && P * 2 * O <= kThreads) P *= 2;
-    const int groups = kThreads / P, gl = tid % P;
-    int qlpr = 1;  // lanes per row of the int8 quantizer
-    while (qlpr < 64 && qlpr * 8 < u) qlpr *= 2;
+    // loading h_{t−1}: a row is W4 float4s over LR lanes (a power of two: as many as keep every row within one pass
+    // of the four waves, at least enough for kLoads float4s per lane to cover the row, at most one per float4), RPW
+    // rows per wave-wide load; lane (rsub, lr) of row group g takes row g·RPW + rsub, float4s lr + LR·s, s < NWL
+    const int W4 = (u + 3) / 4;
+    int LR = 1;
+    while (LR < 64 && LR < W4 && (LR * kLoads < W4 || 2 * LR * B <= kThreads)) LR *= 2;
+    const int RPW = 64 / LR, NWL = (W4 + LR - 1) / LR, ngr = (B + RPW - 1) / RPW;
+    const int lr = lane % LR, rsub = lane / LR;
+
+    // products: RB × NCT output tiles of 16 × 16 (rows of h × local columns); with fewer tiles than waves the k
+    // chunks of a tile are split over kparts waves, whose partial tiles are summed in LDS in wave order
+    const int RB = L.b16 / 16, NCT = ncp / 16, tiles = RB * NCT;
+    const int kparts = tiles >= kWaves ? 1 : tiles == 1 ? kWaves : tiles == 2 ? 2 : 1;
+    const int part = wave % kparts, fr = lane & 15, fq = lane >> 4;
+    const int nkc = i8 ? up / 64 : up / 16;
 
     // the input-side gate values of this thread's pairs, one timestep ahead (they do not depend on h)
     auto load_z = [&](int st, float (&z)[kMaxPairs][4]) {
@@ -152,6 +201,14 @@ __global__ void __launch_bounds__(kThreads) rnn_recurrence(RnnArgs a)
                 z[i][g] = pr < npairs && g < G ? a.zx[((size_t)b * T + tt) * gu + (size_t)g * u + j0 + jj] : 0.0f;
         }
     };
+    // the recurrent term of row b, local column cc from its product (fp32 sum, or int32 sum dequantized as the int8
+    // GEMM's epilogue ((float)acc · sx) · scale), plus the GRU's recurrent bias
+    auto put = [&](int b, int cc, int bits) {
+        float x = i8 ? (float)bits * sxs[b] * csc[cc] : __int_as_float(bits);
+        if (a.brec) x = x + cbi[cc];
+        r[b * NCM + cc] = x;
+    };
+    __syncthreads();
     float zn[kMaxPairs][4];
     load_z(0, zn);
     for (int step = 0; step < T; ++step) {
@@ -165,102 +222,136 @@ __global__ void __launch_bounds__(kThreads) rnn_recurrence(RnnArgs a)
             for (int g = 0; g < 4; ++g) zv[i][g] = zn[i][g];
         if (step + 1 < T) load_z(step + 1, zn);
         if (step > 0) {
-            // h_{t−1} into LDS: the B·u floats as float4s (the buffers are 16-byte aligned and padded to 256 bytes),
-            // up to kLoads in flight per thread, all issued before the first is stored
-            {
-                const int n = B * u, n4 = (n + 3) / 4;
-                const float4* src = reinterpret_cast<const float4*>(hin);
-                for (int f0 = 0; f0 < n4; f0 += kLoads * kThreads) {
-                    float4 v[kLoads];
+            // h_{t−1} into LDS, a batch of up to kLoads float4s per lane issued before the first is used; int8: each
+            // row quantized from the registers (s = max|h|/127, 1 for an all-zero row, NaN for a row holding NaN or
+            // ±inf; q = clamp(rint(h·(1/s)), ±127), four to a word; a row that cannot be quantized stores zeros:
+            // its outputs are NaN through its scale)
+            for (int g = wave_u; g < ngr; g += kWaves) {
+                const int b = g * RPW + rsub;
+                float4 v[kLoads];
+                bool ok[kLoads];
 #pragma unroll
-                    for (int i = 0; i < kLoads; ++i) {
-                        const int f = f0 + tid + i * kThreads;
-                        v[i] = f < n4 ? src[f] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                for (int s = 0; s < kLoads; ++s) {
+                    const int w = lr + LR * s;
+                    ok[s] = s < NWL && b < B && w < W4;
+                    v[s] = ok[s] ? *reinterpret_cast<const float4*>(hin + (size_t)b * ldh + 4 * w)
+                                 : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                }
+#pragma unroll
+                for (int s = 0; s < kLoads; ++s) {
+                    if (s >= NWL) break;
+                    const int w = lr + LR * s;
+                    if (4 * w + 4 > u) {  // the float4 reaching past u: the row padding is not h
+                        if (4 * w + 1 >= u) v[s].y = 0.0f;
+                        if (4 * w + 2 >= u) v[s].z = 0.0f;
+                        v[s].w = 0.0f;
                     }
+                    if (h32 && ok[s]) *reinterpret_cast<float4*>(hs + b * hp + 4 * w) = v[s];
+                }
+                if (i8) {
+                    // the row's max |h| as bits (NaN above +inf above every finite value) over its LR lanes, the
+                    // quantizer's scale (max/127, 1 for an all-zero row, NaN for a row holding NaN or ±inf) and
+                    // q = clamp(rint(h·(1/s)), ±127), four to a word; + 128 is an exact integer that converts
+                    // exactly to a byte; a row that cannot be quantized stores zeros: its outputs are NaN through its
+                    // scale
+                    unsigned m = 0;
 #pragma unroll
-                    for (int i = 0; i < kLoads; ++i) {
-                        const int f = f0 + tid + i * kThreads;
-                        if (f >= n4) continue;
-                        int b = 4 * f / u, k = 4 * f - b * u;  // element 4f is (b, k); the next ones may wrap
+                    for (int s = 0; s < kLoads; ++s) {
+                        if (s >= NWL) break;
+                        const unsigned x = __float_as_uint(v[s].x) & 0x7fffffffu, y = __float_as_uint(v[s].y) & 0x7fffffffu;
+                        const unsigned z = __float_as_uint(v[s].z) & 0x7fffffffu, w = __float_as_uint(v[s].w) & 0x7fffffffu;
+                        m = max(m, max(max(x, y), max(z, w)));
+                    }
+                    m = lane_group_max(m, LR);
+                    const bool bad = m >= 0x7f800000u;
+                    const float mx = __uint_as_float(m);
+                    const float sc = (!bad && mx > 0.0f) ? __fdiv_rn(mx, 127.0f) : 1.0f;
+                    const float inv = bad ? 0.0f : __fdiv_rn(1.0f, sc);
+                    if (lr == 0 && b < B) sxs[b] = bad ? __int_as_float(0x7fc00000) : sc;
 #pragma unroll
-                        for (int q = 0; q < 4; ++q) {
-                            if (b * u + k < n) hs[b * hp + k] = (&v[i].x)[q];
-                            if (++k == u) k = 0, ++b;
-                        }
+                    for (int s = 0; s < kLoads; ++s) {
+                        if (s >= NWL) break;
+                        if (!ok[s]) continue;
+                        unsigned pk = 0;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            pk = __builtin_amdgcn_cvt_pk_u8_f32(
+                                __builtin_amdgcn_fmed3f(rintf((&v[s].x)[e] * inv), -127.0f, 127.0f) + 128.0f, e, pk);
+                        hqw[b * hwp + lr + LR * s] = (int)(pk ^ 0x80808080u);
                     }
                 }
             }
             __syncthreads();
-            if (i8) {
-                // LPR lanes per row (a power of two, about 8 values each): maximum, scale, quantized values packed
-                // four to a word (bytes past u are 0)
-                const int rl = lane % qlpr;
-                for (int b = wave * (64 / qlpr) + lane / qlpr; b - lane / qlpr < B; b += kWaves * (64 / qlpr)) {
-                    const int bb = min(b, B - 1);  // lanes past the last row repeat it, unstored
-                    float mx = 0.0f;
-                    for (int k = rl; k < u; k += qlpr) mx = fmaxf(mx, mag(hs[bb * hp + k]));
-                    for (int off = qlpr / 2; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-                    if (b >= B) continue;
-                    const bool bad = !(mx <= FLT_MAX);
-                    const float sc = (!bad && mx > 0.0f) ? __fdiv_rn(mx, 127.0f) : 1.0f;
-                    const float inv = __fdiv_rn(1.0f, sc);
-                    if (rl == 0) sxs[b] = bad ? __int_as_float(0x7fc00000) : sc;
-                    for (int w = rl; w < up / 4; w += qlpr) {
-                        // a row that cannot be quantized stores zeros: its outputs are NaN through its scale
-                        unsigned pk = 0;
+            // the recurrent terms of this workgroup's columns on the matrix cores: tile (rt, ct), lane (fr, fq) holds
+            // rows 16·rt + 4·fq + e, e < 4, of local column 16·ct + fr
+            for (int ti = wave / kparts; ti < tiles; ti += kWaves / kparts) {
+                const int rt = ti % RB, ct = ti / RB;
+                v4i acc = {0, 0, 0, 0};
+                if (i8) {
+                    const int* ar = hqw + (16 * rt + fr) * hwp + 4 * fq;
+                    const int* br = usw + (16 * ct + fr) * upp + 4 * fq;
+                    for (int kc = part; kc < nkc; kc += 2 * kparts) {
+                        const bool two = kc + kparts < nkc;
+                        const v4i a0 = *reinterpret_cast<const v4i*>(ar + 16 * kc);
+                        const v4i b0 = *reinterpret_cast<const v4i*>(br + 16 * kc);
+                        const v4i a1 = two ? *reinterpret_cast<const v4i*>(ar + 16 * (kc + kparts)) : v4i{0, 0, 0, 0};
+                        const v4i b1 = two ? *reinterpret_cast<const v4i*>(br + 16 * (kc + kparts)) : v4i{0, 0, 0, 0};
+                        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, acc, 0, 0, 0);
+                        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, acc, 0, 0, 0);
+                    }
+                } else {
+                    v4f f = {0.0f, 0.0f, 0.0f, 0.0f};
+                    const float* ar = hs + (16 * rt + fr) * hp + 4 * fq;
+                    const float* br = usf + (16 * ct + fr) * upp + 4 * fq;
+                    for (int kc = part; kc < nkc; kc += 4 * kparts) {
+                        float4 av[4], bv[4];
 #pragma unroll
                         for (int i = 0; i < 4; ++i) {
-                            const int k = 4 * w + i;
-                            const float v = k < u && !bad ? __builtin_amdgcn_fmed3f(rintf(hs[b * hp + k] * inv), -127.0f, 127.0f) : 0.0f;
-                            pk |= (unsigned)(uint8_t)(int8_t)(int)v << (8 * i);
+                            const int kk = kc + i * kparts;
+                            const bool in = kk < nkc;
+                            av[i] = in ? *reinterpret_cast<const float4*>(ar + 16 * kk) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                            bv[i] = in ? *reinterpret_cast<const float4*>(br + 16 * kk) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
                         }
-                        hqw[b * hwp + w] = (int)pk;
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            f = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i].x, bv[i].x, f, 0, 0, 0);
+                            f = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i].y, bv[i].y, f, 0, 0, 0);
+                            f = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i].z, bv[i].z, f, 0, 0, 0);
+                            f = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i].w, bv[i].w, f, 0, 0, 0);
+                        }
                     }
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[e] = __float_as_int(f[e]);
                 }
-                __syncthreads();
-            }
-            // the recurrent terms of this workgroup's columns
-            for (int o0 = 0; o0 < O; o0 += groups) {
-                const int o = min(o0 + tid / P, O - 1);  // lanes past the end repeat the last group, unstored
-                const int b = o / ncg, c0 = (o % ncg) * CB;
-                float v[CB];
-                if (i8) {
-                    int acc[CB] = {};
-                    const int* hw = hqw + b * hwp;
-                    for (int w = gl; w < up / 4; w += P) {
-                        const int hv = hw[w];
+                if (kparts == 1) {
 #pragma unroll
-                        for (int c = 0; c < CB; ++c) acc[c] = __builtin_amdgcn_sdot4(hv, usw[(c0 + c) * upp + w], acc[c], false);
-                    }
-#pragma unroll
-                    for (int c = 0; c < CB; ++c) {
-                        for (int off = P / 2; off > 0; off >>= 1) acc[c] += __shfl_xor(acc[c], off, 64);
-                        v[c] = (float)acc[c] * sxs[b];  // ((float)acc · sx) · scale, the int8 GEMM's epilogue
+                    for (int e = 0; e < 4; ++e) {
+                        const int b = 16 * rt + 4 * fq + e, cc = 16 * ct + fr;
+                        if (b < B && cc < NC) put(b, cc, acc[e]);
                     }
                 } else {
 #pragma unroll
-                    for (int c = 0; c < CB; ++c) v[c] = 0.0f;
-                    const float* hr = hs + b * hp;
-                    for (int k = gl; k < u; k += P) {
-                        const float hv = hr[k];
-#pragma unroll
-                        for (int c = 0; c < CB; ++c) v[c] = fmaf(hv, usf[(c0 + c) * upp + k], v[c]);
-                    }
-#pragma unroll
-                    for (int c = 0; c < CB; ++c)
-                        for (int off = P / 2; off > 0; off >>= 1) v[c] += __shfl_xor(v[c], off, 64);
+                    for (int e = 0; e < 4; ++e) pt[wave * 256 + (4 * fq + e) * 16 + fr] = acc[e];
                 }
-                if (gl == 0 && o0 + tid / P < O) {
-#pragma unroll
-                    for (int c = 0; c < CB; ++c) {
-                        const int cc = c0 + c;
-                        if (cc >= NC) break;
-                        const int col = column(cc);
-                        float x = v[c];
-                        if (i8) x = x * a.qs[col];
-                        if (a.brec) x = x + a.brec[col];
-                        r[b * NCM + cc] = x;
+            }
+            if (kparts > 1) {  // the partial tiles of tile ti are those of waves ti·kparts … ti·kparts + kparts − 1
+                __syncthreads();
+                for (int e = tid; e < tiles * 256; e += kThreads) {
+                    const int ti = e / 256, i = e % 256;
+                    const int b = 16 * (ti % RB) + i / 16, cc = 16 * (ti / RB) + i % 16;
+                    if (b >= B || cc >= NC) continue;
+                    const int* p = pt + ti * kparts * 256 + i;
+                    int bits;
+                    if (i8) {
+                        int s = 0;
+                        for (int w = 0; w < kparts; ++w) s += p[256 * w];
+                        bits = s;
+                    } else {
+                        float s = __int_as_float(p[0]);
+                        for (int w = 1; w < kparts; ++w) s = s + __int_as_float(p[256 * w]);
+                        bits = __float_as_int(s);
                     }
+                    put(b, cc, bits);
                 }
             }
             __syncthreads();
@@ -289,7 +380,7 @@ __global__ void __launch_bounds__(kThreads) rnn_recurrence(RnnArgs a)
                 if (!first) v = v + rec(0);
                 hv = knx_act(v, a.act, a.alpha);
             }
-            if (step + 1 < T) __hip_atomic_store(hout + (size_t)b * u + j, hv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (step + 1 < T) __hip_atomic_store(hout + (size_t)b * ldh + j, hv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (a.ret_seq) a.dst[((size_t)b * T + t) * a.stride + j] = hv;
             else if (step + 1 == T) a.dst[(size_t)b * a.stride + j] = hv;
         }
@@ -468,16 +559,18 @@ int solo_lanes(int B, int gu, int u, bool i8)
     return len <= ks * (i8 ? kSoloRegs / 2 : kSoloRegs) ? ks : 0;  // lane s covers [s·R, (s+1)·R)
 }
 
-// units per workgroup: the grid's workgroups each take ⌈u / G⌉ units, G as large as the barrier allows while each
-// workgroup still has at least one unit and its (row, unit) pairs fit the threads
-int units_per_wg(int B, int u)
+// units per workgroup: enough that the workgroup's gate columns fill a 16-wide tile of the products (LSTM 4, GRU 5,
+// simple RNN 16 units), more where u needs it to stay within kMaxGrid workgroups, fewer where the (row, unit) pairs
+// would not fit the threads
+int units_per_wg(int B, int u, int gates)
 {
-    int uw = (u + kMaxGrid - 1) / kMaxGrid;
+    const int least = (u + kMaxGrid - 1) / kMaxGrid;
+    int uw = std::max(least, 16 / gates);
     if (const char* e = getenv("KNX_RNN_UNITS")) {  // tuning: units per workgroup
         const int v = atoi(e);
-        if (v >= 1) uw = std::max(uw, v);
+        if (v >= 1) uw = std::max(least, v);
     }
-    while (B * uw > kThreads * kMaxPairs && uw > 1) --uw;  // cannot happen for B ≤ 64 (uw ≤ 8 then)
+    while (B * uw > kThreads * kMaxPairs && uw > least) --uw;
     return uw;
 }
 
@@ -488,10 +581,10 @@ extern "C" int knx_hip_rnn_recurrence_fits(int kind, int B, int u, int i8)
     if ((kind != 4 && kind != 5 && kind != 6) || B < 1 || B > 64 || u < 1 || u > 65536) return 0;
     const int gates = kind == 4 ? 4 : kind == 5 ? 3 : 1;
     if (solo_lanes(B, gates * u, u, i8 != 0) > 0) return 1;
-    const int uw = units_per_wg(B, u);
+    if (u > kMaxUnits) return 0;
+    const int uw = units_per_wg(B, u, gates);
     if ((u + uw - 1) / uw > kMaxGrid || B * uw > kThreads * kMaxPairs) return 0;
-    const int up = (u + 3) / 4 * 4;
-    return lds_layout(B, gates, uw, up, i8 != 0).total <= kMaxLds ? 1 : 0;
+    return lds_layout(B, gates, uw, k_extent(u, i8 != 0), i8 != 0, !i8 || kind == 5).total <= kMaxLds ? 1 : 0;
 }
 
 extern "C" int knx_hip_rnn_recurrence(int kind, int act, float alpha, int B, int T, int u, int dir, const float* zx,
@@ -505,6 +598,7 @@ extern "C" int knx_hip_rnn_recurrence(int kind, int act, float alpha, int B, int
     KNX_REQUIRE(knx_hip_rnn_recurrence_fits(kind, B, u, q != nullptr), name);
     const int gates = kind == 4 ? 4 : kind == 5 ? 3 : 1;
     KNX_REQUIRE(zx != nullptr && h0 != nullptr && h1 != nullptr && dst != nullptr && stride >= u, name);
+    KNX_REQUIRE((((uintptr_t)h0 | (uintptr_t)h1) & 15) == 0, name);
     KNX_REQUIRE(kind != 5 || brec != nullptr, name);
     KNX_REQUIRE(q != nullptr ? (qscale != nullptr && kp >= (u + 3) / 4 * 4 && ((uintptr_t)q & 3) == 0 && kp % 4 == 0)
                              : U != nullptr, name);
@@ -513,7 +607,8 @@ extern "C" int knx_hip_rnn_recurrence(int kind, int act, float alpha, int B, int
     RnnArgs a{};
     a.kind = kind; a.act = act; a.alpha = alpha;
     a.B = B; a.T = T; a.u = u; a.gu = gates * u; a.gates = gates; a.dir = dir; a.ret_seq = ret_seq != 0;
-    a.stride = stride; a.uw = units_per_wg(B, u); a.up = (u + 3) / 4 * 4;
+    a.stride = stride; a.uw = units_per_wg(B, u, gates);
+    a.up = k_extent(u, q != nullptr); a.ldh = (u + 3) / 4 * 4;
     a.zx = zx; a.U = U; a.u_nt = u_nt != 0; a.q = q; a.kp = kp; a.qs = qscale; a.brec = brec;
     a.h0 = h0; a.h1 = h1; a.dst = dst;
     a.gs = knx::GridSync{static_cast<unsigned long long*>(scratch), status, knx::grid_spin_limit()};
@@ -524,14 +619,18 @@ extern "C" int knx_hip_rnn_recurrence(int kind, int act, float alpha, int B, int
         return knx::check_launch(name);
     }
     const int G = (u + a.uw - 1) / a.uw;
-    const size_t lds = lds_layout(B, gates, a.uw, a.up, q != nullptr).total;
+    const size_t lds = lds_layout(B, gates, a.uw, a.up, q != nullptr, q == nullptr || kind == 5).total;
     static std::once_flag once;
     static hipError_t attr = hipSuccess;
     std::call_once(once, [] {
-        attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&rnn_recurrence),
+        attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&rnn_recurrence<false>),
                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds);
+        if (attr == hipSuccess)
+            attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&rnn_recurrence<true>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds);
     });
     if (attr != hipSuccess) return knx::fail(KNX_EHIP, "%s: %s", name, hipGetErrorString(attr));
-    hipLaunchKernelGGL(rnn_recurrence, dim3((unsigned)G), dim3(kThreads), lds, knx::as_stream(stream), a);
+    if (q != nullptr) hipLaunchKernelGGL(rnn_recurrence<true>, dim3((unsigned)G), dim3(kThreads), lds, knx::as_stream(stream), a);
+    else hipLaunchKernelGGL(rnn_recurrence<false>, dim3((unsigned)G), dim3(kThreads), lds, knx::as_stream(stream), a);
     return knx::check_launch(name);
 }

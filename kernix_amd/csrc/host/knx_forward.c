@@ -285,10 +285,11 @@ static int ws_walk(kernix_model* m, size_t B, ws_ctx* c)
             const int rnn = s->kind != KERNIX_OP_LINEAR;
             const size_t qrows = rnn ? B : rin; /* rows of the int8 product: batch for the recurrence */
             if (rnn) {
-                const size_t u = (size_t)s->out, gu = gates(s->kind) * u;
+                /* h and the recurrent terms double as the one-launch recurrence's two h buffers: rows of u4 */
+                const size_t u = (size_t)s->out, gu = gates(s->kind) * u, u4 = (u + 3) / 4 * 4;
                 if (ws_tensor(c, &s->tmp[0], rin, gu) || ws_tensor(c, &s->tmp[1], B, gu) ||
-                    (s->kind == KERNIX_OP_LSTM && ws_tensor(c, &s->tmp[2], B, u)) || ws_tensor(c, &s->tmp[3], B, u) ||
-                    ws_tensor(c, &s->tmp[4], B, gu) ||
+                    (s->kind == KERNIX_OP_LSTM && ws_tensor(c, &s->tmp[2], B, u)) || ws_tensor(c, &s->tmp[3], B, u4) ||
+                    ws_tensor(c, &s->tmp[4], B, gu > u4 ? gu : u4) ||
                     (s->dirs == 2 && s->merge != KERNIX_MERGE_CONCAT && ws_tensor(c, &s->tmp[5], s->ret_seq ? rin : B, u)))
                     return -1;
             }
@@ -574,7 +575,7 @@ static int run_rnn_dir(const kernix_model* m, kernix_step* s, int dir, const flo
     if (hip_ok(knx_hip_sgemm_ep(x->row, gu, s->in, x->tensor, s->in, W, gu, bias, -1, 0.0f, zx, gu, st), "RNN input projection")) return -1;
     const int i8 = q != NULL && (m->int8_mode == KERNIX_INT8_I8 || B <= KERNIX_INT8_MAX_ROWS);
     if (rnn_persistent(m) && knx_hip_rnn_recurrence_fits(kind, B, u, i8)) {
-        /* every timestep in one launch; h alternates between h and the recurrent-term buffer (B × gu ≥ B × u) */
+        /* every timestep in one launch; h alternates between h and the recurrent-term buffer (B rows of u4 each) */
         if (!i8 && U == NULL) return -1;
         return hip_ok(knx_hip_rnn_recurrence(kind, s->act, s->alpha, B, T, u, dir, zx, i8 ? NULL : U, q != NULL,
                                              i8 ? dq : NULL, q != NULL ? q->kp : 0, dsc, brec, h, hu, dst, stride,

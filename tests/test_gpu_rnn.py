@@ -46,6 +46,8 @@ CASES = [
     ("LSTM", 2, 128, 128, 6),
     ("GRU", 1, 200, 24, 4),
     ("LSTM", 1, 3, 5, 1),
+    ("RNN", 1, 512, 8, 3),     # a row of h over 64 lanes, two float4s each (fp32 fits the LDS up to batch 17)
+    ("LSTM", 1, 1000, 8, 3),   # int8 recurrences: four float4s per lane, the last row partly past u
 ]
 
 
