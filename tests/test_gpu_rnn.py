@@ -134,3 +134,15 @@ def test_forward_uses_the_persistent_recurrence(tmp_path, monkeypatch, batch, ex
         m.close()
     want, _ = knx_ref.forward(knx_ref.parse(p), x.reshape(-1, 16))
     assert rel_err(y, want) <= 1e-4
+
+
+def test_recurrence_that_stopped_waiting_is_recomputed(tmp_path, monkeypatch):
+    """with a poll limit of 0 (forced from the host) every workgroup but the last to reach a timestep's barrier stops
+    waiting and sets the model's status word; the forward is then recomputed one launch per timestep, so the result
+    is the per-timestep path's, bit for bit (int8 recurrence)"""
+    p = str(tmp_path / "g.knx")
+    x = configs.lstm(p, seed=3, batch=16, T=6, fin=16, units=64, int8=True)
+    want = forward(p, x, "i8", monkeypatch, False)
+    monkeypatch.setenv("KNX_GRID_SPIN", "0")
+    got = forward(p, x, "i8", monkeypatch, True)
+    assert np.array_equal(got, want)
