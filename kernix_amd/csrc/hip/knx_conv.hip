@@ -272,6 +272,12 @@ __global__ void __launch_bounds__(256) conv_small(SmallConvArgs a)
     __shared__ float wl[SMALL_K * CO];  // the weights, [k][co]: staged once per workgroup with coalesced loads
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int rl = lane & 31, g = lane >> 5;
+    // y (and R) as buffers of M·Co floats (< 2^31 bytes, checked at launch)
+    const int ybytes = (int)((long long)a.M * CO * 4);
+    const __amdgpu_buffer_rsrc_t yr = __builtin_amdgcn_make_buffer_rsrc(a.y, (short)0, ybytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(RES ? a.R : a.y), (short)0,
+                                                                        ybytes, 0x00020000);
+    constexpr int kPast = 0x7ffffff0;
     for (int i = threadIdx.x; i < a.K * CO; i += 256) {
         // i walks the weight in memory order: Wt rows (co, then k) or W rows (k, then co)
         const int co = a.wsk == 1 ? i / a.K : i % CO, k = a.wsk == 1 ? i % a.K : i / CO;
@@ -321,35 +327,34 @@ __global__ void __launch_bounds__(256) conv_small(SmallConvArgs a)
                 acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[p], wl[(2 * p + g) * CO + 32 * nb + rl], acc[nb], 0, 0, 0);
         // accumulator e of block nb: pixel m0 + 8·(e >> 2) + 4·g + (e & 3), channel 32·nb + rl; Co = 32·NB, so
         // every element's offset from this lane's first one is a constant
-        const size_t first = (size_t)(m0 + 4 * g) * CO + rl;
-        float* yl = a.y + first;
+        // Every store is issued, rows past M with an offset past the buffer's end (the hardware drops them): a
+        // fixed count of stores per group, so the compiler's count of memory operations in flight stays exact
+        // across the loop and the next group's inputs are waited for without waiting for these stores.
+        const int first = (int)((m0 + 4 * g) * CO + rl) * 4;
         const int left = (int)std::min<long long>(a.M - m0 - 4 * g, 32);  // rows of this lane's half still in M
-        auto write = [&](bool all) {  // all: the whole group is inside M (no per-row test)
-            float rres[NB][16];
-            if (RES) {  // every residual element this lane adds is loaded before its stores (R may be y)
-                const float* rlp = a.R + first;
-#pragma unroll
-                for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-                    for (int e = 0; e < 16; ++e) {
-                        const int row = 8 * (e >> 2) + (e & 3);
-                        rres[nb][e] = all || row < left ? rlp[row * CO + 32 * nb] : 0.0f;
-                    }
-            }
+        float rres[NB][16];
+        if (RES) {  // every residual element this lane adds is loaded before its stores (R may be y)
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
                     const int row = 8 * (e >> 2) + (e & 3);
-                    float v = acc[nb][e];
-                    if (a.bias) v = v + bv[nb];
-                    if (a.relu) v = v >= 0.0f ? v : 0.0f;  // the ReLU of knx_act (NaN → 0)
-                    if (RES) v = v + rres[nb][e];
-                    if (all || row < left) yl[row * CO + 32 * nb] = v;
+                    rres[nb][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                        rr, full || row < left ? first + 4 * (row * CO + 32 * nb) : kPast, 0, 0));
                 }
-        };
-        if (full) write(true);
-        else write(false);
+        }
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int row = 8 * (e >> 2) + (e & 3);
+                float v = acc[nb][e];
+                if (a.bias) v = v + bv[nb];
+                if (a.relu) v = v >= 0.0f ? v : 0.0f;  // the ReLU of knx_act (NaN → 0)
+                if (RES) v = v + rres[nb][e];
+                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, v), yr,
+                                                      full || row < left ? first + 4 * (row * CO + 32 * nb) : kPast, 0, 0);
+            }
     };
     // Each wave takes the groups of 32 pixels m0, m0 + step, …; the next group's inputs are in flight while one
     // multiplies and stores (two input buffers, alternating).
@@ -357,6 +362,9 @@ __global__ void __launch_bounds__(256) conv_small(SmallConvArgs a)
     long long m0 = ((long long)blockIdx.x * 4 + wave) * 32;
     float av0[KP], av1[KP];
     gather(m0, av0);
+    // the first group's inputs waited for here, so that at the loop's head the only loads in flight are those of
+    // the iterations before (followed by their stores) and the waits inside the loop count those stores
+    __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // vmcnt(0)
     while (m0 < a.M) {
         gather(m0 + step, av1);
         group(m0, av0, m0 + 32 <= a.M);  // m0 is the same in every lane: a scalar branch
@@ -381,6 +389,7 @@ int conv_small_entry(const knx_conv_geom* g, const float* x, const float* w, boo
     if (g->groups != 1 || K > SMALL_K || g->Co % 32 != 0 || g->Co > 128 || (act != -1 && act != 0)) return 1;
     const long long span = ((long long)(g->kh - 1) * g->dh * g->W + (long long)(g->kw - 1) * g->dw + 1) * g->C;
     if (span > 0x7fffffffLL || (g->kh - 1) * g->dh > 0x7fff || (g->kw - 1) * g->dw > 0xffff) return 1;
+    if ((long long)g->B * g->Ho * g->Wo * g->Co * 4 >= (1LL << 31) - 16) return 1;  // y as a buffer: 32-bit offsets
     SmallConvArgs a{};
     a.x = x; a.w = w; a.bias = bias; a.R = R; a.y = y;
     a.H = g->H; a.W = g->W; a.C = g->C; a.Ho = g->Ho; a.Wo = g->Wo; a.Co = g->Co;
