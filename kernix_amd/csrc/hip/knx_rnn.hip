@@ -94,12 +94,6 @@ __host__ __device__ inline Lds lds_layout(int B, int gates, int uw, int up, bool
     return l;
 }
 
-__device__ __forceinline__ float mag(float v)
-{
-    const float a = fabsf(v);
-    return a <= FLT_MAX ? a : INFINITY;
-}
-
 // unsigned maximum over aligned groups of n lanes (n a power of two ≤ 64, uniform; every lane active): row-local
 // DPP for groups up to 16, lane exchanges above
 __device__ __forceinline__ unsigned lane_group_max(unsigned v, int n)
@@ -393,8 +387,10 @@ __global__ void __launch_bounds__(kThreads) rnn_recurrence(RnnArgs a)
 // memory (h stores, the barrier, h reloads).  One workgroup of 1024 threads keeps all of U in registers — thread t owns
 // column c = t / KS and its k-slice [s·KSL, (s+1)·KSL), s = t % KS, KS lanes per column (consecutive lanes, so their
 // partial sums are reduced by exchanges; the lanes of one slice read the same h values, 16 bytes at a time) — and h in
-// LDS, so a timestep is two workgroup barriers and no global synchronization.  Same quantizer, int32 sums, epilogue
-// and cells as above.
+// LDS, so a timestep is two workgroup barriers and no global synchronization (three with int8 arithmetic).  Same
+// quantizer, int32 sums, epilogue and cells as above; with int8 arithmetic the cells that write h_t also gather its
+// row maxima (per wave, then one LDS atomic per wave and row), and at the next step every cell quantizes its own value
+// with its row's scale, so the quantization is one multiply-and-round per thread instead of a pass over the rows.
 constexpr int kSoloThreads = 1024;
 constexpr int kSoloRegs = 64;   // U values per thread (fp32; int8: kSoloRegs / 2 words of four values)
 constexpr int kSoloRows = 2;
@@ -405,6 +401,7 @@ __global__ void __launch_bounds__(kSoloThreads) rnn_solo(RnnArgs a, int KS)
     __shared__ __attribute__((aligned(16))) float hs[kSoloRows][2048];  // h_{t−1}, fp32 (u ≤ 2048), zero past u
     __shared__ __attribute__((aligned(16))) int hq[kSoloRows][512];     // its int8 rows, four to a word
     __shared__ float sxs[kSoloRows];
+    __shared__ unsigned rmx[2][kSoloRows];  // int8: each row's max |h| as bits, by the parity of the step that wrote h
     __shared__ float r[kSoloRows][kSoloThreads];                        // recurrent terms (gates·u ≤ 1024)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int B = a.B, T = a.T, u = a.u, gu = a.gu, G = a.gates, uw4 = (u + 3) / 4;
@@ -416,6 +413,7 @@ __global__ void __launch_bounds__(kSoloThreads) rnn_solo(RnnArgs a, int KS)
     // this thread's part of U; h is zero past u, so the slice runs over whole 16-byte groups
     for (int e = tid; e < kSoloRows * 2048; e += kSoloThreads) (&hs[0][0])[e] = 0.0f;
     for (int e = tid; e < kSoloRows * 512; e += kSoloThreads) (&hq[0][0])[e] = 0;
+    if (tid < 2 * kSoloRows) (&rmx[0][0])[tid] = 0u;
     float uf[I8 ? 4 : REGS];
     int uq[I8 ? REGS : 4];
 #pragma unroll
@@ -440,9 +438,7 @@ __global__ void __launch_bounds__(kSoloThreads) rnn_solo(RnnArgs a, int KS)
     // cell phase: thread tid < B·u owns row b = tid / u, unit j = tid % u
     const bool cell = tid < B * u;
     const int cb = cell ? tid / u : 0, cj = cell ? tid % u : 0;
-    float cst = 0.0f;
-    int qlpr = 1;
-    while (qlpr < 64 && qlpr * 8 < u) qlpr *= 2;
+    float cst = 0.0f, hreg = 0.0f;  // the cell's c and h
     // the input-side gate values of this thread's cell, one timestep ahead (they do not depend on h)
     auto load_z = [&](int st, float (&z)[4]) {
         const int tt = a.dir ? T - 1 - st : st;
@@ -459,29 +455,21 @@ __global__ void __launch_bounds__(kSoloThreads) rnn_solo(RnnArgs a, int KS)
         if (step + 1 < T) load_z(step + 1, zn);
         if (step > 0) {
             if (I8) {
-                const int rl = lane % qlpr, b = wave * (64 / qlpr) + lane / qlpr;
-                if (wave * (64 / qlpr) < B) {  // the waves that hold a row (uniform over the wave)
-                    const int bb = min(b, B - 1);
-                    float mx = 0.0f;
-                    for (int k = rl; k < u; k += qlpr) mx = fmaxf(mx, mag(hs[bb][k]));
-                    for (int off = qlpr / 2; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-                    if (b < B) {
-                        const bool bad = !(mx <= FLT_MAX);
-                        const float sc = (!bad && mx > 0.0f) ? __fdiv_rn(mx, 127.0f) : 1.0f;
-                        const float inv = __fdiv_rn(1.0f, sc);
-                        if (rl == 0) sxs[b] = bad ? __int_as_float(0x7fc00000) : sc;
-                        for (int w = rl; w < uw4; w += qlpr) {
-                            unsigned pk = 0;
-#pragma unroll
-                            for (int e = 0; e < 4; ++e) {
-                                const int k = 4 * w + e;
-                                const float v = k < u && !bad ? __builtin_amdgcn_fmed3f(rintf(hs[b][k] * inv), -127.0f, 127.0f) : 0.0f;
-                                pk |= (unsigned)(uint8_t)(int8_t)(int)v << (8 * e);
-                            }
-                            hq[b][w] = (int)pk;
-                        }
-                    }
+                // each cell quantizes its own h_{t−1} with its row's scale (the row maximum was gathered by the cells
+                // that wrote it: s = max|h|/127, 1 for an all-zero row, NaN for a row holding NaN or ±inf;
+                // q = clamp(rint(h·(1/s)), ±127); bytes past u stay 0; a row that cannot be quantized stores zeros:
+                // its outputs are NaN through its scale); this step's row maxima start from 0
+                if (cell) {
+                    const unsigned mb = rmx[(step - 1) & 1][cb];
+                    const bool bad = mb >= 0x7f800000u;
+                    const float mx = __uint_as_float(mb);
+                    const float sc = (!bad && mx > 0.0f) ? __fdiv_rn(mx, 127.0f) : 1.0f;
+                    const float inv = bad ? 0.0f : __fdiv_rn(1.0f, sc);
+                    if (cj == 0) sxs[cb] = bad ? __int_as_float(0x7fc00000) : sc;
+                    const float qv = __builtin_amdgcn_fmed3f(rintf(hreg * inv), -127.0f, 127.0f);
+                    reinterpret_cast<int8_t*>(&hq[cb][0])[cj] = (int8_t)(int)qv;
                 }
+                if (tid < B) rmx[step & 1][tid] = 0u;
                 __syncthreads();
             }
             for (int b = 0; b < B; ++b) {
@@ -520,10 +508,10 @@ __global__ void __launch_bounds__(kSoloThreads) rnn_solo(RnnArgs a, int KS)
             }
         }
         __syncthreads();  // r complete; every read of hs done
+        float hv = 0.0f;
         if (cell) {
             const bool first = step == 0;
             auto rec = [&](int g) { return r[cb][g * u + cj]; };
-            float hv;
             if (a.kind == 4) {
                 float zi = zv[0], zf = zv[1], zg = zv[2], zo = zv[3];
                 if (!first) { zi = zi + rec(0); zf = zf + rec(1); zg = zg + rec(2); zo = zo + rec(3); }
@@ -539,10 +527,20 @@ __global__ void __launch_bounds__(kSoloThreads) rnn_solo(RnnArgs a, int KS)
                 hv = knx_act(v, a.act, a.alpha);
             }
             hs[cb][cj] = hv;
+            hreg = hv;
             if (a.ret_seq) a.dst[((size_t)cb * T + t) * a.stride + cj] = hv;
             else if (step + 1 == T) a.dst[(size_t)cb * a.stride + cj] = hv;
         }
-        __syncthreads();  // h_t complete in LDS
+        if (I8 && step + 1 < T) {
+            // the row maxima of h_t (|h| as bits: NaN above +inf above every finite value) for the next step's
+            // quantization: per wave and row, then one LDS atomic per wave
+            const unsigned mb = __float_as_uint(hv) & 0x7fffffffu;
+            for (int rb = 0; rb < B; ++rb) {
+                const unsigned v = lane_group_max(cell && cb == rb ? mb : 0u, 64);
+                if (lane == 0 && v != 0u) atomicMax(&rmx[step & 1][rb], v);
+            }
+        }
+        __syncthreads();  // h_t (and its row maxima) complete in LDS
     }
 }
 
