@@ -127,10 +127,11 @@ static int upload_step(kernix_step* s, void* stream)
     case KERNIX_OP_LSTM:
     case KERNIX_OP_GRU:
     case KERNIX_OP_RNN:
-        if (up_t(&d->w, s->w, stream) || up_f(&d->bias, s->bias, nb, stream) || up_q(&d->q, &d->qscale, s->q, stream) ||
+        /* the input weight as gates·u × in (K-contiguous: the input projection runs on the NT GEMM kernels) */
+        if (up_tT(&d->w, s->w, stream) || up_f(&d->bias, s->bias, nb, stream) || up_q(&d->q, &d->qscale, s->q, stream) ||
             up_f(&d->rec, s->rec, (size_t)s->out * gu, stream))
             return -1;
-        if (s->dirs == 2 && (up_t(&d->w_b, s->w_b, stream) || up_f(&d->bias_b, s->bias_b, nb, stream) ||
+        if (s->dirs == 2 && (up_tT(&d->w_b, s->w_b, stream) || up_f(&d->bias_b, s->bias_b, nb, stream) ||
                              up_q(&d->q_b, &d->qscale_b, s->q_b, stream) || up_f(&d->rec_b, s->rec_b, (size_t)s->out * gu, stream)))
             return -1;
         if (s->dirs == 2 && s->merge == KERNIX_MERGE_AVE) {
@@ -572,7 +573,8 @@ static int run_rnn_dir(const kernix_model* m, kernix_step* s, int dir, const flo
     /* both directions use the step's one int8 scratch (xq_rows rows): they run one after the other on one stream */
     int8_t* xq = d->xq;
     float* sx = d->sx;
-    if (hip_ok(knx_hip_sgemm_ep(x->row, gu, s->in, x->tensor, s->in, W, gu, bias, -1, 0.0f, zx, gu, st), "RNN input projection")) return -1;
+    if (hip_ok(knx_hip_sgemm_nt_ep(x->row, gu, s->in, x->tensor, s->in, W, s->in, bias, -1, 0.0f, zx, gu, st), "RNN input projection"))
+        return -1;
     const int i8 = q != NULL && (m->int8_mode == KERNIX_INT8_I8 || B <= KERNIX_INT8_MAX_ROWS);
     if (rnn_persistent(m) && knx_hip_rnn_recurrence_fits(kind, B, u, i8)) {
         /* every timestep in one launch; h alternates between h and the recurrent-term buffer (B rows of u4 each) */
