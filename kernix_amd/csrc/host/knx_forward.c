@@ -127,7 +127,9 @@ static int upload_step(kernix_step* s, void* stream)
     case KERNIX_OP_LSTM:
     case KERNIX_OP_GRU:
     case KERNIX_OP_RNN:
-        /* the input weight as gates·u × in (K-contiguous: the input projection runs on the NT GEMM kernels) */
+        /* the input weight as gates·u × in (K-contiguous: the input projection runs on the NT GEMM kernels); a float U
+         * stays u × gates·u as in the file, the layout whose columns the single-workgroup recurrence loads coalesced
+         * (its transposed copy made every lane read a row of its own: LSTM batch 1 71 → 91 µs) */
         if (up_tT(&d->w, s->w, stream) || up_f(&d->bias, s->bias, nb, stream) || up_q(&d->q, &d->qscale, s->q, stream) ||
             up_f(&d->rec, s->rec, (size_t)s->out * gu, stream))
             return -1;
