@@ -422,9 +422,30 @@ __global__ void __launch_bounds__(kSoloThreads) rnn_solo(RnnArgs a, int KS)
     if (tid < 2 * kSoloRows) (&rmx[0][0])[tid] = 0u;
     float uf[I8 ? 4 : REGS];
     int uq[I8 ? REGS : 4];
+    // int8: the column's bytes 16 at a time where the rows allow it (kp a multiple of 16, q 16-byte aligned; a slice
+    // starts at a multiple of 16 bytes), bytes past u masked; else one byte at a time
+    const bool vec16 = I8 && a.kp % 16 == 0 && ((uintptr_t)a.q & 15) == 0;
+    if (I8 && vec16) {
+        const int8_t* row = a.q + (size_t)cc * a.kp;
+#pragma unroll
+        for (int i4 = 0; i4 < REGS / 4; ++i4) {
+            const int w0 = k0 + 4 * i4;
+            int4 v = make_int4(0, 0, 0, 0);
+            if (w0 < uw4) v = *reinterpret_cast<const int4*>(row + 4 * w0);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int w = w0 + j, left = u - 4 * w;  // bytes of word w inside u
+                unsigned x = (unsigned)(&v.x)[j];
+                if (left <= 0) x = 0u;
+                else if (left < 4) x &= (1u << (8 * left)) - 1u;
+                uq[4 * i4 + j] = (int)x;
+            }
+        }
+    }
 #pragma unroll
     for (int i = 0; i < REGS; ++i) {
         if (I8) {
+            if (vec16) continue;
             const int w = k0 + i;
             unsigned v = 0;
             if (w < uw4) {
