@@ -265,10 +265,12 @@ KNX_API int knx_hip_rnn_gates(int kind, int act, float alpha, int B, int u, int 
  * dir 1 runs t = T−1 … 0.  Output: ret_seq: the state of timestep t of sample b at dst + (b·T + t)·stride, else the
  * last state at dst + b·stride.  h0, h1: B rows of ⌈u/4⌉·4 floats each, 16-byte aligned (scratch); scratch: 8 bytes,
  * 256-byte aligned, a multiple
- * of 256 as the chain's barrier words (the chain and this kernel may share them); status as for knx_hip_linear_chain
- * (the launch's workgroups, at most 64, must all be resident).  Shapes knx_hip_rnn_recurrence_fits rejects
- * (B > 64, u > 2048 beyond one workgroup's reach, a weight slice or h that does not fit the workgroup's LDS) are
- * KNX_EINVAL. */
+ * of 256 as the chain's barrier words (the chain and this kernel may share them); status as for knx_hip_linear_chain.
+ * Where U fits one workgroup's registers (gates·u ≤ 1024; LSTM and GRU up to 128 units) the batch rows are split over
+ * workgroups that each run their rows alone (any B; h0, h1, scratch and status are not touched); otherwise the units are
+ * split over a grid of at most 64 workgroups, which must all be resident, with a barrier per timestep.  Shapes
+ * knx_hip_rnn_recurrence_fits rejects (neither form: B > 64 on the grid, u > 2048, a weight slice or h that does not
+ * fit the workgroup's LDS) are KNX_EINVAL. */
 KNX_API int knx_hip_rnn_recurrence_fits(int kind, int B, int u, int i8);
 KNX_API int knx_hip_rnn_recurrence(int kind, int act, float alpha, int B, int T, int u, int dir, const float* zx,
                                    const float* U, int u_nt, const int8_t* q, int kp, const float* qscale,

@@ -17,6 +17,9 @@
 //      pairs, writes h_t (at device scope, for the other workgroups) and the output;
 //   4. waits at a grid barrier (knx_grid.hpp: one 64-bit word, every barrier adds 256; at most 64 workgroups, all
 //      resident).
+// Where one workgroup can hold all of U (rnn_solo, below) the batch is split over workgroups instead, each running
+// its rows' timesteps alone: the rows of a recurrence never meet, so nothing is exchanged and nothing synchronizes
+// across workgroups.
 // The int8 results are the bits of the per-timestep path (same quantizer, exact int32 sums, same epilogue and cell
 // order); fp32 sums run in this kernel's own order.
 #include <float.h>
@@ -25,6 +28,7 @@
 
 #include "knx_common.hpp"
 #include "knx_grid.hpp"
+#include "knx_pipe.hpp"
 
 namespace {
 
@@ -387,21 +391,32 @@ __global__ void __launch_bounds__(kThreads) rnn_recurrence(RnnArgs a)
     }
 }
 
-// ---- one workgroup for the whole recurrence (B ≤ 2: batch 1, and the reference's int8 dispatch at ≤ 2 rows) ----
-// With a few rows the per-timestep work is tiny and the cost of a multi-workgroup step is its round trips through
-// memory (h stores, the barrier, h reloads).  One workgroup of 1024 threads keeps all of U in registers — thread t owns
+// ---- the batch split over workgroups, each running the whole recurrence of its rows ----
+// The rows of a recurrence never meet (h, its int8 row scale and the cells are per row), so a workgroup that holds all
+// of U runs its rows' timesteps alone: no h exchange through memory and no barrier across workgroups, whose round trips
+// are the cost of a multi-workgroup step at these sizes, and no workgroup waits for another (nothing needs to be
+// resident together).  One workgroup of 1024 threads keeps all of U in registers — thread t owns
 // column c = t / KS and its k-slice [s·KSL, (s+1)·KSL), s = t % KS, KS lanes per column (consecutive lanes, so their
 // partial sums are reduced by exchanges; the lanes of one slice read the same h values, 16 bytes at a time) — and h in
 // LDS, so a timestep is two workgroup barriers and no global synchronization (three with int8 arithmetic).  Same
 // quantizer, int32 sums, epilogue and cells as above; with int8 arithmetic the cells that write h_t also gather its
 // row maxima (per wave, then one LDS atomic per wave and row), and at the next step every cell quantizes its own value
 // with its row's scale, so the quantization is one multiply-and-round per thread instead of a pass over the rows.
+// Barrier for the LDS hand-offs of a timestep (h, its int8 rows, the recurrent terms, the row maxima): this wave's LDS
+// accesses retired, then s_barrier.  __syncthreads would also wait for the wave's global stores (the output h) and
+// loads (the next timestep's gate inputs), which no other wave reads.
+__device__ __forceinline__ void lds_barrier()
+{
+    KNX_WAIT_LDS();
+    knx_barrier_nofence();
+}
+
 constexpr int kSoloThreads = 1024;
 constexpr int kSoloRegs = 64;   // U values per thread (fp32; int8: kSoloRegs / 2 words of four values)
 constexpr int kSoloRows = 2;
 
 template <bool I8, int KIND, int ACT>
-__global__ void __launch_bounds__(kSoloThreads) rnn_solo(RnnArgs a, int KS)
+__global__ void __launch_bounds__(kSoloThreads) rnn_solo(RnnArgs a, int KS, int R)
 {
     const int act = ACT == kActAny ? a.act : ACT;
     __shared__ __attribute__((aligned(16))) float hs[kSoloRows][2048];  // h_{t−1}, fp32 (u ≤ 2048), zero past u
@@ -410,7 +425,11 @@ __global__ void __launch_bounds__(kSoloThreads) rnn_solo(RnnArgs a, int KS)
     __shared__ unsigned rmx[2][kSoloRows];  // int8: each row's max |h| as bits, by the parity of the step that wrote h
     __shared__ float r[kSoloRows][kSoloThreads];                        // recurrent terms (gates·u ≤ 1024)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int B = a.B, T = a.T, u = a.u, gu = a.gu, G = a.gates, uw4 = (u + 3) / 4;
+    // this workgroup's rows of the batch: [row0, row0 + B) (the rows of a recurrence never meet)
+    const int row0 = blockIdx.x * R;
+    const int B = min(R, a.B - row0), T = a.T, u = a.u, gu = a.gu, G = a.gates, uw4 = (u + 3) / 4;
+    const float* zx = a.zx + (size_t)row0 * T * gu;
+    float* dst = a.dst + (size_t)row0 * (a.ret_seq ? (size_t)T * a.stride : (size_t)a.stride);
     const int c = tid / KS, ks = tid % KS;
     const bool active = c < gu;
     const int cc = active ? c : gu - 1;
@@ -470,7 +489,7 @@ __global__ void __launch_bounds__(kSoloThreads) rnn_solo(RnnArgs a, int KS)
     auto load_z = [&](int st, float (&z)[4]) {
         const int tt = a.dir ? T - 1 - st : st;
 #pragma unroll
-        for (int g = 0; g < 4; ++g) z[g] = cell && g < G ? a.zx[((size_t)cb * T + tt) * gu + (size_t)g * u + cj] : 0.0f;
+        for (int g = 0; g < 4; ++g) z[g] = cell && g < G ? zx[((size_t)cb * T + tt) * gu + (size_t)g * u + cj] : 0.0f;
     };
     float zn[4];
     load_z(0, zn);
@@ -497,16 +516,18 @@ __global__ void __launch_bounds__(kSoloThreads) rnn_solo(RnnArgs a, int KS)
                     reinterpret_cast<int8_t*>(&hq[cb][0])[cj] = (int8_t)(int)qv;
                 }
                 if (tid < B) rmx[step & 1][tid] = 0u;
-                __syncthreads();
+                lds_barrier();
             }
             for (int b = 0; b < B; ++b) {
                 float v;
                 if (I8) {
                     int acc = 0;
+                    // a slice that starts inside u is read whole (its words past u are zero in hq and in uq, and it
+                    // ends inside the 512-word row: k0 is a multiple of REGS), so its loads go out together
                     const int4* hrow = reinterpret_cast<const int4*>(&hq[b][k0]);
 #pragma unroll
                     for (int i = 0; i < REGS / 4; ++i) {
-                        if (k0 + 4 * i >= uw4) break;  // past u: zero words
+                        if (k0 >= uw4) break;  // the whole slice past u
                         const int4 hv = hrow[i];
                         acc = __builtin_amdgcn_sdot4(hv.x, uq[4 * i], acc, false);
                         acc = __builtin_amdgcn_sdot4(hv.y, uq[4 * i + 1], acc, false);
@@ -518,10 +539,11 @@ __global__ void __launch_bounds__(kSoloThreads) rnn_solo(RnnArgs a, int KS)
                     v = v * col_scale;
                 } else {
                     v = 0.0f;
+                    // as above: zeros past u in hs and uf, the slice inside the 2048-float row
                     const float4* hrow = reinterpret_cast<const float4*>(&hs[b][k0]);
 #pragma unroll
                     for (int i = 0; i < REGS / 4; ++i) {
-                        if (k0 + 4 * i >= u) break;  // past u: zeros
+                        if (k0 >= u) break;  // the whole slice past u
                         const float4 hv = hrow[i];
                         v = fmaf(hv.x, uf[4 * i], v);
                         v = fmaf(hv.y, uf[4 * i + 1], v);
@@ -534,7 +556,7 @@ __global__ void __launch_bounds__(kSoloThreads) rnn_solo(RnnArgs a, int KS)
                 if (active && ks == 0) r[b][c] = v;
             }
         }
-        __syncthreads();  // r complete; every read of hs done
+        lds_barrier();  // r complete; every read of hs done
         float hv = 0.0f;
         if (cell) {
             const bool first = step == 0;
@@ -555,8 +577,8 @@ __global__ void __launch_bounds__(kSoloThreads) rnn_solo(RnnArgs a, int KS)
             }
             hs[cb][cj] = hv;
             hreg = hv;
-            if (a.ret_seq) a.dst[((size_t)cb * T + t) * a.stride + cj] = hv;
-            else if (step + 1 == T) a.dst[(size_t)cb * a.stride + cj] = hv;
+            if (a.ret_seq) dst[((size_t)cb * T + t) * a.stride + cj] = hv;
+            else if (step + 1 == T) dst[(size_t)cb * a.stride + cj] = hv;
         }
         if (I8 && step + 1 < T) {
             // the row maxima of h_t (|h| as bits: NaN above +inf above every finite value) for the next step's
@@ -567,16 +589,23 @@ __global__ void __launch_bounds__(kSoloThreads) rnn_solo(RnnArgs a, int KS)
                 if (lane == 0 && v != 0u) atomicMax(&rmx[step & 1][rb], v);
             }
         }
-        __syncthreads();  // h_t (and its row maxima) complete in LDS
+        lds_barrier();  // h_t (and its row maxima) complete in LDS
     }
 }
 
-// lanes per column of the single-workgroup kernel: the most (a power of two ≤ 64) that the 1024 threads hold, if
-// each lane's slice of its column then fits the registers; else 0 (no single-workgroup kernel for the shape)
+// rows per workgroup of the row-split kernel: one while there is a CU for every row (a workgroup's timestep grows with
+// its rows), two above
+int solo_rows(int B)
+{
+    return B <= 256 ? 1 : kSoloRows;
+}
+
+// lanes per column of the row-split kernel: the most (a power of two ≤ 64) that the 1024 threads hold, if each lane's
+// slice of its column then fits the registers; else 0 (no row-split kernel for the shape)
 int solo_lanes(int B, int gu, int u, bool i8)
 {
-    if (B > kSoloRows || (long)B * u > kSoloThreads || u > 2048 || gu > kSoloThreads) return 0;
-    const char* e = getenv("KNX_RNN_SOLO");  // 0: the multi-workgroup kernel for every shape (tests, tuning)
+    if ((long)solo_rows(B) * u > kSoloThreads || u > 2048 || gu > kSoloThreads) return 0;
+    const char* e = getenv("KNX_RNN_SOLO");  // 0: the grid kernel wherever it fits (tests, tuning)
     if (e != nullptr && *e == '0') return 0;
     int ks = 1;
     while (ks < 64 && (long)gu * ks * 2 <= kSoloThreads) ks *= 2;
@@ -599,13 +628,15 @@ int units_per_wg(int B, int u, int gates)
     return uw;
 }
 
-// one launch of the instantiation for (I8, KIND, ACT): the single-workgroup kernel when ks > 0, else the grid of G
+// one launch of the instantiation for (I8, KIND, ACT): the row-split kernel when ks > 0, else the grid of G
 // workgroups with lds bytes of dynamic LDS (its limit raised once per instantiation)
 template <bool I8, int KIND, int ACT>
 int launch_rnn(const RnnArgs& a, int ks, int G, size_t lds, hipStream_t s, const char* name)
 {
     if (ks > 0) {
-        hipLaunchKernelGGL((rnn_solo<I8, KIND, ACT>), dim3(1), dim3(kSoloThreads), 0, s, a, ks);
+        const int R = solo_rows(a.B);
+        hipLaunchKernelGGL((rnn_solo<I8, KIND, ACT>), dim3((unsigned)((a.B + R - 1) / R)), dim3(kSoloThreads), 0, s, a,
+                           ks, R);
         return knx::check_launch(name);
     }
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&rnn_recurrence<I8, KIND, ACT>),
@@ -633,10 +664,10 @@ int launch_kind(const RnnArgs& a, int ks, int G, size_t lds, hipStream_t s, cons
 
 extern "C" int knx_hip_rnn_recurrence_fits(int kind, int B, int u, int i8)
 {
-    if ((kind != 4 && kind != 5 && kind != 6) || B < 1 || B > 64 || u < 1 || u > 65536) return 0;
+    if ((kind != 4 && kind != 5 && kind != 6) || B < 1 || u < 1 || u > 65536) return 0;
     const int gates = kind == 4 ? 4 : kind == 5 ? 3 : 1;
     if (solo_lanes(B, gates * u, u, i8 != 0) > 0) return 1;
-    if (u > kMaxUnits) return 0;
+    if (B > 64 || u > kMaxUnits) return 0;
     const int uw = units_per_wg(B, u, gates);
     if ((u + uw - 1) / uw > kMaxGrid || B * uw > kThreads * kMaxPairs) return 0;
     return lds_layout(B, gates, uw, k_extent(u, i8 != 0), i8 != 0, !i8 || kind == 5).total <= kMaxLds ? 1 : 0;

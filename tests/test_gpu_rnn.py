@@ -1,6 +1,7 @@
-"""The persistent RNN recurrence (knx_hip_rnn_recurrence: every timestep of a direction in one launch; one workgroup
-at <= 2 rows, a grid of workgroups with a barrier per timestep above, KNX_RNN_SOLO=0 forcing the latter) against the
-per-timestep launches (KNX_RNN_PERSISTENT=0) and the oracle (reference kernix_rnn_dir, include/kernix_model.h:563-632).
+"""The persistent RNN recurrence (knx_hip_rnn_recurrence: every timestep of a direction in one launch; the batch
+rows split over workgroups that each hold all of U where it fits, else a grid of workgroups splitting the units with a
+barrier per timestep, KNX_RNN_SOLO=0 forcing the latter) against the per-timestep launches (KNX_RNN_PERSISTENT=0) and
+the oracle (reference kernix_rnn_dir, include/kernix_model.h:563-632).
 
 Where the recurrence runs int8 arithmetic (int8 recurrent weights in i8 mode, or at <= 2 rows in the reference's
 dispatch) both paths quantize the same rows with the quantizer's operations and sum exactly in int32, so they give the
@@ -67,12 +68,27 @@ def test_persistent_matches_per_step_and_oracle(tmp_path, monkeypatch, case, int
         assert rel_err(got, per_step) <= 1e-5, (cell, dirs, units, batch, mode)
     want, _ = knx_ref.forward(knx_ref.parse(p), x.reshape(-1, fin), mode=mode)
     assert rel_err(got.reshape(want.shape), want) <= (1e-2 if int8_rec else 1e-4)
-    if batch <= 2:  # the single-workgroup kernel above; the multi-workgroup one at the same shape
-        multi = forward(p, x, mode, monkeypatch, True, solo=False)
-        if int8_rec:
-            assert np.array_equal(multi, got)
-        else:
-            assert rel_err(multi, got) <= 1e-5
+    # the grid form at the same shape (the per-timestep path where it does not fit)
+    multi = forward(p, x, mode, monkeypatch, True, solo=False)
+    if int8_rec:
+        assert np.array_equal(multi, got)
+    else:
+        assert rel_err(multi, got) <= 1e-5
+
+
+@pytest.mark.parametrize("int8,mode", [(False, "ref"), (True, "i8")])
+def test_persistent_two_rows_per_workgroup(tmp_path, monkeypatch, int8, mode):
+    """above 256 rows each workgroup of the row split takes two rows: against the per-timestep path and the oracle"""
+    p = str(tmp_path / "w.knx")
+    x = configs.lstm(p, seed=9, batch=300, T=5, fin=12, units=40, int8=int8)
+    got = forward(p, x, mode, monkeypatch, True)
+    per_step = forward(p, x, mode, monkeypatch, False)
+    if int8:
+        assert np.array_equal(got, per_step)
+    else:
+        assert rel_err(got, per_step) <= 1e-5
+    want, _ = knx_ref.forward(knx_ref.parse(p), x.reshape(-1, 12), mode=mode)
+    assert rel_err(got.reshape(want.shape), want) <= (1e-2 if int8 else 1e-4)
 
 
 def test_persistent_returns_sequences_and_nan_rows(tmp_path, monkeypatch):
@@ -109,17 +125,19 @@ def test_recurrence_entry_point_rejects(monkeypatch):
     L = hipabi.lib()
     hipabi.check(L.knx_hip_init())
     assert L.knx_hip_rnn_recurrence_fits(4, 64, 128, 0) == 1
-    assert L.knx_hip_rnn_recurrence_fits(4, 65, 128, 0) == 0  # more than 64 rows: the per-timestep path
+    assert L.knx_hip_rnn_recurrence_fits(4, 1000, 128, 0) == 1  # U fits a workgroup: the rows split, any batch
+    assert L.knx_hip_rnn_recurrence_fits(4, 65, 256, 0) == 0  # neither form: the per-timestep path
+    assert L.knx_hip_rnn_recurrence_fits(4, 64, 256, 0) == 1  # the grid form
     assert L.knx_hip_rnn_recurrence_fits(7, 1, 128, 0) == 0
     assert L.knx_hip_rnn_recurrence_fits(4, 64, 4096, 0) == 0  # h does not fit a workgroup's LDS
 
 
-@pytest.mark.parametrize("batch,expect", [(1, True), (64, True), (65, False)])
-def test_forward_uses_the_persistent_recurrence(tmp_path, monkeypatch, batch, expect):
+@pytest.mark.parametrize("batch,units,expect", [(1, 32, True), (64, 32, True), (65, 32, True), (65, 256, False)])
+def test_forward_uses_the_persistent_recurrence(tmp_path, monkeypatch, batch, units, expect):
     """the forward takes the one-launch recurrence wherever it fits (an injected failure of that entry point fails the
     forward) and the per-timestep launches otherwise or with KNX_RNN_PERSISTENT=0"""
     p = str(tmp_path / "l.knx")
-    x = configs.lstm(p, batch=batch, T=4, fin=16, units=32)
+    x = configs.lstm(p, batch=batch, T=4, fin=16, units=units)
     monkeypatch.setenv("KNX_HIP_FAIL", "knx_hip_rnn_recurrence")
     m = Model(p)
     try:
@@ -137,12 +155,12 @@ def test_forward_uses_the_persistent_recurrence(tmp_path, monkeypatch, batch, ex
 
 
 def test_recurrence_that_stopped_waiting_is_recomputed(tmp_path, monkeypatch):
-    """with a poll limit of 0 (forced from the host) every workgroup but the last to reach a timestep's barrier stops
-    waiting and sets the model's status word; the forward is then recomputed one launch per timestep, so the result
-    is the per-timestep path's, bit for bit (int8 recurrence)"""
+    """with a poll limit of 0 (forced from the host) every workgroup of the grid form but the last to reach a
+    timestep's barrier stops waiting and sets the model's status word; the forward is then recomputed one launch per
+    timestep, so the result is the per-timestep path's, bit for bit (int8 recurrence)"""
     p = str(tmp_path / "g.knx")
     x = configs.lstm(p, seed=3, batch=16, T=6, fin=16, units=64, int8=True)
     want = forward(p, x, "i8", monkeypatch, False)
     monkeypatch.setenv("KNX_GRID_SPIN", "0")
-    got = forward(p, x, "i8", monkeypatch, True)
+    got = forward(p, x, "i8", monkeypatch, True, solo=False)
     assert np.array_equal(got, want)
