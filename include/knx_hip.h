@@ -254,7 +254,8 @@ KNX_API int knx_hip_pad(const float* x, float* y, int B, int H, int W, int C, in
 KNX_API int knx_hip_upsample(const float* x, float* y, int B, int H, int W, int C, int sh, int sw, void* stream);
 /* y[i] = table[id] for integral id in [0, V), else a NaN row; n ids, D floats per row. */
 KNX_API int knx_hip_embedding(const float* ids, int n, const float* table, int V, int D, float* y, void* stream);
-/* RNN gate update for one timestep (see the definition for the exact per-kind formulas). */
+/* RNN gate update for one timestep (see the definition for the exact per-kind formulas; the cells' sigmoid and tanh
+ * on the hardware exp2 and reciprocal, ≤ 1-2 ulp each, as in knx_hip_rnn_recurrence). */
 KNX_API int knx_hip_rnn_gates(int kind, int act, float alpha, int B, int u, int first_step, float* z, const float* zh,
                               float* c, float* h, float* dst, int dst_stride, void* stream);
 /* The recurrence of one RNN direction over T timesteps as one launch (reference include/kernix_model.h:563-632,

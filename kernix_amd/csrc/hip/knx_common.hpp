@@ -75,26 +75,40 @@ __device__ __forceinline__ float knx_act(float x, int act, float alpha)
     }
 }
 
+// The recurrent cells' sigmoid and tanh on the hardware exp2 and reciprocal (≤ 1-2 ulp each, as the GELU above): with
+// libm expf / tanhf and IEEE divisions an LSTM cell is some 150 instructions, and the cells are the serial part of every
+// timestep.  sigmoid(x) = 1 / (1 + 2^(−x·log2 e)); tanh(x) = 1 − 2 / (1 + 2^(2x·log2 e)), ±1 at the extremes, an absolute
+// error of ≈ 1e-7 near 0.  The other activations of a cell stay those of knx_act.
+__device__ __forceinline__ float knx_gate_sigmoid(float x)
+{
+    return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.44269504f));
+}
+__device__ __forceinline__ float knx_gate_act(float x, int act, float alpha)
+{
+    if (act == 4) return 1.0f - 2.0f * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * 2.88539008f));
+    return knx_act(x, act, alpha);
+}
+
 // Recurrent cells on the summed gate inputs (x·W + b + h·U; reference include/kernix_model.h:595-626), shared by the
 // per-timestep gates kernel and the persistent recurrence so that both give the same bits.
 // LSTM (gates i, f, g, o): c = f·c + i·g (c = i·g at the first step), h = o·act(c).
 __device__ __forceinline__ float knx_lstm_cell(float zi, float zf, float zg, float zo, int act, float alpha, bool step0,
                                                float& c)
 {
-    const float ig = knx_act(zi, 3, 0.0f), fg = knx_act(zf, 3, 0.0f), gg = knx_act(zg, act, alpha);
-    const float og = knx_act(zo, 3, 0.0f);
+    const float ig = knx_gate_sigmoid(zi), fg = knx_gate_sigmoid(zf), gg = knx_gate_act(zg, act, alpha);
+    const float og = knx_gate_sigmoid(zo);
     float cv = step0 ? ig * gg : fg * c;
     if (!step0) cv = ig * gg + cv;
     c = cv;
-    return knx_act(cv, act, alpha) * og;
+    return knx_gate_act(cv, act, alpha) * og;
 }
 // GRU (reset after; gates z, r, h~): x* the input side, h* the recurrent side with its bias; h = z·(h − h~) + h~.
 __device__ __forceinline__ float knx_gru_cell(float xz, float xr, float xh, float hz, float hr, float hh_in, int act,
                                               float alpha, bool step0, float prev)
 {
-    const float zg = knx_act(xz + hz, 3, 0.0f);
-    const float rg = knx_act(xr + hr, 3, 0.0f);
-    const float hh = knx_act(rg * hh_in + xh, act, alpha);
+    const float zg = knx_gate_sigmoid(xz + hz);
+    const float rg = knx_gate_sigmoid(xr + hr);
+    const float hh = knx_gate_act(rg * hh_in + xh, act, alpha);
     return step0 ? (-hh) * zg + hh : (prev - hh) * zg + hh;
 }
 

@@ -381,7 +381,7 @@ __global__ void __launch_bounds__(kThreads) rnn_recurrence(RnnArgs a)
             } else {
                 float v = zv[i][0];
                 if (!first) v = v + rec(0);
-                hv = knx_act(v, act, a.alpha);
+                hv = knx_gate_act(v, act, a.alpha);
             }
             if (step + 1 < T) __hip_atomic_store(hout + (size_t)b * ldh + j, hv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (a.ret_seq) a.dst[((size_t)b * T + t) * a.stride + j] = hv;
@@ -573,7 +573,7 @@ __global__ void __launch_bounds__(kSoloThreads) rnn_solo(RnnArgs a, int KS, int 
             } else {
                 float v = zv[0];
                 if (!first) v = v + rec(0);
-                hv = knx_act(v, act, a.alpha);
+                hv = knx_gate_act(v, act, a.alpha);
             }
             hs[cb][cj] = hv;
             hreg = hv;

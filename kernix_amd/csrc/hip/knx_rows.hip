@@ -488,7 +488,7 @@ __global__ void __launch_bounds__(256) rnn_gates_kernel(int kind, int act, float
         } else {
             float v = z[(size_t)b * u + j];
             if (hu) v = v + hu[(size_t)b * u + j];
-            const float hv = knx_act(v, act, alpha);
+            const float hv = knx_gate_act(v, act, alpha);
             h[i] = hv;
             if (dst) dst[(size_t)b * dst_stride + j] = hv;
         }
