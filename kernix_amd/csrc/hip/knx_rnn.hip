@@ -395,10 +395,12 @@ __global__ void __launch_bounds__(kThreads) rnn_recurrence(RnnArgs a)
 // The rows of a recurrence never meet (h, its int8 row scale and the cells are per row), so a workgroup that holds all
 // of U runs its rows' timesteps alone: no h exchange through memory and no barrier across workgroups, whose round trips
 // are the cost of a multi-workgroup step at these sizes, and no workgroup waits for another (nothing needs to be
-// resident together).  One workgroup of 1024 threads keeps all of U in registers — thread t owns
-// column c = t / KS and its k-slice [s·KSL, (s+1)·KSL), s = t % KS, KS lanes per column (consecutive lanes, so their
-// partial sums are reduced by exchanges; the lanes of one slice read the same h values, 16 bytes at a time) — and h in
-// LDS, so a timestep is two workgroup barriers and no global synchronization (three with int8 arithmetic).  Same
+// resident together).  One workgroup of 1024 threads keeps all of U in registers and h in LDS, so a timestep is two
+// workgroup barriers and no global synchronization (three with int8 arithmetic).  fp32: thread t owns column
+// c = t / KS and its 64-value k-slice s = t % KS, KS lanes per column (consecutive lanes, so their partial sums are
+// reduced by exchanges; the lanes of one slice read the same h values, 16 bytes at a time), FMAs on the VALU.  int8:
+// the products on the matrix cores, the rows of h as the rows of A of v_mfma_i32_16x16x64_i8 (one or two of its 16:
+// at u = 128 a wave still needs only four per timestep, against 32 dot4 instructions per lane and the reduction).  Same
 // quantizer, int32 sums, epilogue and cells as above; with int8 arithmetic the cells that write h_t also gather its
 // row maxima (per wave, then one LDS atomic per wave and row), and at the next step every cell quantizes its own value
 // with its row's scale, so the quantization is one multiply-and-round per thread instead of a pass over the rows.
@@ -414,6 +416,8 @@ __device__ __forceinline__ void lds_barrier()
 constexpr int kSoloThreads = 1024;
 constexpr int kSoloRegs = 64;   // U values per thread (fp32; int8: kSoloRegs / 2 words of four values)
 constexpr int kSoloRows = 2;
+constexpr int kSoloBlocks = 2;  // int8: 16-column blocks per wave (gates·u ≤ 512)
+constexpr int kSoloChunks = 2;  // int8: 64-byte k-chunks (u ≤ 128); 4 × 4 fragments spilled registers
 
 template <bool I8, int KIND, int ACT>
 __global__ void __launch_bounds__(kSoloThreads) rnn_solo(RnnArgs a, int KS, int R)
@@ -427,59 +431,66 @@ __global__ void __launch_bounds__(kSoloThreads) rnn_solo(RnnArgs a, int KS, int 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     // this workgroup's rows of the batch: [row0, row0 + B) (the rows of a recurrence never meet)
     const int row0 = blockIdx.x * R;
-    const int B = min(R, a.B - row0), T = a.T, u = a.u, gu = a.gu, G = a.gates, uw4 = (u + 3) / 4;
+    const int B = min(R, a.B - row0), T = a.T, u = a.u, gu = a.gu, G = a.gates;
     const float* zx = a.zx + (size_t)row0 * T * gu;
     float* dst = a.dst + (size_t)row0 * (a.ret_seq ? (size_t)T * a.stride : (size_t)a.stride);
+    // fp32: thread t owns column c = t / KS and its k-slice [k0, k0 + 64), KS lanes per column
     const int c = tid / KS, ks = tid % KS;
     const bool active = c < gu;
     const int cc = active ? c : gu - 1;
-    constexpr int REGS = I8 ? kSoloRegs / 2 : kSoloRegs;
-    const int k0 = ks * REGS;  // first k (fp32) or word (int8) of this lane's slice
-    // this thread's part of U; h is zero past u, so the slice runs over whole 16-byte groups
+    constexpr int REGS = kSoloRegs;
+    const int k0 = ks * REGS;
+    // int8: the products on the matrix cores (v_mfma_i32_16x16x64_i8, rows of h in the rows of A): wave w owns the
+    // 16-column blocks w, w + 16, …; lane (fr, fq) holds bytes 64·kc + 16·fq … + 15 of column 16·block + fr
+    const int fr = lane & 15, fq = lane >> 4;
+    const int nb = (gu + 15) / 16, nkc = (u + 63) / 64;
     for (int e = tid; e < kSoloRows * 2048; e += kSoloThreads) (&hs[0][0])[e] = 0.0f;
     for (int e = tid; e < kSoloRows * 512; e += kSoloThreads) (&hq[0][0])[e] = 0;
     if (tid < 2 * kSoloRows) (&rmx[0][0])[tid] = 0u;
-    float uf[I8 ? 4 : REGS];
-    int uq[I8 ? REGS : 4];
-    // int8: the column's bytes 16 at a time where the rows allow it (kp a multiple of 16, q 16-byte aligned; a slice
-    // starts at a multiple of 16 bytes), bytes past u masked; else one byte at a time
-    const bool vec16 = I8 && a.kp % 16 == 0 && ((uintptr_t)a.q & 15) == 0;
-    if (I8 && vec16) {
-        const int8_t* row = a.q + (size_t)cc * a.kp;
+    float uf[I8 ? 1 : REGS];
+    v4i ub[I8 ? kSoloBlocks : 1][I8 ? kSoloChunks : 1];
+    float csc[I8 ? kSoloBlocks : 1], cbi[I8 ? kSoloBlocks : 1];
+    if (I8) {
+        // U's bytes past u are zeroed (those of h are zero too); rows of kp bytes, kp ≥ u rounded up to 4: 16 bytes at
+        // a time where kp is a multiple of 16 and q 16-byte aligned, else four words
+        const bool vec16 = a.kp % 16 == 0 && ((uintptr_t)a.q & 15) == 0;
 #pragma unroll
-        for (int i4 = 0; i4 < REGS / 4; ++i4) {
-            const int w0 = k0 + 4 * i4;
-            int4 v = make_int4(0, 0, 0, 0);
-            if (w0 < uw4) v = *reinterpret_cast<const int4*>(row + 4 * w0);
+        for (int i = 0; i < kSoloBlocks; ++i) {
+            const int n = 16 * (wave + 16 * i) + fr;
+            const bool col = n < gu;
+            csc[i] = col ? a.qs[n] : 0.0f;
+            cbi[i] = col && a.brec ? a.brec[n] : 0.0f;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int w = w0 + j, left = u - 4 * w;  // bytes of word w inside u
-                unsigned x = (unsigned)(&v.x)[j];
-                if (left <= 0) x = 0u;
-                else if (left < 4) x &= (1u << (8 * left)) - 1u;
-                uq[4 * i4 + j] = (int)x;
+            for (int kc = 0; kc < kSoloChunks; ++kc) {
+                const int kb = 64 * kc + 16 * fq;  // this lane's first byte
+                v4i v = {0, 0, 0, 0};
+                if (col && kb < u) {
+                    const int8_t* src = a.q + (size_t)n * a.kp + kb;
+                    if (vec16) {
+                        v = *reinterpret_cast<const v4i*>(src);
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < 4; ++j)
+                            if (kb + 4 * j < u) v[j] = *reinterpret_cast<const int*>(src + 4 * j);
+                    }
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const int left = u - (kb + 4 * j);  // bytes of word j inside u
+                        if (left <= 0) v[j] = 0;
+                        else if (left < 4) v[j] &= (int)((1u << (8 * left)) - 1u);
+                    }
+                }
+                ub[i][kc] = v;
             }
         }
-    }
+    } else {
 #pragma unroll
-    for (int i = 0; i < REGS; ++i) {
-        if (I8) {
-            if (vec16) continue;
-            const int w = k0 + i;
-            unsigned v = 0;
-            if (w < uw4) {
-                const int8_t* src = a.q + (size_t)cc * a.kp + 4 * w;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) v |= (unsigned)(uint8_t)(4 * w + e < u ? src[e] : 0) << (8 * e);
-            }
-            uq[i] = (int)v;
-        } else {
+        for (int i = 0; i < REGS; ++i) {
             const int k = k0 + i;
             uf[i] = k < u ? (a.u_nt ? a.U[(size_t)cc * u + k] : a.U[(size_t)k * gu + cc]) : 0.0f;
         }
     }
     __syncthreads();
-    const float col_scale = I8 ? a.qs[cc] : 1.0f;
     const float col_bias = a.brec ? a.brec[cc] : 0.0f;
     // cell phase: thread tid < B·u owns row b = tid / u, unit j = tid % u
     const bool cell = tid < B * u;
@@ -518,28 +529,39 @@ __global__ void __launch_bounds__(kSoloThreads) rnn_solo(RnnArgs a, int KS, int 
                 if (tid < B) rmx[step & 1][tid] = 0u;
                 lds_barrier();
             }
-            for (int b = 0; b < B; ++b) {
-                float v;
-                if (I8) {
-                    int acc = 0;
-                    // a slice that starts inside u is read whole (its words past u are zero in hq and in uq, and it
-                    // ends inside the 512-word row: k0 is a multiple of REGS), so its loads go out together
-                    const int4* hrow = reinterpret_cast<const int4*>(&hq[b][k0]);
+            if (I8) {
+                // the rows of h_{t−1} as rows of A (rows from B on repeat row B − 1; their sums are not used), exact
+                // int32 sums in lanes fq = 0 (row b in element b), then the int8 GEMM's epilogue
+                // ((float)acc · sx) · scale (+ bias)
+                const int arow = fr < B ? fr : B - 1;
+                v4i af[kSoloChunks];
 #pragma unroll
-                    for (int i = 0; i < REGS / 4; ++i) {
-                        if (k0 >= uw4) break;  // the whole slice past u
-                        const int4 hv = hrow[i];
-                        acc = __builtin_amdgcn_sdot4(hv.x, uq[4 * i], acc, false);
-                        acc = __builtin_amdgcn_sdot4(hv.y, uq[4 * i + 1], acc, false);
-                        acc = __builtin_amdgcn_sdot4(hv.z, uq[4 * i + 2], acc, false);
-                        acc = __builtin_amdgcn_sdot4(hv.w, uq[4 * i + 3], acc, false);
+                for (int kc = 0; kc < kSoloChunks; ++kc)
+                    af[kc] = kc < nkc ? *reinterpret_cast<const v4i*>(&hq[arow][16 * kc + 4 * fq]) : v4i{0, 0, 0, 0};
+#pragma unroll
+                for (int i = 0; i < kSoloBlocks; ++i) {
+                    if (wave + 16 * i >= nb) break;
+                    v4i acc = {0, 0, 0, 0};
+#pragma unroll
+                    for (int kc = 0; kc < kSoloChunks; ++kc)
+                        if (kc < nkc) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[kc], ub[i][kc], acc, 0, 0, 0);
+                    const int n = 16 * (wave + 16 * i) + fr;
+                    if (fq == 0 && n < gu) {
+#pragma unroll
+                        for (int b = 0; b < kSoloRows; ++b) {
+                            if (b >= B) break;
+                            float v = (float)acc[b] * sxs[b];
+                            v = v * csc[i];
+                            if (a.brec) v = v + cbi[i];
+                            r[b][n] = v;
+                        }
                     }
-                    for (int off = KS / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
-                    v = (float)acc * sxs[b];  // ((float)acc · sx) · scale (+ bias), the int8 GEMM's epilogue
-                    v = v * col_scale;
-                } else {
-                    v = 0.0f;
-                    // as above: zeros past u in hs and uf, the slice inside the 2048-float row
+                }
+            } else {
+                for (int b = 0; b < B; ++b) {
+                    // a slice that starts inside u is read whole (zeros past u in hs and in uf; it ends inside the
+                    // 2048-float row, k0 being a multiple of 64), so its loads go out together
+                    float v = 0.0f;
                     const float4* hrow = reinterpret_cast<const float4*>(&hs[b][k0]);
 #pragma unroll
                     for (int i = 0; i < REGS / 4; ++i) {
@@ -551,9 +573,9 @@ __global__ void __launch_bounds__(kSoloThreads) rnn_solo(RnnArgs a, int KS, int 
                         v = fmaf(hv.w, uf[4 * i + 3], v);
                     }
                     for (int off = KS / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+                    if (a.brec) v = v + col_bias;
+                    if (active && ks == 0) r[b][c] = v;
                 }
-                if (a.brec) v = v + col_bias;
-                if (active && ks == 0) r[b][c] = v;
             }
         }
         lds_barrier();  // r complete; every read of hs done
@@ -607,10 +629,10 @@ int solo_lanes(int B, int gu, int u, bool i8)
     if ((long)solo_rows(B) * u > kSoloThreads || u > 2048 || gu > kSoloThreads) return 0;
     const char* e = getenv("KNX_RNN_SOLO");  // 0: the grid kernel wherever it fits (tests, tuning)
     if (e != nullptr && *e == '0') return 0;
+    if (i8) return u <= 64 * kSoloChunks && gu <= 16 * 16 * kSoloBlocks ? 1 : 0;  // the products on the matrix cores
     int ks = 1;
     while (ks < 64 && (long)gu * ks * 2 <= kSoloThreads) ks *= 2;
-    const int len = i8 ? (u + 3) / 4 : u;
-    return len <= ks * (i8 ? kSoloRegs / 2 : kSoloRegs) ? ks : 0;  // lane s covers [s·R, (s+1)·R)
+    return u <= ks * kSoloRegs ? ks : 0;  // lane s covers [s·64, (s+1)·64)
 }
 
 // units per workgroup: enough that the workgroup's gate columns fill a 16-wide tile of the products (LSTM 4, GRU 5,

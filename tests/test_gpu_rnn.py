@@ -13,6 +13,7 @@ import numpy as np
 import pytest
 
 from kernix_amd import configs, hipabi
+from kernix_amd.hipabi import ptr
 from kernix_amd.kernix import INT8_I8, Model
 from oracle import knx_ref
 
@@ -49,6 +50,7 @@ CASES = [
     ("LSTM", 1, 3, 5, 1),
     ("RNN", 1, 512, 8, 3),     # a row of h over 64 lanes, two float4s each (fp32 fits the LDS up to batch 17)
     ("LSTM", 1, 1000, 8, 3),   # int8 recurrences: four float4s per lane, the last row partly past u
+    ("LSTM", 1, 256, 16, 4),   # past the row-split kernel (int8 and fp32): the grid
 ]
 
 
@@ -119,6 +121,41 @@ def test_persistent_returns_sequences_and_nan_rows(tmp_path, monkeypatch):
     ok = np.isfinite(want)
     assert np.array_equal(np.isnan(got.reshape(want.shape)), ~ok)
     assert rel_err(got.reshape(want.shape)[ok], want[ok]) <= 1e-2
+
+
+@pytest.mark.parametrize("kind,u", [(4, 40), (5, 36), (6, 100)])
+def test_recurrence_int8_rows_of_any_word_pitch(kind, u):
+    """int8 recurrent weight rows of a multiple of 4 bytes but not of 16 (the C ABI allows them; the forward's rows are
+    multiples of 64 bytes) are loaded a word at a time: the bits of the same weight at a 64-byte pitch"""
+    L = hipabi.lib()
+    hipabi.check(L.knx_hip_init())
+    rng = np.random.default_rng(kind)
+    gates = {4: 4, 5: 3, 6: 1}[kind]
+    gu, B, T = gates * u, 3, 5
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    zx = dev(rng.normal(0, 1, (B * T, gu)).astype(np.float32))
+    q = rng.integers(-127, 128, (gu, u)).astype(np.int8)
+    qs = dev(rng.uniform(0.001, 0.01, gu).astype(np.float32))
+    brec = dev(rng.normal(0, 0.1, gu).astype(np.float32)) if kind == 5 else None
+    u4 = (u + 3) // 4 * 4
+    h0 = torch.zeros((B, u4), dtype=torch.float32, device="cuda")
+    h1 = torch.zeros((B, u4), dtype=torch.float32, device="cuda")
+    scratch = torch.zeros(64, dtype=torch.int64, device="cuda")
+    status = torch.zeros(1, dtype=torch.int32, device="cuda")
+    outs = []
+    for kp in (u4, (u + 63) // 64 * 64):
+        assert kp % 16 != 0 or kp % 64 == 0
+        qp = np.zeros((gu, kp), np.int8)
+        qp[:, :u] = q
+        dq = dev(qp)
+        y = torch.full((B, T, u), float("nan"), dtype=torch.float32, device="cuda")
+        hipabi.check(L.knx_hip_rnn_recurrence(kind, 4, 0.0, B, T, u, 0, ptr(zx), None, 0, ptr(dq), kp, ptr(qs),
+                                              ptr(brec), ptr(h0), ptr(h1), ptr(y), u, 1, ptr(scratch), 512,
+                                              ptr(status), hipabi.stream()))
+        torch.cuda.synchronize()
+        outs.append(y.cpu().numpy())
+    assert np.isfinite(outs[1]).all()
+    assert np.array_equal(outs[0], outs[1])
 
 
 def test_recurrence_entry_point_rejects(monkeypatch):
