@@ -105,8 +105,16 @@ __device__ __forceinline__ unsigned lane_group_max(unsigned v, int n)
     if (n > 2) v = max(v, (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));  // quad [2,3,0,1]
     if (n > 4) v = max(v, (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false)); // half-row mirror
     if (n > 8) v = max(v, (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false)); // row mirror
-    if (n > 16) v = max(v, (unsigned)__shfl_xor((int)v, 16, 64));
-    if (n > 32) v = max(v, (unsigned)__shfl_xor((int)v, 32, 64));
+    // rows of 16 lanes, then halves of 32: gfx950's register swaps (each lane's value and its partner's in the pair
+    // of results) instead of a permute through the LDS
+    if (n > 16) {
+        const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        v = max((unsigned)p[0], (unsigned)p[1]);
+    }
+    if (n > 32) {
+        const auto p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        v = max((unsigned)p[0], (unsigned)p[1]);
+    }
     return v;
 }
 
