@@ -193,8 +193,7 @@ __device__ __forceinline__ void item_i8(const LayerDev& L, int rows, __amdgpu_bu
 #pragma unroll
         for (int q = 0; q < kXS; ++q)
             if (32 * q < K4) mx = fmaxf(fmaxf(fmaxf(mx, mag(xv[q].x)), fmaxf(mag(xv[q].y), mag(xv[q].z))), mag(xv[q].w));
-#pragma unroll
-        for (int off = 16; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+        mx = __uint_as_float(knx_lane_group_max(__float_as_uint(mx), 32));  // the half-wave's 32 lanes
         const bool bad = !(mx <= FLT_MAX);
         const float sc = (!bad && mx > 0.0f) ? __fdiv_rn(mx, 127.0f) : 1.0f;
         const float inv = __fdiv_rn(1.0f, sc);

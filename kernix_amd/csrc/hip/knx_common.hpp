@@ -112,6 +112,27 @@ __device__ __forceinline__ float knx_gru_cell(float xz, float xr, float xh, floa
     return step0 ? (-hh) * zg + hh : (prev - hh) * zg + hh;
 }
 
+// Unsigned maximum over aligned groups of n lanes (n a power of two ≤ 64, uniform; every lane active), every lane of a
+// group getting it: DPP within rows of 16 lanes (the quad swaps, then the half-row and row mirrors), gfx950's register
+// swaps across rows and halves (each lane's value and its partner's in the pair of results), no exchange through the
+// LDS.  Non-negative floats compare as their bits.
+__device__ __forceinline__ unsigned knx_lane_group_max(unsigned v, int n)
+{
+    if (n > 1) v = max(v, (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));  // quad [1,0,3,2]
+    if (n > 2) v = max(v, (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));  // quad [2,3,0,1]
+    if (n > 4) v = max(v, (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false)); // half-row mirror
+    if (n > 8) v = max(v, (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false)); // row mirror
+    if (n > 16) {
+        const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        v = max((unsigned)p[0], (unsigned)p[1]);
+    }
+    if (n > 32) {
+        const auto p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        v = max((unsigned)p[0], (unsigned)p[1]);
+    }
+    return v;
+}
+
 // Wave-wide (64 lanes) reductions through DPP/permute; every lane gets the result.
 __device__ __forceinline__ float knx_wave_sum(float v)
 {

@@ -97,27 +97,6 @@ __host__ __device__ inline Lds lds_layout(int B, int gates, int uw, int up, bool
     return l;
 }
 
-// unsigned maximum over aligned groups of n lanes (n a power of two ≤ 64, uniform; every lane active): row-local
-// DPP for groups up to 16, lane exchanges above
-__device__ __forceinline__ unsigned lane_group_max(unsigned v, int n)
-{
-    if (n > 1) v = max(v, (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));  // quad [1,0,3,2]
-    if (n > 2) v = max(v, (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));  // quad [2,3,0,1]
-    if (n > 4) v = max(v, (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false)); // half-row mirror
-    if (n > 8) v = max(v, (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false)); // row mirror
-    // rows of 16 lanes, then halves of 32: gfx950's register swaps (each lane's value and its partner's in the pair
-    // of results) instead of a permute through the LDS
-    if (n > 16) {
-        const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
-        v = max((unsigned)p[0], (unsigned)p[1]);
-    }
-    if (n > 32) {
-        const auto p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-        v = max((unsigned)p[0], (unsigned)p[1]);
-    }
-    return v;
-}
-
 // The kernels are instantiated per cell kind (KIND 4 LSTM, 5 GRU, 6 simple RNN) and for the tanh activation (ACT 4,
 // the recurrent layers' default) or any (kActAny: the activation read from the arguments): with the cell's branches
 // and the activation's switch resolved at compile time a timestep's cells took 0.46 against 0.70 µs.
@@ -273,7 +252,7 @@ __global__ void __launch_bounds__(kThreads) rnn_recurrence(RnnArgs a)
                         const unsigned z = __float_as_uint(v[s].z) & 0x7fffffffu, w = __float_as_uint(v[s].w) & 0x7fffffffu;
                         m = max(m, max(max(x, y), max(z, w)));
                     }
-                    m = lane_group_max(m, LR);
+                    m = knx_lane_group_max(m, LR);
                     const bool bad = m >= 0x7f800000u;
                     const float mx = __uint_as_float(m);
                     const float sc = (!bad && mx > 0.0f) ? __fdiv_rn(mx, 127.0f) : 1.0f;
@@ -615,7 +594,7 @@ __global__ void __launch_bounds__(kSoloThreads) rnn_solo(RnnArgs a, int KS, int 
             // quantization: per wave and row, then one LDS atomic per wave
             const unsigned mb = __float_as_uint(hv) & 0x7fffffffu;
             for (int rb = 0; rb < B; ++rb) {
-                const unsigned v = lane_group_max(cell && cb == rb ? mb : 0u, 64);
+                const unsigned v = knx_lane_group_max(cell && cb == rb ? mb : 0u, 64);
                 if (lane == 0 && v != 0u) atomicMax(&rmx[step & 1][rb], v);
             }
         }
