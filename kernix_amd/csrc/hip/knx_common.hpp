@@ -133,6 +133,30 @@ __device__ __forceinline__ unsigned knx_lane_group_max(unsigned v, int n)
     return v;
 }
 
+// Sum over aligned groups of n lanes, the same exchanges as knx_lane_group_max (every lane of a group ends with the
+// same value: a + b and b + a are the same float).
+template <int CTRL>
+__device__ __forceinline__ float knx_dpp_f32(float x)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float knx_lane_group_sum(float v, int n)
+{
+    if (n > 1) v = v + knx_dpp_f32<0xB1>(v);
+    if (n > 2) v = v + knx_dpp_f32<0x4E>(v);
+    if (n > 4) v = v + knx_dpp_f32<0x141>(v);
+    if (n > 8) v = v + knx_dpp_f32<0x140>(v);
+    if (n > 16) {
+        const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    }
+    if (n > 32) {
+        const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    }
+    return v;
+}
+
 // Wave-wide (64 lanes) reductions through DPP/permute; every lane gets the result.
 __device__ __forceinline__ float knx_wave_sum(float v)
 {

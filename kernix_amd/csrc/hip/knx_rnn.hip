@@ -559,7 +559,7 @@ __global__ void __launch_bounds__(kSoloThreads) rnn_solo(RnnArgs a, int KS, int 
                         v = fmaf(hv.z, uf[4 * i + 2], v);
                         v = fmaf(hv.w, uf[4 * i + 3], v);
                     }
-                    for (int off = KS / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+                    v = knx_lane_group_sum(v, KS);
                     if (a.brec) v = v + col_bias;
                     if (active && ks == 0) r[b][c] = v;
                 }
