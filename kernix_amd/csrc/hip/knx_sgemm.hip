@@ -686,14 +686,15 @@ int dispatch_nt(SgArgs p, int batch, hipStream_t s, const char* name)
     const long cus = knx::num_cus();
     const long t256 = (long)((p.M + 255) / 256) * ((p.N + 255) / 256) * batch;
     const long t128 = (long)((p.M + 127) / 128) * ((p.N + 127) / 128) * batch;
-    // KNX_SGEMM_KERNEL forces the general kernel ("general"), one pipelined tile ("t256", "t128", "t128w8", "t64") or the
-    // small-GEMM kernel ("skinny") where the shape allows it, else the general kernel (tests, tuning)
+    // KNX_SGEMM_KERNEL forces the general kernel ("general"), one pipelined tile ("t256", "t128", "t128w8", "t64",
+    // "t64x64") or the small-GEMM kernel ("skinny") where the shape allows it, else the general kernel (tests, tuning)
     const char* force = getenv("KNX_SGEMM_KERNEL");
     if (force != nullptr && *force) {
         if (strcmp(force, "t256") == 0 && k32_ok(p, 256, 256)) return launch_k32<256, 256, 4, 2>(p, batch, s, name);
         if (strcmp(force, "t128") == 0 && k32_ok(p, 128, 128)) return launch_k32<128, 128, 2, 2>(p, batch, s, name);
         if (strcmp(force, "t128w8") == 0 && k32_ok(p, 128, 128)) return launch_k32<128, 128, 4, 2>(p, batch, s, name);
         if (strcmp(force, "t64") == 0 && k32_ok(p, 128, 64)) return launch_k32<128, 64, 4, 1>(p, batch, s, name);
+        if (strcmp(force, "t64x64") == 0 && k32_ok(p, 64, 64)) return launch_k32<64, 64, 2, 2>(p, batch, s, name);
 #ifdef KNX_TUNING
         // variants no shape selects (measured slower where they fit), built only for tuning (-DKNX_TUNING)
         if (strcmp(force, "t128s3") == 0 && k32_ok(p, 128, 128)) return launch_k32<128, 128, 2, 2, 3>(p, batch, s, name);
@@ -702,6 +703,7 @@ int dispatch_nt(SgArgs p, int batch, hipStream_t s, const char* name)
         if (strcmp(force, "t256x128") == 0 && k32_ok(p, 256, 128)) return launch_k32<256, 128, 4, 2>(p, batch, s, name);
         if (strcmp(force, "t256x192") == 0 && k32_ok(p, 256, 192)) return launch_k32<256, 192, 4, 2>(p, batch, s, name);
         if (strcmp(force, "t128x256") == 0 && k32_ok(p, 128, 256)) return launch_k32<128, 256, 2, 4>(p, batch, s, name);
+        if (strcmp(force, "t64x64s3") == 0 && k32_ok(p, 64, 64)) return launch_k32<64, 64, 2, 2, 3>(p, batch, s, name);
 #endif
         if (strcmp(force, "skinny") == 0 && skinny_ok(p, batch)) return launch_skinny(p, s, name);
         return dispatch<true>(p, batch, s, name);
@@ -723,6 +725,10 @@ int dispatch_nt(SgArgs p, int batch, hipStream_t s, const char* name)
     if (t256 >= cus && k32_ok(p, 256, 256)) return launch_k32<256, 256, 4, 2>(p, batch, s, name);
     if (t128 >= cus && k32_ok(p, 128, 128)) return launch_k32<128, 128, 2, 2>(p, batch, s, name);
     if (t64 >= cus && k32_ok(p, 128, 64)) return launch_k32<128, 64, 4, 1>(p, batch, s, name);
+    // mid shapes that leave CUs idle on the tiles above: 64×64 tiles on 2×2 waves of 32×32 (one box, µs, against the
+    // general kernel and 128×64 tiles: the LSTM input projection at batch 64, 2048×512×128, 6.6 / 11.7 / 9.2;
+    // 1024×512×128 6.3 / 11.2 / 9.2; 2048×512×256 8.3 / 16.3 / 13.2)
+    if (k32_ok(p, 64, 64)) return launch_k32<64, 64, 2, 2>(p, batch, s, name);
     return dispatch<true>(p, batch, s, name);
 }
 

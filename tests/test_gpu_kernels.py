@@ -374,7 +374,7 @@ def test_sgemm_ep(L, M, N, K, act):
 # the weight-transposed entry point: pipelined kernel (K % 32 == 0, tiles inside M and N, moved back at the edges)
 # and the general kernel otherwise; 8100×1500×128 has enough 128×128 tiles for the 8-wave tile by default
 SGNT_SHAPES = [(256, 256, 64), (300, 200, 96), (1024, 1000, 512), (4096, 1024, 256), (128, 128, 32), (100, 77, 50),
-               (512, 512, 30), (2048, 640, 2048), (8100, 1500, 128)]
+               (512, 512, 30), (2048, 640, 2048), (8100, 1500, 128), (2048, 512, 128)]
 # small GEMMs (split-K 16×16 kernel by default): the int8 MLP's layers at batch 64, ragged M/N, K % 16 ≠ 0
 SGNT_SMALL = [(64, 512, 784), (64, 256, 512), (64, 10, 256), (1, 1, 16), (5, 33, 100), (17, 70, 20), (256, 10, 256),
               (3, 4000, 4096), (2, 48, 4100)]
@@ -395,7 +395,7 @@ def test_sgemm_nt_small(L, M, N, K, kernel, monkeypatch):
 
 # the pipelined tiles a shape can select (KNX_TUNING=1 builds also have t128s3, t64s3, t64w2, t256x128, t256x192,
 # t128x256)
-SGNT_VARIANTS = ["t256", "t128", "t128w8", "t64"]
+SGNT_VARIANTS = ["t256", "t128", "t128w8", "t64", "t64x64"]
 
 
 @pytest.mark.parametrize("kernel", SGNT_VARIANTS)
@@ -406,7 +406,7 @@ def test_sgemm_nt_variants(L, M, N, K, kernel, monkeypatch):
     _sgemm_nt_case(L, M, N, K, 1)
 
 
-@pytest.mark.parametrize("kernel", ["", "t128", "t128w8", "t64", "t256", "skinny", "general"])
+@pytest.mark.parametrize("kernel", ["", "t128", "t128w8", "t64", "t64x64", "t256", "skinny", "general"])
 @pytest.mark.parametrize("M,N,K,inplace", [(1024, 768, 512, False), (520, 700, 96, True), (64, 256, 512, True),
                                            (100, 77, 50, False)])
 def test_sgemm_nt_residual(L, M, N, K, inplace, kernel, monkeypatch):
