@@ -378,6 +378,15 @@ __global__ void __launch_bounds__(kThreads) rnn_recurrence(RnnArgs a)
     }
 }
 
+// Barrier for the LDS hand-offs of a timestep (h, its int8 rows, the recurrent terms, the row maxima): this wave's LDS
+// accesses retired, then s_barrier.  __syncthreads would also wait for the wave's global stores (the output h) and
+// loads (the next timestep's gate inputs), which no other wave reads.
+__device__ __forceinline__ void lds_barrier()
+{
+    KNX_WAIT_LDS();
+    knx_barrier_nofence();
+}
+
 // ---- the batch split over workgroups, each running the whole recurrence of its rows ----
 // The rows of a recurrence never meet (h, its int8 row scale and the cells are per row), so a workgroup that holds all
 // of U runs its rows' timesteps alone: no h exchange through memory and no barrier across workgroups, whose round trips
@@ -391,17 +400,8 @@ __global__ void __launch_bounds__(kThreads) rnn_recurrence(RnnArgs a)
 // quantizer, int32 sums, epilogue and cells as above; with int8 arithmetic the cells that write h_t also gather its
 // row maxima (per wave, then one LDS atomic per wave and row), and at the next step every cell quantizes its own value
 // with its row's scale, so the quantization is one multiply-and-round per thread instead of a pass over the rows.
-// Barrier for the LDS hand-offs of a timestep (h, its int8 rows, the recurrent terms, the row maxima): this wave's LDS
-// accesses retired, then s_barrier.  __syncthreads would also wait for the wave's global stores (the output h) and
-// loads (the next timestep's gate inputs), which no other wave reads.
-__device__ __forceinline__ void lds_barrier()
-{
-    KNX_WAIT_LDS();
-    knx_barrier_nofence();
-}
-
 constexpr int kSoloThreads = 1024;
-constexpr int kSoloRegs = 64;   // U values per thread (fp32; int8: kSoloRegs / 2 words of four values)
+constexpr int kSoloRegs = 64;   // fp32: U values per thread
 constexpr int kSoloRows = 2;
 constexpr int kSoloBlocks = 2;  // int8: 16-column blocks per wave (gates·u ≤ 512)
 constexpr int kSoloChunks = 2;  // int8: 64-byte k-chunks (u ≤ 128); 4 × 4 fragments spilled registers
