@@ -1736,6 +1736,7 @@ static int i8gemm_run(I8Args p, hipStream_t s, const char* name)
         if (f == "k128w8ta3e" && k128_fits<256, 256>(p)) return launch_k128<256, 256, 4, 2, 3, true>(p, s, name);
         if (f == "k128m" && k128_fits<128, 128>(p)) return launch_k128<128, 128, 2, 2, 2>(p, s, name);
         if (f == "k128ma3" && k128_fits<128, 128>(p)) return launch_k128<128, 128, 2, 2, 3>(p, s, name);
+        if (f == "k128m8a3e" && k128_fits<128, 128>(p)) return launch_k128<128, 128, 4, 2, 3, true>(p, s, name);
         if (f == "ring64s4" && k128_fits<64, 64>(p)) return launch_ring<64, 64, 2, 2, 4, 1>(p, s, name);
         if (f == "ring64g2" && k128_fits<64, 64>(p) && ring_split_fits<2, 4>(p)) return launch_ring<64, 64, 2, 2, 4, 1, 2>(p, s, name);
         if (f == "k128ms4" && ksplit_fits<128, 128, 4>(p)) return launch_k128<128, 128, 2, 2, 2, false, 4>(p, s, name);
@@ -1759,6 +1760,8 @@ static int i8gemm_run(I8Args p, hipStream_t s, const char* name)
         if (f == "k128c" && k128_fits<128, 256>(p)) return launch_k128<128, 256, 2, 4, 3, true>(p, s, name);
         if (f == "ring64s8k2" && k128_fits<64, 64>(p)) return launch_ring<64, 64, 2, 2, 8, 2>(p, s, name);
         if (f == "ring64s8" && k128_fits<64, 64>(p)) return launch_ring<64, 64, 2, 2, 8, 1>(p, s, name);
+        if (f == "k128m8" && k128_fits<128, 128>(p)) return launch_k128<128, 128, 4, 2, 2>(p, s, name);
+        if (f == "k128m8a3" && k128_fits<128, 128>(p)) return launch_k128<128, 128, 4, 2, 3>(p, s, name);
 #endif
         if (f == "skinny" && M <= 64) return M <= 16 ? launch_skinny<1>(p, s, name) : M <= 32 ? launch_skinny<2>(p, s, name) : launch_skinny<4>(p, s, name);
     }
@@ -1774,11 +1777,11 @@ static int i8gemm_run(I8Args p, hipStream_t s, const char* name)
         return launch_k128<256, 256, 4, 2, 2>(p, s, name);
     }
     const long tiles128 = (long)((M + 127) / 128) * ((N + 127) / 128);
-    // 128×128: three A stages once K is long (8192×512×2048 + residual: 19.5 against 21.3 µs)
-    if (tiles128 >= knx::num_cus() && k128_fits<128, 128>(p)) {
-        if (K >= 2048) return launch_k128<128, 128, 2, 2, 3>(p, s, name);
-        return launch_k128<128, 128, 2, 2, 2>(p, s, name);
-    }
+    // 128×128 on 8 waves of 32×64, three A stages, the A loads spread over the k-tile: one workgroup per CU still has
+    // two waves per SIMD (one box, µs, against 4 waves of 64×64 with two / three A stages: 8192×512×2048 + residual
+    // 17.7-18.0 against 20.9-21.0 / 20.3; 8192×1536×512 17.6-18.2 against 19.6-20.3 / 19.9-20.6; two stages on the
+    // 8 waves: 18.3-19.7)
+    if (tiles128 >= knx::num_cus() && k128_fits<128, 128>(p)) return launch_k128<128, 128, 4, 2, 3, true>(p, s, name);
     // fewer tiles than CUs even at 128×128 (e.g. M = 256, N = 4096): one 64×64 tile per workgroup on the deep LDS
     // ring (M = 256: 13.2 µs against 16.8 for the 64-byte k-tile pipeline), K split over two rings in the workgroup
     // when the 64×64 tiles leave CUs without a second workgroup

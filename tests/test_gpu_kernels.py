@@ -92,7 +92,7 @@ def test_i8gemm_standalone_config(L, M):
 # every kernel instantiation a shape can select, each forced onto every edge shape (a library built with KNX_TUNING=1
 # also has the tuning-only variants: pp, k128, k128w8, k128w8ta3, k128w16, k128r, k128c, ring64s8k2, ring64s8,
 # pipe256, pipe256w8, pipe256s3, pipe128, tile256, which this list can name there)
-I8_VARIANTS = ["default", "k128w8t", "k128m", "k128ma3", "k128w8ta3e", "ring64s4", "ring64g2", "pipe64", "tile64",
+I8_VARIANTS = ["default", "k128w8t", "k128m", "k128ma3", "k128m8a3e", "k128w8ta3e", "ring64s4", "ring64g2", "pipe64", "tile64",
                "k128ms4", "k128ma3s4", "k128m8s4", "k128ms2", "k128ms8"]
 # tiles moved back at the M/N edges, half k-tiles (K % 128 == 64), N % 4 != 0, one whole 256x256 tile, 2..4 k-tiles
 # (every branch of the three-stage A ring's prologue and tail), an 8 x 8 tile grid split into XCD blocks, and for the
@@ -194,7 +194,7 @@ def test_i8gemm_skinny_variants(L, monkeypatch, variant, M, N, K):
     assert np.array_equal(host(Y), want_y)
 
 
-@pytest.mark.parametrize("variant", ["default", "k128w8t", "k128w8ta3e", "k128m", "ring64s4", "ring64g2", "pipe64", "tile64",
+@pytest.mark.parametrize("variant", ["default", "k128w8t", "k128w8ta3e", "k128m", "k128m8a3e", "ring64s4", "ring64g2", "pipe64", "tile64",
                                      "skinny", "k128ms4", "k128m8s4"])
 @pytest.mark.parametrize("M,N,K,inplace", [(300, 300, 1024, False), (520, 700, 320, True), (2048, 2048, 2048, False),
                                            (48, 520, 192, True)])
