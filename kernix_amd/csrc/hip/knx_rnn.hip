@@ -478,7 +478,7 @@ __global__ void __launch_bounds__(kSoloThreads) rnn_solo(RnnArgs a, int KS, int 
         }
     }
     __syncthreads();
-    const float col_bias = a.brec ? a.brec[cc] : 0.0f;
+    const float col_bias = !I8 && a.brec ? a.brec[cc] : 0.0f;  // fp32 (int8: cbi)
     // cell phase: thread tid < B·u owns row b = tid / u, unit j = tid % u
     const bool cell = tid < B * u;
     const int cb = cell ? tid / u : 0, cj = cell ? tid % u : 0;
