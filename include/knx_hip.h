@@ -39,6 +39,8 @@
  *   knx_hip_embedding       kernix_embedding_run                                include/kernix_model.h:987-1000
  *   knx_hip_rnn_gates       per-timestep gate update of kernix_rnn_dir          include/kernix_model.h:580-631
  *   knx_hip_rnn_recurrence  one RNN direction's timesteps in one launch         include/kernix_model.h:563-632
+ *   knx_hip_rnn_recurrence_dense  the same and the LINEAR on its last state    include/kernix_model.h:563-632,
+ *                                                                               :1843-1860
  *   knx_hip_linear_chain    consecutive LINEAR steps of a small batch           include/kernix_model.h:1843-1860,
  *                           (kernix_step_run layer after layer, int8 ones       :99-182
  *                           through kernix_qmatmul)
@@ -273,6 +275,18 @@ KNX_API int knx_hip_rnn_gates(int kind, int act, float alpha, int B, int u, int 
  * knx_hip_rnn_recurrence_fits rejects (neither form: B > 64 on the grid, u > 2048, a weight slice or h that does not
  * fit the workgroup's LDS) are KNX_EINVAL. */
 KNX_API int knx_hip_rnn_recurrence_fits(int kind, int B, int u, int i8);
+/* The recurrence of one direction (as knx_hip_rnn_recurrence, its last state only: ret_seq 0) and the LINEAR step that
+ * reads only that state, in one launch (reference include/kernix_model.h:563-632, then the LINEAR dispatch :1843-1860
+ * on its B rows): y (B rows of dn) = act(h_T·Wᵀ + b), with dq (dn rows of dkp bytes, k = u contiguous) and dqs its
+ * per-output scales the int8 arithmetic of knx_hip_qlinear (the same bits), else fp32 on dw (dn rows of u floats);
+ * db may be NULL.  Only the batch-split form (knx_hip_rnn_recurrence_dense_fits: U fits a workgroup, u ≤ 256);
+ * dst still receives the last state. */
+KNX_API int knx_hip_rnn_recurrence_dense_fits(int kind, int B, int u, int i8, int n);
+KNX_API int knx_hip_rnn_recurrence_dense(int kind, int act, float alpha, int B, int T, int u, int dir, const float* zx,
+                                         const float* U, int u_nt, const int8_t* q, int kp, const float* qscale,
+                                         const float* brec, float* dst, int stride, const float* dw, const int8_t* dq,
+                                         int dkp, const float* dqs, const float* db, int dn, int dact, float dalpha,
+                                         float* dy, void* stream);
 KNX_API int knx_hip_rnn_recurrence(int kind, int act, float alpha, int B, int T, int u, int dir, const float* zx,
                                    const float* U, int u_nt, const int8_t* q, int kp, const float* qscale,
                                    const float* brec, float* h0, float* h1, float* dst, int stride, int ret_seq,

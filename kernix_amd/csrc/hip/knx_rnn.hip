@@ -57,6 +57,16 @@ struct RnnArgs {
     float* h1;
     float* dst;
     knx::GridSync gs;
+    // the row-split kernel only: the LINEAR step that reads only the last state, at the end of the same launch
+    // (dn > 0): y = act(h_T·Wᵀ + b) over dn outputs, int8 (dq: dn rows of dkp bytes, dqs their scales) or fp32 (dw:
+    // dn rows of u floats); dy: B rows of dn
+    const float* dw;
+    const int8_t* dq;
+    const float* dqs;
+    const float* db;
+    int dn, dkp, dact;
+    float dalpha;
+    float* dy;
 };
 
 __host__ __device__ inline size_t round16(size_t b) { return (b + 15) / 16 * 16; }
@@ -600,6 +610,63 @@ __global__ void __launch_bounds__(kSoloThreads) rnn_solo(RnnArgs a, int KS, int 
         }
         lds_barrier();  // h_t (and its row maxima) complete in LDS
     }
+    if (a.dn > 0) {
+        // The LINEAR after the recurrence, on h_T still in LDS (zero past u).  int8: each row quantized by one wave with
+        // the quantizer's operations (as above) into hq and sxs, exact int32 sums, ((float)acc · sx) · scale (+ bias),
+        // then the activation — the bits of knx_hip_qlinear; fp32: lane sums of h·w (+ bias), then the activation.
+        const bool di8 = a.dq != nullptr;
+        if (di8) {
+            if (wave < B) {
+                float hv[4];  // u ≤ 256 on the row-split kernel
+                unsigned mb = 0u;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int j = lane + 64 * i;
+                    hv[i] = j < u ? hs[wave][j] : 0.0f;
+                    mb = max(mb, __float_as_uint(hv[i]) & 0x7fffffffu);
+                }
+                mb = knx_lane_group_max(mb, 64);
+                const bool bad = mb >= 0x7f800000u;
+                const float mx = __uint_as_float(mb);
+                const float sc = (!bad && mx > 0.0f) ? __fdiv_rn(mx, 127.0f) : 1.0f;
+                const float inv = bad ? 0.0f : __fdiv_rn(1.0f, sc);
+                if (lane == 0) sxs[wave] = bad ? __int_as_float(0x7fc00000) : sc;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int j = lane + 64 * i;
+                    if (j < u)
+                        reinterpret_cast<int8_t*>(&hq[wave][0])[j] =
+                            (int8_t)(int)__builtin_amdgcn_fmed3f(rintf(hv[i] * inv), -127.0f, 127.0f);
+                }
+            }
+            lds_barrier();
+        }
+        for (int pr = wave; pr < B * a.dn; pr += kSoloThreads / 64) {  // (row, output) pairs, one per wave
+            const int b = pr / a.dn, c = pr % a.dn;
+            float v;
+            if (di8) {
+                int acc = 0;  // lane: bytes 4·lane … 4·lane + 3 (hq is zero past u, so the weight's bytes there do not count)
+                if (4 * lane < u)
+                    acc = __builtin_amdgcn_sdot4(hq[b][lane], *reinterpret_cast<const int*>(a.dq + (size_t)c * a.dkp + 4 * lane),
+                                                 0, false);
+#pragma unroll
+                for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, 64);
+                v = (float)acc * sxs[b];
+                v = v * a.dqs[c];
+            } else {
+                float part = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int j = lane + 64 * i;
+                    if (j < u) part = fmaf(hs[b][j], a.dw[(size_t)c * u + j], part);
+                }
+                v = knx_lane_group_sum(part, 64);
+            }
+            if (a.db) v = v + a.db[c];
+            v = knx_act(v, a.dact, a.dalpha);
+            if (lane == 0) a.dy[(size_t)(row0 + b) * a.dn + c] = v;
+        }
+    }
 }
 
 // rows per workgroup of the row-split kernel: one while there is a CU for every row (a workgroup's timestep grows with
@@ -680,6 +747,45 @@ extern "C" int knx_hip_rnn_recurrence_fits(int kind, int B, int u, int i8)
     const int uw = units_per_wg(B, u, gates);
     if ((u + uw - 1) / uw > kMaxGrid || B * uw > kThreads * kMaxPairs) return 0;
     return lds_layout(B, gates, uw, k_extent(u, i8 != 0), i8 != 0, !i8 || kind == 5).total <= kMaxLds ? 1 : 0;
+}
+
+extern "C" int knx_hip_rnn_recurrence_dense_fits(int kind, int B, int u, int i8, int n)
+{
+    if ((kind != 4 && kind != 5 && kind != 6) || B < 1 || u < 1 || u > 65536 || n < 1) return 0;
+    const int gates = kind == 4 ? 4 : kind == 5 ? 3 : 1;
+    return solo_lanes(B, gates * u, u, i8 != 0) > 0 && u <= 256 ? 1 : 0;
+}
+
+extern "C" int knx_hip_rnn_recurrence_dense(int kind, int act, float alpha, int B, int T, int u, int dir, const float* zx,
+                                            const float* U, int u_nt, const int8_t* q, int kp, const float* qscale,
+                                            const float* brec, float* dst, int stride, const float* dw, const int8_t* dq,
+                                            int dkp, const float* dqs, const float* db, int dn, int dact, float dalpha,
+                                            float* dy, void* stream)
+{
+    const char* name = "knx_hip_rnn_recurrence_dense";
+    KNX_ENTRY(name);
+    KNX_REQUIRE(T >= 1 && act >= -1 && act <= 15 && dact >= -1 && dact <= 15 && (dir == 0 || dir == 1), name);
+    KNX_REQUIRE(knx_hip_rnn_recurrence_dense_fits(kind, B, u, q != nullptr, dn), name);
+    const int gates = kind == 4 ? 4 : kind == 5 ? 3 : 1;
+    KNX_REQUIRE(zx != nullptr && dst != nullptr && stride >= u && dy != nullptr, name);
+    KNX_REQUIRE(kind != 5 || brec != nullptr, name);
+    KNX_REQUIRE(q != nullptr ? (qscale != nullptr && kp >= (u + 3) / 4 * 4 && ((uintptr_t)q & 3) == 0 && kp % 4 == 0)
+                             : U != nullptr, name);
+    KNX_REQUIRE(dq != nullptr ? (dqs != nullptr && dkp >= (u + 3) / 4 * 4 && ((uintptr_t)dq & 3) == 0 && dkp % 4 == 0)
+                              : dw != nullptr, name);
+    RnnArgs a{};
+    a.kind = kind; a.act = act; a.alpha = alpha;
+    a.B = B; a.T = T; a.u = u; a.gu = gates * u; a.gates = gates; a.dir = dir; a.ret_seq = 0;
+    a.stride = stride; a.uw = units_per_wg(B, u, gates);
+    a.up = k_extent(u, q != nullptr); a.ldh = (u + 3) / 4 * 4;
+    a.zx = zx; a.U = U; a.u_nt = u_nt != 0; a.q = q; a.kp = kp; a.qs = qscale; a.brec = brec;
+    a.dst = dst;
+    a.dw = dq != nullptr ? nullptr : dw; a.dq = dq; a.dkp = dkp; a.dqs = dqs; a.db = db;
+    a.dn = dn; a.dact = dact; a.dalpha = dalpha; a.dy = dy;
+    const int ks = solo_lanes(B, a.gu, u, q != nullptr);
+    const hipStream_t s = knx::as_stream(stream);
+    if (q != nullptr) return launch_kind<true>(a, ks, 0, 0, s, name);
+    return launch_kind<false>(a, ks, 0, 0, s, name);
 }
 
 extern "C" int knx_hip_rnn_recurrence(int kind, int act, float alpha, int B, int T, int u, int dir, const float* zx,

@@ -550,10 +550,25 @@ static int rnn_persistent(const kernix_model* m)
     return m->dev->chain != NULL && !m->dev->no_chain && (e == NULL || *e != '0');
 }
 
+/* The LINEAR step that reads only an RNN's last state, run at the end of the recurrence's launch (rnn_dense_fusable):
+ * its weight in the form its own step would use (int8 q with its scales, or fp32 w: n rows of k floats). */
+struct rnn_dense {
+    const float* w;
+    const int8_t* q;
+    int kp;
+    const float* qscale;
+    const float* bias;
+    int n, act;
+    float alpha;
+    float* y;
+};
+
 /* One direction of an RNN, reference include/kernix_model.h:563-632: the input projection of all timesteps is one
  * GEMM; then the timesteps in one launch (knx_hip_rnn_recurrence) where the shape fits it, else per timestep h·U
- * (int8 or fp32) and the gates as launches of their own. */
-static int run_rnn_dir(const kernix_model* m, kernix_step* s, int dir, const float_tensor* x, float* dst, int stride, void* st)
+ * (int8 or fp32) and the gates as launches of their own.  With `dense` the LINEAR after it runs in the same launch
+ * (knx_hip_rnn_recurrence_dense; rnn_dense_fusable has checked that it fits). */
+static int run_rnn_dir(const kernix_model* m, kernix_step* s, int dir, const float_tensor* x, float* dst, int stride, void* st,
+                       const struct rnn_dense* dense)
 {
     struct knx_dstep* d = s->dev;
     const int kind = s->kind, T = s->seq, u = s->out, gu = (int)gates(kind) * u;
@@ -578,6 +593,14 @@ static int run_rnn_dir(const kernix_model* m, kernix_step* s, int dir, const flo
     if (hip_ok(knx_hip_sgemm_nt_ep(x->row, gu, s->in, x->tensor, s->in, W, s->in, bias, -1, 0.0f, zx, gu, st), "RNN input projection"))
         return -1;
     const int i8 = q != NULL && (m->int8_mode == KERNIX_INT8_I8 || B <= KERNIX_INT8_MAX_ROWS);
+    if (dense != NULL) {
+        if (!i8 && U == NULL) return -1;
+        return hip_ok(knx_hip_rnn_recurrence_dense(kind, s->act, s->alpha, B, T, u, dir, zx, i8 ? NULL : U, q != NULL,
+                                                   i8 ? dq : NULL, q != NULL ? q->kp : 0, dsc, brec, dst, stride, dense->w,
+                                                   dense->q, dense->kp, dense->qscale, dense->bias, dense->n, dense->act,
+                                                   dense->alpha, dense->y, st),
+                      "RNN recurrence + Linear");
+    }
     if (rnn_persistent(m) && knx_hip_rnn_recurrence_fits(kind, B, u, i8)) {
         /* every timestep in one launch; h alternates between h and the recurrent-term buffer (B rows of u4 each) */
         if (!i8 && U == NULL) return -1;
@@ -617,11 +640,12 @@ static int run_rnn_dir(const kernix_model* m, kernix_step* s, int dir, const flo
 static int run_rnn(const kernix_model* m, kernix_step* s, const float_tensor* x, float_tensor* y, void* st)
 {
     const int u = s->out;
-    if (s->dirs == 1) return run_rnn_dir(m, s, 0, x, y->tensor, u, st);
+    if (s->dirs == 1) return run_rnn_dir(m, s, 0, x, y->tensor, u, st, NULL);
     if (s->merge == KERNIX_MERGE_CONCAT)
-        return run_rnn_dir(m, s, 0, x, y->tensor, 2 * u, st) || run_rnn_dir(m, s, 1, x, y->tensor + u, 2 * u, st) ? -1 : 0;
+        return run_rnn_dir(m, s, 0, x, y->tensor, 2 * u, st, NULL) || run_rnn_dir(m, s, 1, x, y->tensor + u, 2 * u, st, NULL)
+                   ? -1 : 0;
     float* bw = s->tmp[5]->tensor;
-    if (run_rnn_dir(m, s, 0, x, y->tensor, u, st) || run_rnn_dir(m, s, 1, x, bw, u, st)) return -1;
+    if (run_rnn_dir(m, s, 0, x, y->tensor, u, st, NULL) || run_rnn_dir(m, s, 1, x, bw, u, st, NULL)) return -1;
     const int rows = y->row;
     if (hip_ok(knx_hip_binary(s->merge == KERNIX_MERGE_MUL ? KERNIX_BIN_MUL : KERNIX_BIN_ADD, y->tensor, rows, u, bw, rows, u,
                               y->tensor, 1, rows, u, st), "RNN merge")) return -1;
@@ -801,6 +825,51 @@ static int fusable_add(const kernix_model* m, int i)
     return other;
 }
 
+/* An RNN step i (one direction, its last state only) whose output is read only by step i + 1, a LINEAR (and not by a
+ * fused add after it): the LINEAR runs at the end of the recurrence's launch on the last state still in LDS, with the
+ * arithmetic its own step would have (run_qlinear: int8 in i8 mode or at <= KERNIX_INT8_MAX_ROWS rows, the same bits;
+ * else fp32 on the fp32 or dequantized weight) — one launch and one round trip through memory less. */
+static int rnn_dense_fusable(const kernix_model* m, int i)
+{
+    if (i + 1 >= m->n_steps) return 0;
+    const kernix_step* s = &m->steps[i];
+    const kernix_step* n = &m->steps[i + 1];
+    if (s->kind != KERNIX_OP_LSTM && s->kind != KERNIX_OP_GRU && s->kind != KERNIX_OP_RNN) return 0;
+    if (s->dirs != 1 || s->ret_seq || n->kind != KERNIX_OP_LINEAR || n->n_in != 1 || n->inp[0] != i + 1) return 0;
+    const kernix_val* v = &m->vals[i + 1];
+    if (v->last != i + 1 || m->out_v == i + 1 || fusable_add(m, i + 1) >= 0) return 0;
+    /* the launch writes both outputs (the step temporaries it reads are outside the value storage) */
+    if (!rnn_persistent(m) || n->in != s->out || knx_storage_overlaps(m, i + 1, i + 2)) return 0;
+    const int B = m->views[s->inp[0]].row / s->seq;
+    if (B <= 0) return 0;
+    const int rec_i8 = s->q != NULL && (m->int8_mode == KERNIX_INT8_I8 || B <= KERNIX_INT8_MAX_ROWS);
+    const int lin_i8 = n->q != NULL && (m->int8_mode == KERNIX_INT8_I8 || B <= KERNIX_INT8_MAX_ROWS);
+    if (n->q != NULL && !lin_i8 && n->deq == NULL) return 0;
+    return knx_hip_rnn_recurrence_dense_fits(s->kind, B, s->out, rec_i8, n->out);
+}
+
+/* Runs RNN step i with the LINEAR step i + 1 (see rnn_dense_fusable). */
+static int run_rnn_dense(kernix_model* m, int i, void* st)
+{
+    kernix_step* s = &m->steps[i];
+    const kernix_step* n = &m->steps[i + 1];
+    const struct knx_dstep* d = n->dev;
+    const float_tensor* x = &m->views[s->inp[0]];
+    const int B = x->row / s->seq;
+    const int lin_i8 = n->q != NULL && (m->int8_mode == KERNIX_INT8_I8 || B <= KERNIX_INT8_MAX_ROWS);
+    struct rnn_dense dn;
+    dn.w = lin_i8 ? NULL : n->q != NULL ? n->deq->tensor : d->w;
+    dn.q = lin_i8 ? d->q : NULL;
+    dn.kp = lin_i8 ? n->q->kp : 0;
+    dn.qscale = lin_i8 ? d->qscale : NULL;
+    dn.bias = d->bias;
+    dn.n = n->out;
+    dn.act = n->act;
+    dn.alpha = n->alpha;
+    dn.y = m->views[i + 2].tensor;
+    return run_rnn_dir(m, s, 0, x, m->views[i + 1].tensor, s->out, st, &dn);
+}
+
 /* LAYERNORM step i whose output is read only by step i + 1, an int8 LINEAR that runs int8 arithmetic at more than 4
  * rows (i8 mode) and so quantizes its input rows anyway: both run as knx_hip_layernorm_quantize into the LINEAR's
  * int8 scratch and the int8 GEMM, and the fp32 LAYERNORM output is never written.  The normalized rows are computed
@@ -951,6 +1020,11 @@ static int run_chunk(kernix_model* m, const float* in, int B, float* out, void* 
                        "Linear chain"))
                 return -1;
             i += nc - 1;
+            continue;
+        }
+        if (fuse && rnn_dense_fusable(m, i)) {
+            if (run_rnn_dense(m, i, st) != 0) return -1;
+            i++;
             continue;
         }
         if (fuse && ln_quant_fusable(m, i)) {

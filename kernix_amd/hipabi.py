@@ -58,6 +58,7 @@ SIGS = {
     "knx_hip_linear_chain": ([P, I, I, ctypes.POINTER(ChainLayer), I, P, Z, P, P], I),
     "knx_hip_memset": ([P, I, Z, P], I),
     "knx_hip_rnn_recurrence_fits": ([I, I, I, I], I),
+    "knx_hip_rnn_recurrence_dense_fits": ([I, I, I, I, I], I),
     "knx_hip_rnn_recurrence": ([I, I, F, I, I, I, I, P, P, I, P, I, P, P, P, P, P, I, I, P, Z, P, P], I),
 }
 

@@ -158,6 +158,43 @@ def test_recurrence_int8_rows_of_any_word_pitch(kind, u):
     assert np.array_equal(outs[0], outs[1])
 
 
+@pytest.mark.parametrize("cell,units", [("LSTM", 128), ("GRU", 40), ("RNN", 100)])
+@pytest.mark.parametrize("int8,mode", [(False, "ref"), (True, "ref"), (True, "i8")])
+@pytest.mark.parametrize("batch", [1, 2, 17, 300])
+def test_recurrence_runs_its_linear_in_the_same_launch(tmp_path, monkeypatch, cell, units, int8, mode, batch):
+    """a one-direction recurrence whose last state only feeds a Linear runs that Linear at the end of its own launch
+    (knx_hip_rnn_recurrence_dense): against the separate steps (KNX_NO_FUSE=1), an int8 Linear gives the same bits
+    (the same quantizer, int32 sums and epilogue), an fp32 one is within 1e-5; with and without the Linear's bias and
+    activation; and the forward against the oracle"""
+    from kernix_amd.knxfile import ModelBuilder
+
+    rng = np.random.default_rng(units + batch)
+    T, F, n = 6, 24, 12
+    g = {"LSTM": 4, "GRU": 3, "RNN": 1}[cell] * units
+    b = ModelBuilder((T, F), int8=int8)
+    h = b.recurrent(b.input, cell, units, [(rng.normal(0, 1 / np.sqrt(F), (F, g)), rng.normal(0, 1 / np.sqrt(units), (units, g)),
+                                           rng.normal(0, 0.01, 2 * g if cell == "GRU" else g))])
+    bias = None if cell == "GRU" else rng.normal(0, 0.1, n)
+    h = b.linear(h, rng.normal(0, 1 / np.sqrt(units), (units, n)), bias, activation="relu" if cell == "LSTM" else None)
+    p = str(tmp_path / "d.knx")
+    b.save(p)
+    x = rng.normal(0, 1, (batch, T, F)).astype(np.float32)
+    L = hipabi.lib()
+    kind = {"LSTM": 4, "GRU": 5, "RNN": 6}[cell]
+    rec_i8 = int8 and (mode == "i8" or batch <= 2)
+    assert L.knx_hip_rnn_recurrence_dense_fits(kind, batch, units, int(rec_i8), n) == 1
+    got = forward(p, x, mode, monkeypatch, True)
+    monkeypatch.setenv("KNX_NO_FUSE", "1")
+    sep = forward(p, x, mode, monkeypatch, True)
+    monkeypatch.delenv("KNX_NO_FUSE")
+    if rec_i8:
+        assert np.array_equal(got, sep)
+    else:
+        assert rel_err(got, sep) <= 1e-5
+    want, _ = knx_ref.forward(knx_ref.parse(p), x.reshape(-1, F), mode=mode)
+    assert rel_err(got.reshape(want.shape), want) <= (1e-2 if rec_i8 else 1e-4)
+
+
 def test_recurrence_entry_point_rejects(monkeypatch):
     L = hipabi.lib()
     hipabi.check(L.knx_hip_init())
@@ -165,6 +202,8 @@ def test_recurrence_entry_point_rejects(monkeypatch):
     assert L.knx_hip_rnn_recurrence_fits(4, 1000, 128, 0) == 1  # U fits a workgroup: the rows split, any batch
     assert L.knx_hip_rnn_recurrence_fits(4, 65, 256, 0) == 0  # neither form: the per-timestep path
     assert L.knx_hip_rnn_recurrence_fits(4, 64, 256, 0) == 1  # the grid form
+    assert L.knx_hip_rnn_recurrence_dense_fits(4, 64, 256, 0, 10) == 0  # the Linear only joins the batch-split form
+    assert L.knx_hip_rnn_recurrence_dense_fits(4, 1000, 128, 1, 10) == 1
     assert L.knx_hip_rnn_recurrence_fits(7, 1, 128, 0) == 0
     assert L.knx_hip_rnn_recurrence_fits(4, 64, 4096, 0) == 0  # h does not fit a workgroup's LDS
 
@@ -175,7 +214,7 @@ def test_forward_uses_the_persistent_recurrence(tmp_path, monkeypatch, batch, un
     forward) and the per-timestep launches otherwise or with KNX_RNN_PERSISTENT=0"""
     p = str(tmp_path / "l.knx")
     x = configs.lstm(p, batch=batch, T=4, fin=16, units=units)
-    monkeypatch.setenv("KNX_HIP_FAIL", "knx_hip_rnn_recurrence")
+    monkeypatch.setenv("KNX_HIP_FAIL", "knx_hip_rnn_recurrence,knx_hip_rnn_recurrence_dense")
     m = Model(p)
     try:
         if expect:
