@@ -402,14 +402,13 @@ __device__ __forceinline__ void lds_barrier()
 // of U runs its rows' timesteps alone: no h exchange through memory and no barrier across workgroups, whose round trips
 // are the cost of a multi-workgroup step at these sizes, and no workgroup waits for another (nothing needs to be
 // resident together).  One workgroup of 1024 threads keeps all of U in registers and h in LDS, so a timestep is two
-// workgroup barriers and no global synchronization (three with int8 arithmetic).  fp32: thread t owns column
+// workgroup barriers and no global synchronization.  fp32: thread t owns column
 // c = t / KS and its 64-value k-slice s = t % KS, KS lanes per column (consecutive lanes, so their partial sums are
 // reduced by exchanges; the lanes of one slice read the same h values, 16 bytes at a time), FMAs on the VALU.  int8:
 // the products on the matrix cores, the rows of h as the rows of A of v_mfma_i32_16x16x64_i8 (one or two of its 16:
 // at u = 128 a wave still needs only four per timestep, against 32 dot4 instructions per lane and the reduction).  Same
-// quantizer, int32 sums, epilogue and cells as above; with int8 arithmetic the cells that write h_t also gather its
-// row maxima (per wave, then one LDS atomic per wave and row), and at the next step every cell quantizes its own value
-// with its row's scale, so the quantization is one multiply-and-round per thread instead of a pass over the rows.
+// quantizer, int32 sums, epilogue and cells as above; with int8 arithmetic one wave holds a row's cells (two units per
+// lane), takes the row maximum of h_t by lane exchanges and quantizes the row right after the cells.
 constexpr int kSoloThreads = 1024;
 constexpr int kSoloRegs = 64;   // fp32: U values per thread
 constexpr int kSoloRows = 2;
@@ -423,7 +422,6 @@ __global__ void __launch_bounds__(kSoloThreads) rnn_solo(RnnArgs a, int KS, int 
     __shared__ __attribute__((aligned(16))) float hs[kSoloRows][2048];  // h_{t−1}, fp32 (u ≤ 2048), zero past u
     __shared__ __attribute__((aligned(16))) int hq[kSoloRows][512];     // its int8 rows, four to a word
     __shared__ float sxs[kSoloRows];
-    __shared__ unsigned rmx[2][kSoloRows];  // int8: each row's max |h| as bits, by the parity of the step that wrote h
     __shared__ float r[kSoloRows][kSoloThreads];                        // recurrent terms (gates·u ≤ 1024)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     // this workgroup's rows of the batch: [row0, row0 + B) (the rows of a recurrence never meet)
@@ -443,7 +441,6 @@ __global__ void __launch_bounds__(kSoloThreads) rnn_solo(RnnArgs a, int KS, int 
     const int nb = (gu + 15) / 16, nkc = (u + 63) / 64;
     for (int e = tid; e < kSoloRows * 2048; e += kSoloThreads) (&hs[0][0])[e] = 0.0f;
     for (int e = tid; e < kSoloRows * 512; e += kSoloThreads) (&hq[0][0])[e] = 0;
-    if (tid < 2 * kSoloRows) (&rmx[0][0])[tid] = 0u;
     float uf[I8 ? 1 : REGS];
     v4i ub[I8 ? kSoloBlocks : 1][I8 ? kSoloChunks : 1];
     float csc[I8 ? kSoloBlocks : 1], cbi[I8 ? kSoloBlocks : 1];
@@ -489,47 +486,42 @@ __global__ void __launch_bounds__(kSoloThreads) rnn_solo(RnnArgs a, int KS, int 
     }
     __syncthreads();
     const float col_bias = !I8 && a.brec ? a.brec[cc] : 0.0f;  // fp32 (int8: cbi)
-    // cell phase: thread tid < B·u owns row b = tid / u, unit j = tid % u
-    const bool cell = tid < B * u;
-    const int cb = cell ? tid / u : 0, cj = cell ? tid % u : 0;
-    float cst = 0.0f, hreg = 0.0f;  // the cell's c and h
-    // the input-side gate values of this thread's cell, one timestep ahead (they do not depend on h)
-    auto load_z = [&](int st, float (&z)[4]) {
+    // cell phase: fp32 — thread tid < B·u owns row tid / u, unit tid % u; int8 — wave b < B owns row b, lane l its
+    // units l and l + 64 (u ≤ 128), so the wave that writes a row of h_t also takes its maximum by lane exchanges and
+    // quantizes it for the next timestep's products, before the timestep's last barrier
+    constexpr int NU = I8 ? 2 : 1;  // units per thread
+    const bool cell = I8 ? wave < B : tid < B * u;
+    const int cb = cell ? (I8 ? wave : tid / u) : 0;
+    const int cj0 = I8 ? lane : (cell ? tid % u : 0);  // unit of slot 0 (int8: slot i is unit cj0 + 64·i)
+    float cst[NU];  // the cells' c
+#pragma unroll
+    for (int i = 0; i < NU; ++i) cst[i] = 0.0f;
+    // the input-side gate values of this thread's cells, one timestep ahead (they do not depend on h)
+    auto load_z = [&](int st, float (&z)[NU][4]) {
         const int tt = a.dir ? T - 1 - st : st;
 #pragma unroll
-        for (int g = 0; g < 4; ++g) z[g] = cell && g < G ? zx[((size_t)cb * T + tt) * gu + (size_t)g * u + cj] : 0.0f;
+        for (int i = 0; i < NU; ++i) {
+            const int j = cj0 + 64 * i;
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                z[i][g] = cell && j < u && g < G ? zx[((size_t)cb * T + tt) * gu + (size_t)g * u + j] : 0.0f;
+        }
     };
-    float zn[4];
+    float zn[NU][4];
     load_z(0, zn);
     for (int step = 0; step < T; ++step) {
         const int t = a.dir ? T - 1 - step : step;
-        float zv[4];
+        float zv[NU][4];
 #pragma unroll
-        for (int g = 0; g < 4; ++g) zv[g] = zn[g];
+        for (int i = 0; i < NU; ++i)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) zv[i][g] = zn[i][g];
         if (step + 1 < T) load_z(step + 1, zn);
         if (step > 0) {
             if (I8) {
-                // each cell quantizes its own h_{t−1} with its row's scale (the row maximum was gathered by the cells
-                // that wrote it: s = max|h|/127, 1 for an all-zero row, NaN for a row holding NaN or ±inf;
-                // q = clamp(rint(h·(1/s)), ±127); bytes past u stay 0; a row that cannot be quantized stores zeros:
-                // its outputs are NaN through its scale); this step's row maxima start from 0
-                if (cell) {
-                    const unsigned mb = rmx[(step - 1) & 1][cb];
-                    const bool bad = mb >= 0x7f800000u;
-                    const float mx = __uint_as_float(mb);
-                    const float sc = (!bad && mx > 0.0f) ? __fdiv_rn(mx, 127.0f) : 1.0f;
-                    const float inv = bad ? 0.0f : __fdiv_rn(1.0f, sc);
-                    if (cj == 0) sxs[cb] = bad ? __int_as_float(0x7fc00000) : sc;
-                    const float qv = __builtin_amdgcn_fmed3f(rintf(hreg * inv), -127.0f, 127.0f);
-                    reinterpret_cast<int8_t*>(&hq[cb][0])[cj] = (int8_t)(int)qv;
-                }
-                if (tid < B) rmx[step & 1][tid] = 0u;
-                lds_barrier();
-            }
-            if (I8) {
-                // the rows of h_{t−1} as rows of A (rows from B on repeat row B − 1; their sums are not used), exact
-                // int32 sums in lanes fq = 0 (row b in element b), then the int8 GEMM's epilogue
-                // ((float)acc · sx) · scale (+ bias)
+                // the rows of h_{t−1} (quantized by the cells that wrote them) as rows of A (rows from B on repeat row
+                // B − 1; their sums are not used), exact int32 sums in lanes fq = 0 (row b in element b), then the
+                // int8 GEMM's epilogue ((float)acc · sx) · scale (+ bias)
                 const int arow = fr < B ? fr : B - 1;
                 v4i af[kSoloChunks];
 #pragma unroll
@@ -575,40 +567,57 @@ __global__ void __launch_bounds__(kSoloThreads) rnn_solo(RnnArgs a, int KS, int 
                 }
             }
         }
-        lds_barrier();  // r complete; every read of hs done
-        float hv = 0.0f;
+        lds_barrier();  // r complete; every read of hs, hq and sxs done
         if (cell) {
             const bool first = step == 0;
-            auto rec = [&](int g) { return r[cb][g * u + cj]; };
-            if (KIND == 4) {
-                float zi = zv[0], zf = zv[1], zg = zv[2], zo = zv[3];
-                if (!first) { zi = zi + rec(0); zf = zf + rec(1); zg = zg + rec(2); zo = zo + rec(3); }
-                hv = knx_lstm_cell(zi, zf, zg, zo, act, a.alpha, first, cst);
-            } else if (KIND == 5) {
-                const float hz = first ? a.brec[cj] : rec(0);
-                const float hr = first ? a.brec[u + cj] : rec(1);
-                const float hh = first ? a.brec[2 * u + cj] : rec(2);
-                hv = knx_gru_cell(zv[0], zv[1], zv[2], hz, hr, hh, act, a.alpha, first, first ? 0.0f : hs[cb][cj]);
-            } else {
-                float v = zv[0];
-                if (!first) v = v + rec(0);
-                hv = knx_gate_act(v, act, a.alpha);
+            auto rec = [&](int g, int j) { return r[cb][g * u + j]; };
+            float hv[NU];
+            unsigned mb = 0u;  // int8: the row maximum of |h_t| as bits (NaN above +inf above every finite value)
+#pragma unroll
+            for (int i = 0; i < NU; ++i) {
+                const int j = cj0 + 64 * i;
+                hv[i] = 0.0f;
+                if (j >= u) continue;
+                if (KIND == 4) {
+                    float zi = zv[i][0], zf = zv[i][1], zg = zv[i][2], zo = zv[i][3];
+                    if (!first) { zi = zi + rec(0, j); zf = zf + rec(1, j); zg = zg + rec(2, j); zo = zo + rec(3, j); }
+                    hv[i] = knx_lstm_cell(zi, zf, zg, zo, act, a.alpha, first, cst[i]);
+                } else if (KIND == 5) {
+                    const float hz = first ? a.brec[j] : rec(0, j);
+                    const float hr = first ? a.brec[u + j] : rec(1, j);
+                    const float hh = first ? a.brec[2 * u + j] : rec(2, j);
+                    hv[i] = knx_gru_cell(zv[i][0], zv[i][1], zv[i][2], hz, hr, hh, act, a.alpha, first,
+                                         first ? 0.0f : hs[cb][j]);
+                } else {
+                    float v = zv[i][0];
+                    if (!first) v = v + rec(0, j);
+                    hv[i] = knx_gate_act(v, act, a.alpha);
+                }
+                hs[cb][j] = hv[i];
+                if (I8) mb = max(mb, __float_as_uint(hv[i]) & 0x7fffffffu);
+                if (a.ret_seq) dst[((size_t)cb * T + t) * a.stride + j] = hv[i];
+                else if (step + 1 == T) dst[(size_t)cb * a.stride + j] = hv[i];
             }
-            hs[cb][cj] = hv;
-            hreg = hv;
-            if (a.ret_seq) dst[((size_t)cb * T + t) * a.stride + cj] = hv;
-            else if (step + 1 == T) dst[(size_t)cb * a.stride + cj] = hv;
-        }
-        if (I8 && step + 1 < T) {
-            // the row maxima of h_t (|h| as bits: NaN above +inf above every finite value) for the next step's
-            // quantization: per wave and row, then one LDS atomic per wave
-            const unsigned mb = __float_as_uint(hv) & 0x7fffffffu;
-            for (int rb = 0; rb < B; ++rb) {
-                const unsigned v = knx_lane_group_max(cell && cb == rb ? mb : 0u, 64);
-                if (lane == 0 && v != 0u) atomicMax(&rmx[step & 1][rb], v);
+            if (I8 && step + 1 < T) {
+                // h_t's int8 row for the next timestep: s = max|h|/127, 1 for an all-zero row, NaN for a row holding
+                // NaN or ±inf; q = clamp(rint(h·(1/s)), ±127); bytes past u stay 0; a row that cannot be quantized
+                // stores zeros (its outputs are NaN through its scale)
+                mb = knx_lane_group_max(mb, 64);
+                const bool bad = mb >= 0x7f800000u;
+                const float mx = __uint_as_float(mb);
+                const float sc = (!bad && mx > 0.0f) ? __fdiv_rn(mx, 127.0f) : 1.0f;
+                const float inv = bad ? 0.0f : __fdiv_rn(1.0f, sc);
+                if (lane == 0) sxs[cb] = bad ? __int_as_float(0x7fc00000) : sc;
+#pragma unroll
+                for (int i = 0; i < NU; ++i) {
+                    const int j = cj0 + 64 * i;
+                    if (j < u)
+                        reinterpret_cast<int8_t*>(&hq[cb][0])[j] =
+                            (int8_t)(int)__builtin_amdgcn_fmed3f(rintf(hv[i] * inv), -127.0f, 127.0f);
+                }
             }
         }
-        lds_barrier();  // h_t (and its row maxima) complete in LDS
+        lds_barrier();  // h_t (and its int8 row and scale) complete in LDS
     }
     if (a.dn > 0) {
         // The LINEAR after the recurrence, on h_T still in LDS (zero past u).  int8: each row quantized by one wave with
