@@ -14,10 +14,13 @@ the model's device workspace.  Use one Model per thread to run concurrently.
 
 The shared library is kernix_amd/libkernix.so, or the file named by $KERNIX_LIB.  It is opened on first use (the first
 Model, or the first call of an extension), not at import; opening fails with OSError when the library is missing or
-was built for another target — there is no CPU fallback.
+was built for another target — there is no CPU fallback.  Where PyTorch is installed, its own HIP runtime is loaded
+first (without importing torch), so that the library and torch share one runtime whichever is imported first.
 """
 import ctypes
+import importlib.util
 import os
+import sys
 import threading
 import warnings
 
@@ -55,6 +58,28 @@ def library_path():
     return os.environ.get("KERNIX_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), "libkernix.so")
 
 
+def _share_torch_runtime():
+    """PyTorch-ROCm wheels ship their own HIP runtime (torch/lib/libamdhip64.so, the soname libkernix.so links).  When
+    torch is installed but not imported yet, load its copy before the library (without importing torch): the library
+    then binds to it, and a later `import torch` uses the same one instead of loading a second runtime, which would
+    leave the library without a device.  Nothing to do when torch is already imported (its runtime is loaded) or not
+    installed (the system runtime); KNX_SYSTEM_HIP=1 keeps the system runtime."""
+    if "torch" in sys.modules or os.environ.get("KNX_SYSTEM_HIP", "") not in ("", "0"):
+        return
+    try:
+        spec = importlib.util.find_spec("torch")
+    except (ImportError, ValueError):
+        return
+    for d in (spec.submodule_search_locations or []) if spec is not None else []:
+        path = os.path.join(d, "lib", "libamdhip64.so")
+        if os.path.exists(path):
+            try:
+                ctypes.CDLL(path, mode=ctypes.RTLD_GLOBAL)
+            except OSError:
+                pass
+            return
+
+
 class _Library:
     """libkernix.so with its entry points typed, opened once on first attribute access."""
 
@@ -65,6 +90,7 @@ class _Library:
     def _open(self):
         with self._opening:
             if self._dll is None:
+                _share_torch_runtime()
                 dll = ctypes.CDLL(library_path())
                 for name, (args, res) in _ABI.items():
                     fn = getattr(dll, name)

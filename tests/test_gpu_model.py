@@ -408,3 +408,41 @@ def test_ffn_fusions_full_size(tmp_path, monkeypatch):
         outs.append(np.array(m(x)))
         m.close()
     assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+
+
+_TORCH_AFTER = r"""
+import sys
+import numpy as np
+sys.path.insert(0, sys.argv[1])
+from kernix_amd import configs
+from kernix_amd.kernix import Model
+x = configs.int8_mlp(sys.argv[2], batch=3)
+m = Model(sys.argv[2])
+y1 = m(x)
+assert "torch" not in sys.modules
+import torch
+t = torch.arange(4, dtype=torch.float32, device="cuda") * 2
+assert float(t.sum()) == 12.0
+y2 = m(x)
+m.close()
+np.save(sys.argv[3], np.stack([y1, y2]))
+print("ok")
+"""
+
+
+def test_model_before_torch_import(tmp_path):
+    """a Model created and run before `import torch` keeps working after it (the binding loads torch's HIP runtime
+    before the library, so the two share one): a child process runs the forward, imports torch, uses the device
+    through torch and runs the forward again; both outputs match the oracle"""
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    p, out = str(tmp_path / "m.knx"), str(tmp_path / "y.npy")
+    r = subprocess.run([sys.executable, "-c", _TORCH_AFTER, root, p, out], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0 and r.stdout.strip().endswith("ok"), r.stderr[-2000:]
+    y = np.load(out)
+    assert np.array_equal(y[0], y[1])
+    x = configs.int8_mlp(p, batch=3)
+    want, _ = knx_ref.forward(knx_ref.parse(p), x.reshape(3, -1))
+    assert rel_err(y[0], want) <= 1e-4
