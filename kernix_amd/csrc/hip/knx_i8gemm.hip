@@ -1594,41 +1594,37 @@ __global__ void __launch_bounds__(256) quantize_rows_vec(const float* __restrict
     const float4* xr = reinterpret_cast<const float4*>(x + (size_t)row * ldx);
     const int nq = k >> 2, nqp = kp >> 2;
     float4 v[NV];
-    float m = 0.0f;
-    int bad = 0;
+    // the row maximum of |x| as integer bits: NaN above ±inf above every finite value, so one maximum also finds a row
+    // that cannot be quantized; DPP and register swaps across the wave
+    unsigned mb = 0u;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
         const int q = i * 64 + lane;
         v[i] = q < nq ? xr[q] : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const float a = fabsf(q4e(v[i], e));
-            if (!(a <= 3.402823466e38f)) bad = 1;  // NaN or ±inf
-            else m = a > m ? a : m;
-        }
+        for (int e = 0; e < 4; ++e) mb = max(mb, __float_as_uint(q4e(v[i], e)) & 0x7fffffffu);
     }
-    m = knx_wave_max(m);
-    bad = __any(bad);
+    mb = knx_lane_group_max(mb, 64);
     int* qr = reinterpret_cast<int*>(xq + (size_t)row * ldq);
-    if (bad) {
+    if (mb >= 0x7f800000u) {  // NaN or ±inf
         for (int q = lane; q < nqp; q += 64) qr[q] = 0;
         if (lane == 0) sx[row] = __int_as_float(0x7fc00000);
         return;
     }
+    const float m = __uint_as_float(mb);
     const float s = m > 0.0f ? __fdiv_rn(m, 127.0f) : 1.0f;
     const float inv = __fdiv_rn(1.0f, s);
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
         const int q = i * 64 + lane;
         if (q >= nq) continue;
+        // q = clamp(rint(x·inv), ±127) by v_med3; q + 128 converts exactly to a byte, and ^ 0x80 makes it q's byte
         unsigned w = 0;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const float r = rintf(q4e(v[i], e) * inv);
-            const int b = (int)(r > 127.0f ? 127.0f : r < -127.0f ? -127.0f : r);
-            w |= (unsigned)(b & 0xff) << (8 * e);
-        }
-        qr[q] = (int)w;
+        for (int e = 0; e < 4; ++e)
+            w = __builtin_amdgcn_cvt_pk_u8_f32(
+                __builtin_amdgcn_fmed3f(rintf(q4e(v[i], e) * inv), -127.0f, 127.0f) + 128.0f, e, w);
+        qr[q] = (int)(w ^ 0x80808080u);
     }
     for (int q = nq + lane; q < nqp; q += 64) qr[q] = 0;
     if (lane == 0) sx[row] = s;

@@ -307,6 +307,8 @@ def test_quantize_rows_bit_exact(L, rows, k):
     if rows >= 3:
         x[1, k // 2] = np.nan
         x[2, :] = 0.0
+    if rows >= 4:
+        x[3, k - 1] = -np.inf
     kp = (k + 63) // 64 * 64
     xq_want, sx_want, bad = knx_ref.quantize_rows(x)
     dx = dev(x)
