@@ -61,9 +61,7 @@ __global__ void __launch_bounds__(256) softmax_kernel(const float* __restrict__ 
 template <int G>
 __device__ __forceinline__ float group_sum(float v)
 {
-#pragma unroll
-    for (int o = G / 2; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+    return knx_lane_group_sum(v, G);  // DPP and gfx950's register swaps (every lane of the group gets the sum)
 }
 template <int G>
 __device__ __forceinline__ float group_max(float v)
@@ -152,25 +150,22 @@ __global__ void __launch_bounds__(256) layernorm_quant_vec(const float* x, int r
     float4 o[NV];
     ln_row<G, NV>(x, row, cols, l, gamma, beta, eps, o);
     const int nq = cols >> 2, nqp = kp >> 2;
-    float m = 0.0f;
-    float bad = 0.0f;
+    // the quantizer's operations as knx_hip_quantize_rows: the row maximum of |x| as integer bits (NaN above ±inf above
+    // every finite value), q = clamp(rint(x·inv), ±127) by v_med3, bytes by cvt_pk_u8 of q + 128, ^ 0x80
+    unsigned mb = 0u;
 #pragma unroll
     for (int i = 0; i < NV; ++i)
         if (i * G + l < nq)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float a = fabsf(f4(o[i], e));
-                if (!(a <= 3.402823466e38f)) bad = 1.0f;  // NaN or ±inf
-                else m = a > m ? a : m;
-            }
-    m = group_max<G>(m);
-    bad = group_max<G>(bad);
+            for (int e = 0; e < 4; ++e) mb = max(mb, __float_as_uint(f4(o[i], e)) & 0x7fffffffu);
+    mb = knx_lane_group_max(mb, G);
     int* qr = reinterpret_cast<int*>(xq + (size_t)row * kp);
-    if (bad != 0.0f) {
+    if (mb >= 0x7f800000u) {  // NaN or ±inf
         for (int q = l; q < nqp; q += G) qr[q] = 0;
         if (l == 0) sx[row] = __int_as_float(0x7fc00000);
         return;
     }
+    const float m = __uint_as_float(mb);
     const float s = m > 0.0f ? __fdiv_rn(m, 127.0f) : 1.0f;
     const float inv = __fdiv_rn(1.0f, s);
 #pragma unroll
@@ -179,12 +174,10 @@ __global__ void __launch_bounds__(256) layernorm_quant_vec(const float* x, int r
         if (q >= nq) continue;
         unsigned w = 0;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const float r = rintf(f4(o[i], e) * inv);
-            const int b = (int)(r > 127.0f ? 127.0f : r < -127.0f ? -127.0f : r);
-            w |= (unsigned)(b & 0xff) << (8 * e);
-        }
-        qr[q] = (int)w;
+        for (int e = 0; e < 4; ++e)
+            w = __builtin_amdgcn_cvt_pk_u8_f32(
+                __builtin_amdgcn_fmed3f(rintf(f4(o[i], e) * inv), -127.0f, 127.0f) + 128.0f, e, w);
+        qr[q] = (int)(w ^ 0x80808080u);
     }
     for (int q = nq + l; q < nqp; q += G) qr[q] = 0;
     if (l == 0) sx[row] = s;
