@@ -368,6 +368,23 @@ def forward_bench(name, make, flops, steps, warmup, mode="ref", i8_ops=0.0, cpu=
         stream = torch.cuda.Stream()
         st = stream.cuda_stream
 
+        # end to end through kernix_capi_forward (host buffers, PCIe included), before the device forwards (so that
+        # the timed device forwards end the run of identical launch sequences in a kernel trace): untimed calls for
+        # 50 ms (at least one), then calls back to back for at least 0.2 s (at least 2) — a handful of calls after an
+        # idle spell times the clock ramp, not the path
+        n_host = 0
+        t0 = time.perf_counter()
+        while n_host < 1 or time.perf_counter() - t0 < 0.05:
+            m(x)
+            n_host += 1
+        n_e2e = 0
+        t0 = time.perf_counter()
+        while n_e2e < 2 or time.perf_counter() - t0 < 0.2:
+            m(x)
+            n_e2e += 1
+        e2e = (time.perf_counter() - t0) * 1e3 / n_e2e
+        n_host += n_e2e
+
         n_dev = [0]
 
         def run():
@@ -376,12 +393,6 @@ def forward_bench(name, make, flops, steps, warmup, mode="ref", i8_ops=0.0, cpu=
 
         with torch.cuda.stream(stream):
             ms, _ = time_launches(run, steps, warmup, warm_ms)
-        m(x)  # end to end through kernix_capi_forward (host buffers, PCIe included)
-        t0 = time.perf_counter()
-        n_e2e = max(2, steps // 4)
-        for _ in range(n_e2e):
-            m(x)
-        e2e = (time.perf_counter() - t0) * 1e3 / n_e2e
         seq = m.seq_len
         m.close()
         base = {}
@@ -394,7 +405,7 @@ def forward_bench(name, make, flops, steps, warmup, mode="ref", i8_ops=0.0, cpu=
     res = dict(batch=B, ms=round(ms, 4), samples_per_s=round(B / (ms * 1e-3), 1),
                e2e_ms=round(e2e, 3), e2e_samples_per_s=round(B / (e2e * 1e-3), 1),
                tflops=round(tf, 2), roofline_frac=round(ideal_ms / ms, 4), mode=mode,
-               forwards={"device": n_dev[0], "host": 1 + n_e2e})
+               forwards={"device": n_dev[0], "host": n_host})
     if base:
         res["cpu_baseline"] = base
     return res

@@ -224,8 +224,8 @@ __global__ void __launch_bounds__(kThreads) rnn_recurrence(RnnArgs a)
         if (step > 0) {
             // h_{t−1} into LDS, a batch of up to kLoads float4s per lane issued before the first is used; int8: each
             // row quantized from the registers (s = max|h|/127, 1 for an all-zero row, NaN for a row holding NaN or
-            // ±inf; q = clamp(rint(h·(1/s)), ±127), four to a word; a row that cannot be quantized stores zeros:
-            // its outputs are NaN through its scale)
+            // ±inf; q = clamp(rint(h·(1/s)), ±127), four to a word; the bytes of a row that cannot be quantized do
+            // not matter: its products are NaN through its scale)
             for (int g = wave_u; g < ngr; g += kWaves) {
                 const int b = g * RPW + rsub;
                 float4 v[kLoads];
@@ -252,8 +252,8 @@ __global__ void __launch_bounds__(kThreads) rnn_recurrence(RnnArgs a)
                     // the row's max |h| as bits (NaN above +inf above every finite value) over its LR lanes, the
                     // quantizer's scale (max/127, 1 for an all-zero row, NaN for a row holding NaN or ±inf) and
                     // q = clamp(rint(h·(1/s)), ±127), four to a word; + 128 is an exact integer that converts
-                    // exactly to a byte; a row that cannot be quantized stores zeros: its outputs are NaN through its
-                    // scale
+                    // exactly to a byte; the bytes of a row that cannot be quantized do not matter: its products are
+                    // NaN through its scale
                     unsigned m = 0;
 #pragma unroll
                     for (int s = 0; s < kLoads; ++s) {
@@ -600,8 +600,8 @@ __global__ void __launch_bounds__(kSoloThreads) rnn_solo(RnnArgs a, int KS, int 
             }
             if (I8 && step + 1 < T) {
                 // h_t's int8 row for the next timestep: s = max|h|/127, 1 for an all-zero row, NaN for a row holding
-                // NaN or ±inf; q = clamp(rint(h·(1/s)), ±127); bytes past u stay 0; a row that cannot be quantized
-                // stores zeros (its outputs are NaN through its scale)
+                // NaN or ±inf; q = clamp(rint(h·(1/s)), ±127); bytes past u stay 0; the bytes of a row that cannot be
+                // quantized do not matter (its products are NaN through its scale)
                 mb = knx_lane_group_max(mb, 64);
                 const bool bad = mb >= 0x7f800000u;
                 const float mx = __uint_as_float(mb);
