@@ -93,6 +93,35 @@ def test_persistent_two_rows_per_workgroup(tmp_path, monkeypatch, int8, mode):
     assert rel_err(got.reshape(want.shape), want) <= (1e-2 if int8 else 1e-4)
 
 
+@pytest.mark.parametrize("seed", [1, 2])
+def test_recurrence_sweep(tmp_path, monkeypatch, seed):
+    """shapes drawn at random (cell, directions, units 1-300 log-uniform, inputs, timesteps, batch 1-300 log-uniform,
+    fp32 or int8 weights, ref or i8 mode): the one-launch recurrence (the row-split kernel where it fits, with the
+    Linear after a one-direction layer in the same launch) and the grid form against the per-timestep launches"""
+    rng = np.random.default_rng(seed)
+
+    def logu(lo, hi):
+        return int(np.exp(rng.uniform(np.log(lo), np.log(hi + 1))))
+
+    for case in range(20):
+        cell, dirs = str(rng.choice(["LSTM", "GRU", "RNN"])), int(rng.integers(1, 3))
+        units, fin, T, batch = logu(1, 300), logu(1, 64), int(rng.integers(1, 13)), logu(1, 300)
+        int8 = bool(rng.random() < 0.6)
+        mode = "i8" if int8 and rng.random() < 0.5 else "ref"
+        name = f"case {case}: {cell} dirs {dirs} units {units} fin {fin} T {T} batch {batch} int8 {int8} mode {mode}"
+        print(name, flush=True)
+        p = str(tmp_path / f"sweep{seed}_{case}.knx")
+        x = configs.lstm(p, seed=100 * seed + case, batch=batch, T=T, fin=fin, units=units, int8=int8, cell=cell,
+                         directions=dirs)
+        got = forward(p, x, mode, monkeypatch, True)
+        per_step = forward(p, x, mode, monkeypatch, False)
+        grid = forward(p, x, mode, monkeypatch, True, solo=False)
+        if int8 and (mode == "i8" or batch <= 2):
+            assert np.array_equal(got, per_step) and np.array_equal(grid, per_step), name
+        else:
+            assert rel_err(got, per_step) <= 1e-5 and rel_err(grid, per_step) <= 1e-5, name
+
+
 def test_persistent_returns_sequences_and_nan_rows(tmp_path, monkeypatch):
     """a sequence-returning bidirectional LSTM (every timestep's state at its own position, the backward direction
     from t = T-1) feeding a GRU, int8 in i8 mode; a sample holding NaN gives a NaN output row and leaves the others
