@@ -288,6 +288,52 @@ def test_linear_chain_matches_separate_steps(tmp_path, monkeypatch, mode, batch)
         assert rel_err(got["1"], got["0"]) <= 1e-5
 
 
+@pytest.mark.parametrize("seed", [1, 2])
+def test_linear_chain_sweep(tmp_path, monkeypatch, seed):
+    """Random MLPs (1-5 Linear layers of widths 1-2048 log-uniform, fp32 / int8-column / int8-row weights, with or
+    without bias, activations with and without transcendentals), batch 1-64, ref or i8 mode: the forward with chains
+    against the layers launched one by one (KNX_CHAIN=0) — the same bits where every layer runs int8 arithmetic (int8
+    column weights in i8 mode or at <= 2 rows), within 1e-5 otherwise."""
+    from kernix_amd.knxfile import ModelBuilder
+
+    rng = np.random.default_rng(seed)
+
+    def logu(lo, hi):
+        return int(np.exp(rng.uniform(np.log(lo), np.log(hi + 1))))
+
+    for case in range(25):
+        depth = int(rng.integers(1, 6))
+        dims = [logu(1, 2048) for _ in range(depth + 1)]
+        fmts = [str(rng.choice(["f32", "i8_col", "i8_row"])) for _ in range(depth)]
+        acts = [rng.choice([None, "relu", "gelu", "leaky_relu", "tanh", "sigmoid"]) for _ in range(depth)]
+        batch = logu(1, 64)
+        mode = str(rng.choice(["ref", "i8"]))
+        name = f"case {case}: dims {dims} formats {fmts} activations {acts} batch {batch} mode {mode}"
+        print(name, flush=True)
+        b = ModelBuilder((dims[0],))
+        h = b.input
+        for i in range(depth):
+            w = rng.normal(0.0, 1.0 / np.sqrt(dims[i]), (dims[i], dims[i + 1]))
+            bias = rng.normal(0.0, 0.1, dims[i + 1]) if rng.random() < 0.8 else None
+            h = b.linear(h, w, bias, activation=acts[i], alpha=0.1, fmt=fmts[i])
+        p = str(tmp_path / f"sweep{seed}_{case}.knx")
+        b.save(p)
+        x = rng.normal(0.0, 1.0, (batch, dims[0])).astype(np.float32)
+        got = {}
+        for chain in ("1", "0"):
+            monkeypatch.setenv("KNX_CHAIN", chain)
+            m = Model(p)
+            if mode == "i8":
+                m.set_int8_mode(INT8_I8)
+            got[chain] = m(x).copy()
+            m.close()
+        # int8 arithmetic needs int8-column weights (an int8-row block is dequantized to fp32 when it is read)
+        if all(f == "i8_col" for f in fmts) and (mode == "i8" or batch <= 2):
+            assert np.array_equal(got["1"], got["0"]), name
+        else:
+            assert rel_err(got["1"], got["0"]) <= 1e-5, name
+
+
 @pytest.mark.parametrize("batch", [1, 16])
 def test_linear_chain_gave_up_is_recomputed(tmp_path, monkeypatch, capfd, batch):
     """A chain launch whose barrier stops waiting (forced from the host: KNX_GRID_SPIN=0 stops every workgroup but
