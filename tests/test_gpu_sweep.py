@@ -1,12 +1,13 @@
 """Randomized parity sweep through the C ABI over shapes drawn log-uniformly within each entry point's contract: the
 int8 GEMM (with accumulate, residual and raw accumulators), the row quantizer (zero, NaN, ±inf and integral rows),
-the quantize + int8 GEMM call (both of its paths), the fp32 NT GEMM and the convolutions (groups, depthwise, stride,
-dilation, asymmetric padding, both weight layouts, residual).  The dispatch rules pick a different kernel by shape,
-so a sweep reaches tile/edge combinations that fixed cases miss.
+the quantize + int8 GEMM call (both of its paths), the fp32 NT GEMM, the convolutions (groups, depthwise, stride,
+dilation, asymmetric padding, both weight layouts, residual), the row and elementwise ops and the attention core.
+The dispatch rules pick a different kernel by shape, so a sweep reaches tile/edge combinations that fixed cases miss.
 
-References are the closed forms: int8 — exact int32 sums (float64 products of int8 values are exact integers below
-2^53) and the epilogue's fp32 steps in order, bit-exact (reference include/kernix_model.h:112-178); fp32 — float64,
-max|a−b| / max(1, max|ref|) ≤ 1e-4 (reference include/kernix.h:951-977, include/kernix_model.h:711-771).
+References: int8 — exact int32 sums (float64 products of int8 values are exact integers below 2^53) and the
+epilogue's fp32 steps in order, bit-exact (reference include/kernix_model.h:112-178); fp32 GEMM and convolution —
+float64, max|a−b| / max(1, max|ref|) ≤ 1e-4 (reference include/kernix.h:951-977, include/kernix_model.h:711-771);
+row ops, activations, binary ops and attention — the oracle's restatements, at the tolerances of their kernel tests.
 """
 import ctypes
 
@@ -276,3 +277,132 @@ def test_conv_sweep(L, seed):
         if res:
             ref = ref + R
         assert rel_err(dy.cpu().numpy(), ref) <= 1e-4, name
+
+
+@pytest.mark.parametrize("seed", [1, 2])
+def test_row_ops_sweep(L, seed):
+    """layer_norm (in place or not), layer_norm + quantize (the bits of layer_norm then the quantizer), softmax with
+    masked (−inf) entries, bias + each activation, elementwise binary ops with broadcast rows or channels: against the
+    oracle's restatements (layer_norm 1e-5, activations 2e-6 as their kernel test, binary ops and the quantized rows
+    bit-exact) and softmax against float64 (1e-5)"""
+    from oracle import knx_ref
+
+    rng = np.random.default_rng(seed)
+    st = hipabi.stream()
+    for case in range(40):
+        rows, cols = logu(rng, 1, 20000), logu(rng, 1, 4096)
+        while rows * cols > 2e7:
+            rows //= 2
+        inplace, eps = bool(rng.random() < 0.5), float(rng.choice([1e-5, 1e-6, 1e-3]))
+        act = int(rng.integers(-1, 16))
+        name = f"case {case}: rows {rows} cols {cols} in place {inplace} eps {eps} act {act}"
+        print(name, flush=True)
+        x = (rng.standard_normal((rows, cols)) * 3).astype(F32)
+        g = (1 + rng.normal(0, 0.5, cols)).astype(F32)
+        bt = rng.normal(0, 0.5, cols).astype(F32)
+        d = Device()
+        dx = d(x)
+        y = dx if inplace else torch.empty_like(dx)
+        hipabi.check(L.knx_hip_layernorm(ptr(dx), ptr(y), rows, cols, ptr(d(g)), ptr(d(bt)), eps, st))
+        torch.cuda.synchronize()
+        ln = y.cpu().numpy()
+        assert rel_err(ln, knx_ref.layernorm(x, g, bt, eps)) <= 1e-5, name
+        if cols % 4 == 0 and cols <= 2048:
+            kp = cols + 4 * int(rng.integers(0, 17))
+            dxq = torch.full((rows, kp), 99, dtype=torch.int8, device="cuda")
+            dsx = torch.zeros(rows, device="cuda")
+            dx2 = d(x)
+            hipabi.check(L.knx_hip_layernorm_quantize(ptr(dx2), rows, cols, ptr(d(g)), ptr(d(bt)), eps, kp, ptr(dxq),
+                                                      ptr(dsx), st))
+            torch.cuda.synchronize()
+            q, s = quantize(ln, cols, kp)  # the GPU layer_norm's own bits, quantized
+            assert np.array_equal(dxq.cpu().numpy(), q) and np.array_equal(dsx.cpu().numpy(), s), name
+        xm = x.copy()
+        if cols >= 2:
+            for r in rng.choice(rows, min(rows, 5), replace=False):
+                xm[r, int(rng.integers(1, cols)):] = -np.inf  # a causal row's masked tail (never the whole row)
+        dm = d(xm)
+        hipabi.check(L.knx_hip_softmax(ptr(dm), ptr(dm), rows, cols, st))
+        torch.cuda.synchronize()
+        xd = xm.astype(np.float64)
+        e = np.exp(xd - xd.max(axis=1, keepdims=True))
+        # against float64: the oracle's sequential float32 row sum (the reference's order) itself drifts by up to
+        # 1.5e-5 at 4096 columns
+        assert rel_err(dm.cpu().numpy(), e / e.sum(axis=1, keepdims=True)) <= 1e-5, name
+        xa = (x * 4 / 3).astype(F32)
+        ba = rng.normal(0, 1, cols).astype(F32)
+        da = d(xa)
+        hipabi.check(L.knx_hip_bias_act(ptr(da), ptr(da), rows, cols, ptr(d(ba)), act, 0.2, st))
+        torch.cuda.synchronize()
+        xb = (xa + ba).astype(F32)
+        want = xb if act == -1 else knx_ref.act(xb, act, 0.2)
+        assert np.allclose(da.cpu().numpy(), want, rtol=2e-6, atol=2e-6, equal_nan=True), name
+    for case in range(60):
+        op = int(rng.integers(0, 6))
+        B, R, C = logu(rng, 1, 16), logu(rng, 1, 300), logu(rng, 1, 600)
+        ra, ca = (R if rng.random() < 0.7 else 1), (C if rng.random() < 0.7 else 1)
+        rb, cb = (R if rng.random() < 0.7 else 1), (C if rng.random() < 0.7 else 1)
+        alias = ra == R and ca == C and rng.random() < 0.3
+        name = f"binary {case}: op {op} B {B} R {R} C {C} a {ra}x{ca} b {rb}x{cb} y is a {alias}"
+        print(name, flush=True)
+        a = rng.normal(0, 1, (B * ra, ca)).astype(F32)
+        b = (rng.normal(0, 1, (B * rb, cb)) + 2.5).astype(F32)
+        want = np.zeros((B * R, C), F32)
+        knx_ref.lib().ko_binary(op, knx_ref._p(a), ra, ca, knx_ref._p(b), rb, cb, knx_ref._p(want), B, R, C)
+        d = Device()
+        da = d(a)
+        y = da if alias else torch.empty((B * R, C), dtype=torch.float32, device="cuda")
+        hipabi.check(L.knx_hip_binary(op, ptr(da), ra, ca, ptr(d(b)), rb, cb, ptr(y), B, R, C, st))
+        torch.cuda.synchronize()
+        assert np.array_equal(y.cpu().numpy(), want), name
+
+
+@pytest.mark.parametrize("seed", [1, 2])
+def test_attention_sweep(L, seed):
+    """the attention core (fused where the shape allows, else the scores GEMM, softmax and P·V) over random batch,
+    heads, query and key counts, head widths, causal masks, and the strided form with and without the Vᵀ scratch,
+    against the oracle's loop (reference include/kernix_model.h:1021-1046), 1e-4"""
+    from oracle import knx_ref
+
+    rng = np.random.default_rng(seed)
+    st = hipabi.stream()
+    for case in range(40):
+        B, H, Rq, S = logu(rng, 1, 16), logu(rng, 1, 8), logu(rng, 1, 300), logu(rng, 1, 300)
+        while B * H * Rq * S > 4e6:
+            B = max(1, B // 2)
+            if B == 1:
+                Rq = max(1, Rq // 2)
+        dk = int(rng.choice([4, 8, 16, 32, 64, 128])) if rng.random() < 0.7 else logu(rng, 1, 128)
+        dv = dk if rng.random() < 0.6 else logu(rng, 1, 128)
+        causal, strided = int(rng.random() < 0.5), bool(rng.random() < 0.4)
+        use_vt = strided and rng.random() < 0.5
+        name = f"case {case}: B {B} H {H} Rq {Rq} S {S} dk {dk} dv {dv} causal {causal} strided {strided} vt {use_vt}"
+        print(name, flush=True)
+        Q = rng.standard_normal((B * Rq, H * dk)).astype(F32)
+        K = rng.standard_normal((B * S, H * dk)).astype(F32)
+        V = rng.standard_normal((B * S, H * dv)).astype(F32)
+        scale = F32(1.0) / np.sqrt(F32(dk))
+        want = np.zeros((B * Rq, H * dv), F32)
+        knx_ref.lib().ko_attention_core(knx_ref._p(Q), knx_ref._p(K), knx_ref._p(V), knx_ref._p(want), B, H, Rq, S, dk,
+                                        dv, float(scale), causal)
+        d = Device()
+        ctx = torch.empty((B * Rq, H * dv), dtype=torch.float32, device="cuda")
+        sc = torch.empty((B * H * Rq, S), dtype=torch.float32, device="cuda")
+        if strided:
+            pq, pk, pv = (4 * int(rng.integers(0, 3)) for _ in range(3))  # row padding (16-byte steps)
+            Qp = np.zeros((B * Rq, H * dk + pq), F32)
+            Kp = np.zeros((B * S, H * dk + pk), F32)
+            Vp = np.zeros((B * S, H * dv + pv), F32)
+            Qp[:, :H * dk], Kp[:, :H * dk], Vp[:, :H * dv] = Q, K, V
+            dvt = torch.empty((H * dv, B * S), dtype=torch.float32, device="cuda") if use_vt else None
+            hipabi.check(L.knx_hip_attention_core_ex(ptr(d(Qp)), H * dk + pq, ptr(d(Kp)), H * dk + pk, ptr(d(Vp)),
+                                                     H * dv + pv, opt(dvt), ptr(ctx), ptr(sc), B, H, Rq, S, dk, dv,
+                                                     float(scale), causal, st))
+        else:
+            hipabi.check(L.knx_hip_attention_core(ptr(d(Q)), ptr(d(K)), ptr(d(V)), ptr(ctx), ptr(sc), B, H, Rq, S, dk,
+                                                  dv, float(scale), causal, st))
+        torch.cuda.synchronize()
+        got = ctx.cpu().numpy()
+        ok = np.isfinite(want)  # a causal query row with no key at or before it has an empty softmax
+        assert np.array_equal(np.isfinite(got), ok), name
+        assert rel_err(got[ok], want[ok]) <= 1e-4, name
