@@ -111,3 +111,74 @@ def inputs(b, batch, seed=0):
     if shape == (5,):  # token ids of the embedding model
         return rng.integers(0, 12, (batch,) + shape).astype(np.float32)
     return rng.standard_normal((batch,) + shape).astype(np.float32)
+
+
+def random_sequence_model(rng, int8=False):
+    """A random graph over one T × F sample (T 1-12, F 1-64): 3-9 ops drawn from Linear (with and without bias and
+    activation), activations, layer norm, softmax, a Linear whose output is added to its input (the residual add the
+    runtime fuses into the Linear), affine, constant add, self-attention (causal or not), recurrent layers (one or two
+    directions, every merge, sequences or the last state), concat and select; each op reads the latest value or an
+    earlier one.  Weights N(0, 1/in) so values stay of order one; layer norm eps ≥ 1e-3 (a near-constant row otherwise
+    turns last-bit differences of fp32 sums into large ones).  Returns (builder, output value)."""
+    T, F = int(rng.integers(1, 13)), int(rng.integers(1, 65))
+    b = ModelBuilder((T, F), int8=int8)
+    vals = [b.input]
+
+    def w(i, o):
+        return rng.normal(0.0, 1.0 / np.sqrt(i), (i, o))
+
+    def maybe_bias(n):
+        return rng.normal(0.0, 0.1, n) if rng.random() < 0.8 else None
+
+    acts = [None, "relu", "gelu", "tanh", "sigmoid", "silu", "leaky_relu", "elu"]
+    for _ in range(int(rng.integers(3, 10))):
+        x = vals[-1] if rng.random() < 0.6 else vals[int(rng.integers(0, len(vals)))]
+        seq, d = len(x.shape) == 2, x.shape[-1]
+        ops = ["linear", "act", "layer_norm", "softmax", "residual", "affine", "add_const", "concat"]
+        if seq:
+            ops += ["attention", "attention", "recurrent", "recurrent", "select"]
+        op = str(rng.choice(ops))
+        if op == "linear":
+            n = int(rng.integers(1, 97))
+            y = b.linear(x, w(d, n), maybe_bias(n), activation=acts[int(rng.integers(0, len(acts)))], alpha=0.1)
+        elif op == "act":
+            y = b.activation(x, str(rng.choice(acts[1:])), alpha=0.1)
+        elif op == "layer_norm":
+            affine = rng.random() < 0.7
+            y = b.layer_norm(x, rng.normal(1.0, 0.2, d) if affine else None, rng.normal(0.0, 0.2, d) if affine else None,
+                             eps=float(rng.choice([1e-3, 1e-2])))
+        elif op == "softmax":
+            y = b.softmax(x)
+        elif op == "residual":
+            h = b.linear(x, w(d, d), maybe_bias(d), activation=str(rng.choice(["relu", "gelu"])) if rng.random() < 0.4
+                         else None)
+            y = b.add(h, x) if rng.random() < 0.5 else b.add(x, h)
+        elif op == "affine":
+            y = b.affine(x, rng.normal(1.0, 0.2, d), rng.normal(0.0, 0.2, d))
+        elif op == "add_const":
+            y = b.add_const(x, rng.normal(0.0, 0.2, int(np.prod(x.shape))))
+        elif op == "concat":
+            peers = [v for v in vals if v.shape[:-1] == x.shape[:-1]]
+            y = b.concat([x, peers[int(rng.integers(0, len(peers)))]])
+        elif op == "attention":
+            heads, dk, dv, out = int(rng.integers(1, 5)), int(rng.integers(1, 33)), int(rng.integers(1, 33)), int(
+                rng.integers(1, 97))
+            bias = rng.random() < 0.5
+            bs = [rng.normal(0.0, 0.1, n) if bias else None for n in (heads * dk, heads * dk, heads * dv, out)]
+            y = b.attention(x, heads, w(d, heads * dk), w(d, heads * dk), w(d, heads * dv), w(heads * dv, out), *bs,
+                            causal=bool(rng.random() < 0.5))
+        elif op == "recurrent":
+            cell = str(rng.choice(["LSTM", "GRU", "RNN"]))
+            units, g = int(rng.integers(1, 65)), {"LSTM": 4, "GRU": 3, "RNN": 1}[cell]
+            dirs = [(w(d, g * units), w(units, g * units), rng.normal(0.0, 0.1, (2 if cell == "GRU" else 1) * g * units))
+                    for _ in range(int(rng.integers(1, 3)))]
+            y = b.recurrent(x, cell, units, dirs, return_sequences=bool(rng.random() < 0.5),
+                            merge=str(rng.choice(["concat", "sum", "mul", "ave"])))
+        else:  # select rows of the sequence
+            if x.shape[0] < 2:
+                continue
+            start = int(rng.integers(0, x.shape[0]))
+            length = int(rng.integers(1, x.shape[0] - start + 1))
+            y = b.select(x, "first", start, length, squeeze=length == 1 and bool(rng.random() < 0.5))
+        vals.append(y)
+    return b, vals[-1]

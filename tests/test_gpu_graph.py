@@ -62,6 +62,40 @@ def test_graph_int8_weights(tmp_path, family, mode):
         assert rel_err(y, want) <= tol, (family, mode, batch)
 
 
+@pytest.mark.parametrize("seed", [1, 2])
+def test_random_sequence_graphs(tmp_path, monkeypatch, seed):
+    """random graphs (graph_models.random_sequence_model), fp32 or int8 weights, ref or i8 mode, batch 1-40: the forward
+    with every fusion of the runtime (residual adds in the producer's epilogue, layer norm + quantize, Linear chains,
+    the one-launch recurrence and its fused Linear) against the same forward with all of them off (KNX_NO_FUSE=1,
+    KNX_CHAIN=0, KNX_RNN_PERSISTENT=0), and both against the oracle"""
+    from tests.graph_models import random_sequence_model
+
+    rng = np.random.default_rng(seed)
+    for case in range(15):
+        int8 = bool(rng.random() < 0.4)
+        mode = "i8" if int8 and rng.random() < 0.5 else "ref"
+        b, _ = random_sequence_model(rng, int8=int8)
+        p = str(tmp_path / f"g{seed}_{case}.knx")
+        b.save(p)
+        batch = int(np.exp(rng.uniform(0.0, np.log(41))))
+        x = rng.standard_normal((batch,) + b.input.shape).astype(np.float32)
+        name = (f"case {case}: ops {[n.kind for n in b._nodes]} input {b.input.shape} batch {batch} int8 {int8} "
+                f"mode {mode}")
+        print(name, flush=True)
+        for var in ("KNX_NO_FUSE", "KNX_CHAIN", "KNX_RNN_PERSISTENT"):
+            monkeypatch.delenv(var, raising=False)
+        y, want = run(p, x, mode)
+        monkeypatch.setenv("KNX_NO_FUSE", "1")
+        monkeypatch.setenv("KNX_CHAIN", "0")
+        monkeypatch.setenv("KNX_RNN_PERSISTENT", "0")
+        y_off, _ = run(p, x, mode)
+        tol = 1e-2 if int8 else 1e-4  # int8: fp32 ops feed the per-row quantizer (see the module docstring)
+        assert np.isfinite(want).all(), name
+        assert rel_err(y, y_off) <= tol and rel_err(y, want) <= tol and rel_err(y_off, want) <= tol, name
+    for var in ("KNX_NO_FUSE", "KNX_CHAIN", "KNX_RNN_PERSISTENT"):
+        monkeypatch.delenv(var, raising=False)
+
+
 @pytest.mark.parametrize("family", sorted(FAMILIES))
 def test_graph_chunked(tmp_path, family):
     """a workspace limit of a few samples: the forward runs in chunks and must give the unchunked result"""
