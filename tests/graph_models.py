@@ -182,3 +182,72 @@ def random_sequence_model(rng, int8=False):
             y = b.select(x, "first", start, length, squeeze=length == 1 and bool(rng.random() < 0.5))
         vals.append(y)
     return b, vals[-1]
+
+
+def _extent(n, k, stride, dil, pad_a, pad_b):
+    """output length of a window of k taps (dilation dil) over n padded positions"""
+    return (n + pad_a + pad_b - dil * (k - 1) - 1) // stride + 1
+
+
+def random_vision_model(rng, int8=False):
+    """A random graph over one H × W × C sample (H, W 1-20; C 1-16, 32 or 64): 3-8 ops drawn from convolutions (kernel
+    1-3, stride, dilation, padding, groups, activation), a convolution added to its input (the residual add fused into
+    the convolution), pooling (max / average, padding counted or not), padding, upsampling, concat on channels,
+    binary ops against the sample's pooled channel vector (row broadcast), affine and activations; then a global pool
+    and a Linear.  Returns (builder, output value)."""
+    H, W = int(rng.integers(1, 21)), int(rng.integers(1, 21))
+    C = int(rng.choice([1, 2, 3, 4, 8, 16, 32, 64]))
+    b = ModelBuilder((H, W, C), int8=int8)
+    vals = [b.input]
+
+    def conv_w(k, cin, cout, groups):
+        return rng.normal(0.0, 1.0 / np.sqrt(k * cin / groups), (k * cin // groups, cout))
+
+    acts = [None, "relu", "relu6", "gelu", "tanh", "silu"]
+    for _ in range(int(rng.integers(3, 9))):
+        x = vals[-1] if rng.random() < 0.6 else vals[int(rng.integers(0, len(vals)))]
+        h, w, c = x.shape
+        op = str(rng.choice(["conv", "conv", "conv", "residual", "pool", "pad", "upsample", "concat", "binary",
+                             "affine", "act"]))
+        if op in ("conv", "residual"):
+            kh, kw = (int(rng.integers(1, 4)), int(rng.integers(1, 4))) if op == "conv" else (3, 3)
+            groups = int(rng.choice([g for g in (1, 1, 1, 2, 4, c) if c % g == 0]))
+            co = c if op == "residual" or groups == c else groups * int(rng.choice([1, 2, 4, 8, 16, 32]))
+            if op == "residual":
+                y = b.conv(x, conv_w(9, c, co, groups), rng.normal(0.0, 0.1, co), kernel=(3, 3), padding=(1, 1, 1, 1),
+                           groups=groups, activation="relu" if rng.random() < 0.5 else None)
+                y = b.add(y, x) if rng.random() < 0.5 else b.add(x, y)
+            else:
+                sh, sw = int(rng.integers(1, 3)), int(rng.integers(1, 3))
+                dh, dw = int(rng.integers(1, 3)), int(rng.integers(1, 3))
+                pad = tuple(int(rng.integers(0, k)) for k in (kh, kh, kw, kw))
+                if _extent(h, kh, sh, dh, pad[0], pad[1]) < 1 or _extent(w, kw, sw, dw, pad[2], pad[3]) < 1:
+                    continue
+                y = b.conv(x, conv_w(kh * kw, c, co, groups), rng.normal(0.0, 0.1, co) if rng.random() < 0.8 else None,
+                           kernel=(kh, kw), stride=(sh, sw), dilation=(dh, dw), padding=pad, groups=groups,
+                           activation=acts[int(rng.integers(0, len(acts)))])
+        elif op == "pool":
+            k, s = int(rng.integers(1, 4)), int(rng.integers(1, 3))
+            pad = tuple(int(rng.integers(0, k)) for _ in range(4))
+            if _extent(h, k, s, 1, pad[0], pad[1]) < 1 or _extent(w, k, s, 1, pad[2], pad[3]) < 1:
+                continue
+            y = b.pool(x, str(rng.choice(["max", "avg"])), (k, k), (s, s), pad, count_pad=bool(rng.random() < 0.5))
+        elif op == "pad":
+            y = b.pad(x, tuple(int(rng.integers(0, 3)) for _ in range(4)))
+        elif op == "upsample":
+            if h * w > 200:
+                continue
+            y = b.upsample(x, (int(rng.integers(1, 3)), int(rng.integers(1, 3))))
+        elif op == "concat":
+            peers = [v for v in vals if v.shape[:-1] == x.shape[:-1]]
+            y = b.concat([x, peers[int(rng.integers(0, len(peers)))]])
+        elif op == "binary":
+            y = b.binary(x, b.global_pool(x, str(rng.choice(["avg", "max"]))), str(rng.choice(["add", "sub", "mul", "max"])))
+        elif op == "affine":
+            y = b.affine(x, rng.normal(1.0, 0.2, c), rng.normal(0.0, 0.2, c))
+        else:
+            y = b.activation(x, str(rng.choice(acts[1:])))
+        vals.append(y)
+    g = b.global_pool(vals[-1], str(rng.choice(["avg", "max"])))
+    n = int(rng.integers(1, 17))
+    return b, b.linear(g, rng.normal(0.0, 1.0 / np.sqrt(g.shape[-1]), (g.shape[-1], n)), rng.normal(0.0, 0.1, n))

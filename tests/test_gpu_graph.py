@@ -62,20 +62,22 @@ def test_graph_int8_weights(tmp_path, family, mode):
         assert rel_err(y, want) <= tol, (family, mode, batch)
 
 
+@pytest.mark.parametrize("kind", ["sequence", "vision"])
 @pytest.mark.parametrize("seed", [1, 2])
-def test_random_sequence_graphs(tmp_path, monkeypatch, seed):
-    """random graphs (graph_models.random_sequence_model), fp32 or int8 weights, ref or i8 mode, batch 1-40: the forward
-    with every fusion of the runtime (residual adds in the producer's epilogue, layer norm + quantize, Linear chains,
-    the one-launch recurrence and its fused Linear) against the same forward with all of them off (KNX_NO_FUSE=1,
-    KNX_CHAIN=0, KNX_RNN_PERSISTENT=0), and both against the oracle"""
-    from tests.graph_models import random_sequence_model
+def test_random_graphs(tmp_path, monkeypatch, kind, seed):
+    """random graphs (graph_models.random_sequence_model / random_vision_model), fp32 or int8 weights, ref or i8 mode,
+    batch 1-40: the forward with every fusion of the runtime (residual adds in the producer's epilogue, layer norm +
+    quantize, Linear chains, the one-launch recurrence and its fused Linear) against the same forward with all of them
+    off (KNX_NO_FUSE=1, KNX_CHAIN=0, KNX_RNN_PERSISTENT=0), and both against the oracle"""
+    from tests.graph_models import random_sequence_model, random_vision_model
 
+    make_graph = random_sequence_model if kind == "sequence" else random_vision_model
     rng = np.random.default_rng(seed)
     for case in range(15):
         int8 = bool(rng.random() < 0.4)
         mode = "i8" if int8 and rng.random() < 0.5 else "ref"
-        b, _ = random_sequence_model(rng, int8=int8)
-        p = str(tmp_path / f"g{seed}_{case}.knx")
+        b, _ = make_graph(rng, int8=int8)
+        p = str(tmp_path / f"{kind}{seed}_{case}.knx")
         b.save(p)
         batch = int(np.exp(rng.uniform(0.0, np.log(41))))
         x = rng.standard_normal((batch,) + b.input.shape).astype(np.float32)
