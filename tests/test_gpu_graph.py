@@ -68,7 +68,8 @@ def test_random_graphs(tmp_path, monkeypatch, kind, seed):
     """random graphs (graph_models.random_sequence_model / random_vision_model), fp32 or int8 weights, ref or i8 mode,
     batch 1-40: the forward with every fusion of the runtime (residual adds in the producer's epilogue, layer norm +
     quantize, Linear chains, the one-launch recurrence and its fused Linear) against the same forward with all of them
-    off (KNX_NO_FUSE=1, KNX_CHAIN=0, KNX_RNN_PERSISTENT=0), and both against the oracle"""
+    off (KNX_NO_FUSE=1, KNX_CHAIN=0, KNX_RNN_PERSISTENT=0) and against the oracle, also run in pieces of a few samples
+    under a small workspace limit"""
     from tests.graph_models import random_sequence_model, random_vision_model
 
     make_graph = random_sequence_model if kind == "sequence" else random_vision_model
@@ -91,9 +92,13 @@ def test_random_graphs(tmp_path, monkeypatch, kind, seed):
         monkeypatch.setenv("KNX_CHAIN", "0")
         monkeypatch.setenv("KNX_RNN_PERSISTENT", "0")
         y_off, _ = run(p, x, mode)
+        for var in ("KNX_NO_FUSE", "KNX_CHAIN", "KNX_RNN_PERSISTENT"):
+            monkeypatch.delenv(var, raising=False)
+        y_chunk, _ = run(p, x, mode, workspace_mb=0.02)  # pieces of a few samples (fusions on)
         tol = 1e-2 if int8 else 1e-4  # int8: fp32 ops feed the per-row quantizer (see the module docstring)
         assert np.isfinite(want).all(), name
         assert rel_err(y, y_off) <= tol and rel_err(y, want) <= tol and rel_err(y_off, want) <= tol, name
+        assert rel_err(y_chunk, want) <= tol, name
     for var in ("KNX_NO_FUSE", "KNX_CHAIN", "KNX_RNN_PERSISTENT"):
         monkeypatch.delenv(var, raising=False)
 
