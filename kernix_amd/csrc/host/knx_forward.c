@@ -459,6 +459,7 @@ void knx_model_release_device_all(kernix_model* m)
             knx_hip_event_destroy(m->dev->ring_ev[k]);
             knx_hip_host_free(m->dev->ring[k]);
         }
+        knx_hip_host_free(m->dev->stage); /* release_ws has synchronized the model's stream */
         knx_hip_host_free(m->dev->chain_status);
         free(m->dev);
         m->dev = NULL;
@@ -1292,6 +1293,35 @@ static int copy_in(kernix_model* m, float* dst, const float* src, size_t bytes, 
     return 0;
 }
 
+/* A piece of at most KNX_STAGE_MAX bytes without overlap: the host copies it into the model's pinned staging buffer
+ * and a copy kernel on the model's stream reads it from there (pinned host memory is mapped into the device's address
+ * space).  The runtime's pageable copy would stage the bytes through its own buffer and hand the transfer to the copy
+ * engine, whose completion the first kernel then waits for (larger inputs keep the copy engine, which moves bulk data
+ * faster than a kernel reading over PCIe).  A host forward ends with a synchronization of the model's stream, so the
+ * buffer is free when the next one starts; only a later piece of the same forward (or a forward that failed after
+ * the copy was enqueued) finds stage_pending set and waits for the stream first. */
+#define KNX_STAGE_MAX ((size_t)1 << 20)
+
+static int stage_in(kernix_model* m, float* dst, const float* src, size_t bytes, void* st)
+{
+    struct knx_dmodel* d = m->dev;
+    if (d->stage_pending && hip_ok(knx_hip_stream_sync(st), "staging wait")) return -1;
+    d->stage_pending = 0;
+    if (d->stage_bytes < bytes) {
+        knx_hip_host_free(d->stage);
+        d->stage = NULL;
+        d->stage_bytes = 0;
+        const size_t want = (bytes + 65535) / 65536 * 65536;
+        if (hip_ok(knx_hip_host_malloc(&d->stage, want), "pinned staging allocation")) return -1;
+        d->stage_bytes = want;
+    }
+    copy_parallel(d->stage, src, bytes);
+    const int n = (int)(bytes / sizeof(float));
+    if (hip_ok(knx_hip_copy_cols(d->stage, n, 0, dst, n, 0, 1, n, st), "input copy")) return -1;
+    d->stage_pending = 1;
+    return 0;
+}
+
 static int overlap_ready(kernix_model* m)
 {
     struct knx_dmodel* d = m->dev;
@@ -1361,14 +1391,17 @@ static const float_tensor* forward_host(kernix_model* m, const float_tensor* x)
     } else {
         for (int s0 = 0; s0 < samples; s0 += per) {
             const int n = samples - s0 < per ? samples - s0 : per;
+            const float* src = x->tensor + (size_t)s0 * in_row;
+            const size_t bytes = (size_t)n * in_row * sizeof(float);
             /* the staged input holds one piece: piece s0 is copied to its start */
-            if (hip_ok(knx_hip_memcpy_h2d(m->dev->d_in, x->tensor + (size_t)s0 * in_row, (size_t)n * in_row * sizeof(float), st),
-                       "input copy") ||
+            if ((bytes <= KNX_STAGE_MAX ? stage_in(m, m->dev->d_in, src, bytes, st)
+                                         : hip_ok(knx_hip_memcpy_h2d(m->dev->d_in, src, bytes, st), "input copy")) ||
                 run_piece(m, m->dev->d_in, s0, n, out, 1, st) != 0)
                 return NULL;
         }
     }
     if (mark_done(m, st) != 0 || hip_ok(knx_hip_stream_sync(st), "forward")) return NULL;
+    m->dev->stage_pending = 0; /* every copy out of the staging buffer has completed */
     if (chunked) return m->out_all;
     m->out_view = (float_tensor){ samples, m->out_dim, out };
     return &m->out_view;

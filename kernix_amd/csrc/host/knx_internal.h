@@ -69,6 +69,10 @@ struct knx_dmodel {
     void* ring[KNX_RING_SLOTS];
     void* ring_ev[KNX_RING_SLOTS];   /* the copy out of slot k has completed after this event */
     int ring_next;
+    /* pinned staging of a small host input, read by a copy kernel (grown on use to the largest piece, ≤ 1 MB) */
+    void* stage;
+    size_t stage_bytes;
+    int stage_pending;  /* a copy kernel reading `stage` may not have completed (no stream synchronization since) */
 };
 
 /* A decoded .knx file: its header and op records in file order (inputs, arguments, host weights). */
