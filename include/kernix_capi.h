@@ -31,6 +31,8 @@ KERNIX_API void kernix_capi_shapes(const kernix_model* m, int* in_nd, int* in_sh
 KERNIX_API int kernix_capi_set_int8_mode(kernix_model* m, int mode);  /* KERNIX_INT8_REF / KERNIX_INT8_I8; 0 or -1 */
 /* Forward on device buffers (rows × in_dim → (rows/seq_len) × out_dim), stream = hipStream_t or NULL; enqueues only. */
 KERNIX_API int kernix_capi_forward_device(kernix_model* m, const float* d_x, int rows, float* d_out, void* stream);
+/* kernix_capi_forward with each sample of x channels-first (kernix_model_forward_cf): the transpose runs on the GPU. */
+KERNIX_API int kernix_capi_forward_cf(kernix_model* m, const float* x, int rows, float* out);
 /* Waits for the last forward; -1 if a device forward since the previous call must be run again (kernix_model.h). */
 KERNIX_API int kernix_capi_device_status(kernix_model* m);
 /* Workspace accounting: floats per sample, batch-independent floats, rows of the current workspace (-1 = none). */

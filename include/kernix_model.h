@@ -183,6 +183,11 @@ KERNIX_API int kernix_model_set_int8_mode(kernix_model* m, int mode);
  * both device pointers; stream is a hipStream_t (NULL = the model's own stream). Work is stream-ordered; the call
  * returns after enqueueing (it synchronizes only when it has to allocate). 0 or -1. */
 KERNIX_API int kernix_model_forward_device(kernix_model* m, const float* d_x, int rows, float* d_out, void* stream);
+/* kernix_model_forward with each sample of x in channels-first order (C × the spatial positions, the PyTorch layout)
+ * for a model whose file records layout 1: the input is copied as it is and transposed on the device, where the
+ * reference's binding moves the axis on the host first.  Same rows, output and errors as kernix_model_forward; for a
+ * layout-0 model, or one row per sample, it is kernix_model_forward. */
+KERNIX_API const float_tensor* kernix_model_forward_cf(kernix_model* m, const float_tensor* x);
 /* Waits for the model's last forward and reports the device forwards since the previous call: -1 if one of them ran a
  * Linear chain whose workgroups could not all be resident (more chains running at once than the GPU holds), so its
  * outputs are wrong and it must be run again; else 0.  Host-buffer forwards recompute such a forward themselves. */

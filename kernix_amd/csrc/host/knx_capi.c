@@ -38,6 +38,17 @@ KERNIX_API int kernix_capi_forward(kernix_model* m, const float* x, int rows, fl
     return 0;
 }
 
+/* kernix_capi_forward on channels-first samples (an extension: the axis moved on the device) */
+KERNIX_API int kernix_capi_forward_cf(kernix_model* m, const float* x, int rows, float* out)
+{
+    if (m == NULL || x == NULL || out == NULL || rows <= 0) return -1;
+    const float_tensor in = { rows, m->in_dim, (float*)x };
+    const float_tensor* y = kernix_model_forward_cf(m, &in);
+    if (y == NULL) return -1;
+    memcpy(out, y->tensor, sizeof(float) * (size_t)y->row * (size_t)y->col);
+    return 0;
+}
+
 /* reference src/kernix_capi.c:35: the Neural Engine assist does not exist here: -1 ("unavailable") */
 KERNIX_API int kernix_capi_set_ane(kernix_model* m, int on) { return kernix_model_set_ane(m, on); }
 

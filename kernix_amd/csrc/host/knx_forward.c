@@ -434,6 +434,9 @@ static void release_ws(kernix_model* m)
         knx_hip_host_free(m->dev->h_out);
         m->dev->h_out = NULL;
         m->dev->h_out_floats = 0;
+        knx_hip_free(m->dev->cf_in);
+        m->dev->cf_in = NULL;
+        m->dev->cf_in_floats = 0;
     }
     free_out_all(m);
     free_views(m);
@@ -1367,7 +1370,17 @@ static int forward_overlapped(kernix_model* m, const float* x, int samples, int 
     return 0;
 }
 
-static const float_tensor* forward_host(kernix_model* m, const float_tensor* x)
+/* A piece of n samples at src (device memory) in channels-first order (per sample C × S: C = in_dim, S = seq_len),
+ * transposed into the staged input's channels-last rows (S × C), the order the steps read. */
+static int transpose_in(kernix_model* m, const float* src, int n, void* st)
+{
+    const int d[2] = { m->in_dim, m->seq_len }, perm[2] = { 1, 0 };
+    return hip_ok(knx_hip_permute(src, m->dev->d_in, n, 2, d, perm, st), "input transpose");
+}
+
+/* cf: the input holds each sample channels-first (the PyTorch layout of a model whose file records layout 1); it is
+ * copied as it is and transposed on the device, instead of by the caller on the host. */
+static const float_tensor* forward_host(kernix_model* m, const float_tensor* x, int cf)
 {
     if (m == NULL || x == NULL || x->tensor == NULL || x->row < 0 || x->col != m->in_dim || x->row % m->seq_len != 0)
         return NULL;
@@ -1385,7 +1398,16 @@ static const float_tensor* forward_host(kernix_model* m, const float_tensor* x)
     float* out = host_output(m, samples, chunked);
     if (out == NULL || order_after_previous(m, st) != 0) return NULL;
     const size_t in_row = (size_t)m->seq_len * (size_t)m->in_dim;
-    const int pp = overlap_piece(m, samples, per);
+    cf = cf && m->seq_len > 1; /* one row per sample: both orders are the same */
+    if (cf && m->dev->cf_in_floats < (size_t)per * in_row) {
+        knx_hip_free(m->dev->cf_in);
+        m->dev->cf_in = NULL;
+        m->dev->cf_in_floats = 0;
+        if (hip_ok(knx_hip_malloc((void**)&m->dev->cf_in, (size_t)per * in_row * sizeof(float)), "input allocation"))
+            return NULL;
+        m->dev->cf_in_floats = (size_t)per * in_row;
+    }
+    const int pp = cf ? 0 : overlap_piece(m, samples, per);
     if (pp > 0) {
         if (forward_overlapped(m, x->tensor, samples, pp, out, st) != 0) return NULL;
     } else {
@@ -1393,10 +1415,11 @@ static const float_tensor* forward_host(kernix_model* m, const float_tensor* x)
             const int n = samples - s0 < per ? samples - s0 : per;
             const float* src = x->tensor + (size_t)s0 * in_row;
             const size_t bytes = (size_t)n * in_row * sizeof(float);
-            /* the staged input holds one piece: piece s0 is copied to its start */
-            if ((bytes <= KNX_STAGE_MAX ? stage_in(m, m->dev->d_in, src, bytes, st)
-                                         : hip_ok(knx_hip_memcpy_h2d(m->dev->d_in, src, bytes, st), "input copy")) ||
-                run_piece(m, m->dev->d_in, s0, n, out, 1, st) != 0)
+            float* to = cf ? m->dev->cf_in : m->dev->d_in;
+            /* the staged input holds one piece: piece s0 is copied to its start (channels-first: transposed there) */
+            if ((bytes <= KNX_STAGE_MAX ? stage_in(m, to, src, bytes, st)
+                                         : hip_ok(knx_hip_memcpy_h2d(to, src, bytes, st), "input copy")) ||
+                (cf && transpose_in(m, to, n, st) != 0) || run_piece(m, m->dev->d_in, s0, n, out, 1, st) != 0)
                 return NULL;
         }
     }
@@ -1409,20 +1432,30 @@ static const float_tensor* forward_host(kernix_model* m, const float_tensor* x)
 
 /* A chain launch whose workgroups could not all be resident (its barrier stopped waiting, so its outputs are wrong)
  * is recomputed in the same call: the whole forward again, every Linear its own launch. */
-const float_tensor* kernix_model_forward(kernix_model* m, const float_tensor* x)
+static const float_tensor* forward_host_checked(kernix_model* m, const float_tensor* x, int cf)
 {
     int prev;
     if (enter_device(m, &prev) != 0) return NULL;
-    const float_tensor* y = forward_host(m, x);
+    const float_tensor* y = forward_host(m, x, cf);
     if (y != NULL && __atomic_exchange_n(m->dev->chain_status, 0, __ATOMIC_SEQ_CST)) {
         KNX_LOG("KERNIX: a Linear chain's workgroups were not all resident; forward recomputed one launch per layer\n");
         m->dev->no_chain = 1;
-        y = forward_host(m, x);
+        y = forward_host(m, x, cf);
         m->dev->no_chain = 0;
         if (y != NULL && __atomic_exchange_n(m->dev->chain_status, 0, __ATOMIC_SEQ_CST)) y = NULL; /* cannot happen */
     }
     leave_device(prev);
     return y;
+}
+
+const float_tensor* kernix_model_forward(kernix_model* m, const float_tensor* x)
+{
+    return forward_host_checked(m, x, 0);
+}
+
+const float_tensor* kernix_model_forward_cf(kernix_model* m, const float_tensor* x)
+{
+    return forward_host_checked(m, x, m != NULL && m->layout == 1);
 }
 
 static int forward_device(kernix_model* m, const float* d_x, int rows, float* d_out, void* stream);

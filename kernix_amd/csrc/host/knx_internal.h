@@ -73,6 +73,10 @@ struct knx_dmodel {
     void* stage;
     size_t stage_bytes;
     int stage_pending;  /* a copy kernel reading `stage` may not have completed (no stream synchronization since) */
+    /* a channels-first host input piece on the device, before its per-sample transpose into d_in (grown on use,
+     * released with the workspace) */
+    float* cf_in;
+    size_t cf_in_floats;
 };
 
 /* A decoded .knx file: its header and op records in file order (inputs, arguments, host weights). */

@@ -46,6 +46,7 @@ _ABI = {
     # extensions of this build
     "kernix_capi_set_int8_mode": ((_VOID, _INT), _INT),
     "kernix_capi_forward_device": ((_VOID, _VOID, _INT, _VOID, _VOID), _INT),
+    "kernix_capi_forward_cf": ((_VOID, _VOID, _INT, _VOID), _INT),
     "kernix_capi_device_status": ((_VOID,), _INT),
     "kernix_capi_ws_info": ((_VOID, _PSIZE, _PSIZE, _PINT), None),
 }
@@ -149,26 +150,27 @@ class Model:
 
     # ---- forward ----
     def _rows_of(self, x):
-        """x as contiguous float32 rows of in_dim (channels-last), and the row count"""
+        """x as contiguous float32 values, the row count (of in_dim values) and whether the samples are channels-first:
+        a batched input of a channels-first model keeps its layout (the library moves the axis on the device, the
+        reference binding's host-side move), anything else is channels-last rows"""
         x = np.asarray(x)
         batched = x.ndim >= 2 and tuple(x.shape[1:]) == self.in_shape
-        if batched:
-            if self.channels_first and x.ndim >= 3:
-                x = np.moveaxis(x, 1, -1)
-        elif not (x.ndim == 2 and x.shape[1] == self.in_dim):
+        cf = batched and self.channels_first and x.ndim >= 3
+        if not batched and not (x.ndim == 2 and x.shape[1] == self.in_dim):
             want = ", ".join(str(d) for d in self.in_shape)
             raise ValueError(f"input shape {x.shape}: expected (batch, {want}) or (rows, {self.in_dim})")
         x = np.ascontiguousarray(x, dtype=np.float32)
         rows = x.size // self.in_dim
         if rows == 0 or rows % self.seq_len != 0:
             raise ValueError(f"{rows} input rows: must be a positive multiple of seq_len {self.seq_len}")
-        return x, rows
+        return x, rows, cf
 
     def __call__(self, x):
-        x, rows = self._rows_of(x)
+        x, rows, cf = self._rows_of(x)
         y = np.empty((rows // self.seq_len,) + self._out_cl, dtype=np.float32)
+        forward = _lib.kernix_capi_forward_cf if cf else _lib.kernix_capi_forward
         with self._lock:
-            ok = _lib.kernix_capi_forward(self._h, x.ctypes.data, rows, y.ctypes.data) == 0
+            ok = forward(self._h, x.ctypes.data, rows, y.ctypes.data) == 0
         if not ok:
             raise RuntimeError("KERNIX forward failed (see stderr)")
         if self.channels_first and y.ndim >= 3:

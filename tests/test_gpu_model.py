@@ -173,6 +173,27 @@ def test_zero_rows_bad_input_and_own_output(tmp_path):
     m.close()
 
 
+@pytest.mark.parametrize("batch,workspace_mb", [(1, None), (64, None), (256, None), (64, 0.5)])
+def test_channels_first_input_moved_on_the_device(tmp_path, batch, workspace_mb):
+    """A channels-first model called with NCHW samples: the binding passes them as they are to kernix_capi_forward_cf,
+    which transposes them on the GPU (inputs of up to 1 MB through the pinned staging buffer, larger ones through the
+    copy engine, in workspace pieces when a limit splits the batch).  The result is the bits of kernix_capi_forward on
+    the channels-last rows that the binding used to make on the host."""
+    from kernix_amd import kernix as kx
+
+    p = str(tmp_path / "c.knx")
+    x = configs.cnn(p, batch=batch, hw=32 if batch > 1 else 16)
+    m = Model(p, workspace_mb=workspace_mb)
+    assert m.channels_first
+    y = m(x)
+    rows = np.ascontiguousarray(np.moveaxis(x, 1, -1), np.float32).reshape(-1, m.in_dim)
+    want = np.empty_like(y)
+    assert kx._lib.kernix_capi_forward(m._h, rows.ctypes.data, rows.shape[0], want.ctypes.data) == 0
+    assert np.array_equal(y, want)
+    assert np.array_equal(m(x), want)  # again, with the staging buffer and the device copy already allocated
+    m.close()
+
+
 def test_workspace_identical_across_batch_sizes(tmp_path):
     """batch 37 after 4096 after 1 gives the same result (buffer reallocation, reference test/model_test.c:148)"""
     p = str(tmp_path / "f.knx")
