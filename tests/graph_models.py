@@ -194,10 +194,10 @@ def random_vision_model(rng, int8=False):
     1-3, stride, dilation, padding, groups, activation), a convolution added to its input (the residual add fused into
     the convolution), pooling (max / average, padding counted or not), padding, upsampling, concat on channels,
     binary ops against the sample's pooled channel vector (row broadcast), affine and activations; then a global pool
-    and a Linear.  Returns (builder, output value)."""
+    and a Linear.  Half of the models take channels-first input.  Returns (builder, output value)."""
     H, W = int(rng.integers(1, 21)), int(rng.integers(1, 21))
     C = int(rng.choice([1, 2, 3, 4, 8, 16, 32, 64]))
-    b = ModelBuilder((H, W, C), int8=int8)
+    b = ModelBuilder((H, W, C), channels_first=bool(rng.random() < 0.5), int8=int8)
     vals = [b.input]
 
     def conv_w(k, cin, cout, groups):

@@ -34,10 +34,11 @@ def run(path, x, mode="ref", workspace_mb=None):
         if mode == "i8":
             m.set_int8_mode(INT8_I8)
         y = m(x).reshape(len(x), -1)
-        in_dim = m.in_dim
+        in_dim, cf = m.in_dim, m.channels_first and np.ndim(x) >= 3
     finally:
         m.close()
-    want, _ = knx_ref.forward(knx_ref.parse(path), np.ascontiguousarray(x).reshape(-1, in_dim), mode=mode)
+    rows = np.moveaxis(np.asarray(x), 1, -1) if cf else x  # the oracle reads channels-last rows
+    want, _ = knx_ref.forward(knx_ref.parse(path), np.ascontiguousarray(rows).reshape(-1, in_dim), mode=mode)
     return y, want
 
 
@@ -81,9 +82,10 @@ def test_random_graphs(tmp_path, monkeypatch, kind, seed):
         p = str(tmp_path / f"{kind}{seed}_{case}.knx")
         b.save(p)
         batch = int(np.exp(rng.uniform(0.0, np.log(41))))
-        x = rng.standard_normal((batch,) + b.input.shape).astype(np.float32)
-        name = (f"case {case}: ops {[n.kind for n in b._nodes]} input {b.input.shape} batch {batch} int8 {int8} "
-                f"mode {mode}")
+        shape = (b.input.shape[-1],) + b.input.shape[:-1] if b.channels_first else b.input.shape  # what the caller gives
+        x = rng.standard_normal((batch,) + shape).astype(np.float32)
+        name = (f"case {case}: ops {[n.kind for n in b._nodes]} input {shape} channels-first {b.channels_first} "
+                f"batch {batch} int8 {int8} mode {mode}")
         print(name, flush=True)
         for var in ("KNX_NO_FUSE", "KNX_CHAIN", "KNX_RNN_PERSISTENT"):
             monkeypatch.delenv(var, raising=False)
