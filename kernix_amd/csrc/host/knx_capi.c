@@ -34,7 +34,7 @@ KERNIX_API int kernix_capi_forward(kernix_model* m, const float* x, int rows, fl
     const float_tensor in = { rows, m->in_dim, (float*)x }; /* forward does not modify its input */
     const float_tensor* y = kernix_model_forward(m, &in);
     if (y == NULL) return -1;
-    memcpy(out, y->tensor, sizeof(float) * (size_t)y->row * (size_t)y->col);
+    knx_copy_parallel(out, y->tensor, sizeof(float) * (size_t)y->row * (size_t)y->col);
     return 0;
 }
 
@@ -45,7 +45,7 @@ KERNIX_API int kernix_capi_forward_cf(kernix_model* m, const float* x, int rows,
     const float_tensor in = { rows, m->in_dim, (float*)x };
     const float_tensor* y = kernix_model_forward_cf(m, &in);
     if (y == NULL) return -1;
-    memcpy(out, y->tensor, sizeof(float) * (size_t)y->row * (size_t)y->col);
+    knx_copy_parallel(out, y->tensor, sizeof(float) * (size_t)y->row * (size_t)y->col);
     return 0;
 }
 

@@ -1239,8 +1239,9 @@ static void copy_pool_start(void)
     g_copy.ok = n == KNX_COPY_HELPERS;
 }
 
-/* memcpy of n bytes split over the caller and the helpers (a plain memcpy if the pool could not start) */
-static void copy_parallel(void* dst, const void* src, size_t n)
+/* memcpy of n bytes split over the caller and the helpers (a plain memcpy if the pool could not start, or for fewer
+ * than 256 KB); also the C ABI's copy of a forward's output into the caller's buffer */
+void knx_copy_parallel(void* dst, const void* src, size_t n)
 {
     pthread_once(&g_copy.once, copy_pool_start);
     if (!g_copy.ok || n < ((size_t)256 << 10)) {
@@ -1288,7 +1289,7 @@ static int copy_in(kernix_model* m, float* dst, const float* src, size_t bytes, 
         const int k = d->ring_next;
         d->ring_next = (k + 1) % KNX_RING_SLOTS;
         if (hip_ok(knx_hip_event_sync(d->ring_ev[k]), "staging wait")) return -1; /* slot k's previous DMA is done */
-        copy_parallel(d->ring[k], (const char*)src + off, n);
+        knx_copy_parallel(d->ring[k], (const char*)src + off, n);
         if (hip_ok(knx_hip_memcpy_h2d((char*)dst + off, d->ring[k], n, st), "input copy") ||
             hip_ok(knx_hip_event_record(d->ring_ev[k], st), "event record"))
             return -1;
@@ -1318,7 +1319,7 @@ static int stage_in(kernix_model* m, float* dst, const float* src, size_t bytes,
         if (hip_ok(knx_hip_host_malloc(&d->stage, want), "pinned staging allocation")) return -1;
         d->stage_bytes = want;
     }
-    copy_parallel(d->stage, src, bytes);
+    knx_copy_parallel(d->stage, src, bytes);
     const int n = (int)(bytes / sizeof(float));
     if (hip_ok(knx_hip_copy_cols(d->stage, n, 0, dst, n, 0, 1, n, st), "input copy")) return -1;
     d->stage_pending = 1;

@@ -103,6 +103,8 @@ int knx_model_count_ws(kernix_model* m, size_t* per_sample); /* floats per sampl
 /* workspace / device (knx_forward.c) */
 void knx_model_release_device_ws(kernix_model* m);
 void knx_model_release_device_all(kernix_model* m);
+/* memcpy of n bytes on the calling thread and a process-wide pool of copying threads (plain below 256 KB) */
+void knx_copy_parallel(void* dst, const void* src, size_t n);
 
 /* messages */
 #define KNX_LOG(...) fprintf(stderr, __VA_ARGS__)
