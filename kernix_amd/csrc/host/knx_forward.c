@@ -1179,8 +1179,9 @@ static float* host_output(kernix_model* m, int samples, int chunked)
  * These copies go through the model's own ring of four pinned 4 MB buffers instead: the host copies chunk j + 1
  * (split over four threads) into the next slot while the DMA of chunk j runs; a slot is reused once the event
  * recorded after its DMA has completed.  fp32 MLP 8192 × 4096 forward from host buffers: 11.2 ms without overlap,
- * 8.2 ms overlapped with one copying thread, 7.4 ms with four.  Smaller inputs keep the runtime's copy (a 3 MB
- * input took 0.9 ms longer through the ring, the copying threads being woken for a single chunk). */
+ * 8.2 ms overlapped with one copying thread, 7.4 ms with four.  Inputs from 1 MB to 32 MB keep the runtime's copy
+ * (through the ring they were 0-3% faster, not worth 16 MB of pinned memory per model); smaller ones go through the
+ * staging buffer (stage_in). */
 #define KNX_RING_BYTES ((size_t)4 << 20)
 #define KNX_OVERLAP_MIN_BYTES ((size_t)32 << 20)
 
