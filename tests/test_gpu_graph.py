@@ -100,7 +100,10 @@ def test_random_graphs(tmp_path, monkeypatch, kind, seed):
         tol = 1e-2 if int8 else 1e-4  # int8: fp32 ops feed the per-row quantizer (see the module docstring)
         assert np.isfinite(want).all(), name
         assert rel_err(y, y_off) <= tol and rel_err(y, want) <= tol and rel_err(y_off, want) <= tol, name
-        assert rel_err(y_chunk, want) <= tol, name
+        # ref mode dispatches int8 weights by rows (the reference's): pieces of one or two samples run them on int8
+        # arithmetic where the whole batch runs their fp32 copies, so the int8-vs-fp32 bound holds there
+        # (reference test/zoo_torch_test.py:207-208)
+        assert rel_err(y_chunk, want) <= (5e-2 if int8 and mode == "ref" else tol), name
     for var in ("KNX_NO_FUSE", "KNX_CHAIN", "KNX_RNN_PERSISTENT"):
         monkeypatch.delenv(var, raising=False)
 
